@@ -1,0 +1,242 @@
+// extern "C" entry points of libechokv.so (declared in include/echokv.h):
+// argument checks on the host, then asynchronous kernel launches on the
+// caller's stream. Nothing here allocates, synchronizes or touches device data.
+#include "args.h"
+
+namespace {
+
+bool lay_ok(const echokv_layout* L) {
+  if (!L) return false;
+  const int H = L->num_kv_heads, D = L->head_size, BS = L->block_size, KG = L->k_group, VG = L->v_group;
+  if (H <= 0 || D <= 0 || BS <= 0 || KG <= 0 || VG < 4 || L->chunks_per_page <= 0 || L->num_blocks <= 0) return false;
+  if (D % 4 || D % VG || BS % 16 || BS % KG || (VG & (VG - 1)) || VG > 256) return false;
+  if (L->page_stride % 16 || L->chunk_bytes != (int64_t)BS * H * D / 2) return false;
+  return true;
+}
+
+ek::Lay to_lay(const echokv_layout* L) {
+  ek::Lay d;
+  d.H = L->num_kv_heads;
+  d.D = L->head_size;
+  d.BS = L->block_size;
+  d.KG = L->k_group;
+  d.VG = L->v_group;
+  d.KC = L->chunks_per_page;
+  d.nb = L->num_blocks;
+  d.stride = L->page_stride;
+  d.o_vs = L->o_v_scale;
+  d.o_vm = L->o_v_min;
+  d.o_ks = L->o_k_scale;
+  d.o_km = L->o_k_min;
+  d.o_data = L->o_data;
+  d.cb = L->chunk_bytes;
+  return d;
+}
+
+bool dtype_ok(int dt) { return dt == ECHOKV_F32 || dt == ECHOKV_F16 || dt == ECHOKV_BF16; }
+
+bool res_ok(const echokv_residual* r) { return r && r->ptr && dtype_ok(r->dtype) && r->rows >= 1; }
+
+ek::Res to_res(const echokv_residual* r) {
+  ek::Res d;
+  d.ptr = r->ptr;
+  d.dtype = r->dtype;
+  d.rows = r->rows;
+  d.s0 = r->s0;
+  d.s1 = r->s1;
+  d.s2 = r->s2;
+  return d;
+}
+
+int launched(hipError_t e) { return e == hipSuccess ? ECHOKV_OK : ECHOKV_ELAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+const char* echokv_error_string(int code) {
+  switch (code) {
+    case ECHOKV_OK: return "ok";
+    case ECHOKV_EINVAL: return "invalid argument (null pointer, count or stride)";
+    case ECHOKV_ESHAPE: return "layout or head shape not supported by this build";
+    case ECHOKV_EDTYPE: return "unsupported dtype";
+    case ECHOKV_ELAUNCH: return "kernel launch failed";
+    default: return "unknown error";
+  }
+}
+
+int echokv_write_tokens(const echokv_layout* L, uint8_t* pages, const void* key, int64_t k_s0, int64_t k_s1,
+                        const void* value, int64_t v_s0, int64_t v_s1, int32_t kv_dtype, const int64_t* tok,
+                        int64_t tok_s0, int64_t n_rows, const echokv_residual* res, float* kref, int64_t kref_s0,
+                        int64_t kref_s1, echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (!dtype_ok(kv_dtype)) return ECHOKV_EDTYPE;
+  if (n_rows < 0 || tok_s0 < n_rows || !res_ok(res)) return ECHOKV_EINVAL;
+  if (n_rows == 0) return ECHOKV_OK;
+  if (!pages || !key || !value || !tok) return ECHOKV_EINVAL;
+  ek::WriteTokArgs a{to_lay(L), pages, key, k_s0, k_s1, value, v_s0, v_s1, kv_dtype, tok, tok_s0, to_res(res),
+                     kref, kref_s0, kref_s1};
+  return launched(ek::launch_write_tokens(a, n_rows, (hipStream_t)stream));
+}
+
+int echokv_finalize_k(const echokv_layout* L, uint8_t* pages, const void* key, int64_t k_s0, int64_t k_s1,
+                      int32_t kv_dtype, const int64_t* fin, const int64_t* fin_count, int64_t grid_rows,
+                      const echokv_residual* res, echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (!dtype_ok(kv_dtype)) return ECHOKV_EDTYPE;
+  if (grid_rows < 0 || !res_ok(res)) return ECHOKV_EINVAL;
+  if (grid_rows == 0) return ECHOKV_OK;
+  if (!pages || !key || !fin || !fin_count) return ECHOKV_EINVAL;
+  ek::FinArgs a{to_lay(L), pages, key, k_s0, k_s1, kv_dtype, fin, fin_count, to_res(res)};
+  return launched(ek::launch_finalize_k(a, grid_rows, (hipStream_t)stream));
+}
+
+int echokv_seal_groups(const echokv_layout* L, uint8_t* pages, const int64_t* ev, int64_t n,
+                       const echokv_residual* res, echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (n < 0 || !res_ok(res)) return ECHOKV_EINVAL;
+  if (n == 0) return ECHOKV_OK;
+  if (!pages || !ev) return ECHOKV_EINVAL;
+  ek::SealArgs a{to_lay(L), pages, ev, to_res(res)};
+  return launched(ek::launch_seal(a, n, (hipStream_t)stream));
+}
+
+int echokv_gather(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,
+                  const echokv_residual* res, const int64_t* blk, const int64_t* off, int64_t n, float* k_out,
+                  float* v_out, echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (n < 0 || !res_ok(res)) return ECHOKV_EINVAL;
+  if (n == 0) return ECHOKV_OK;
+  if (!pages || !block_res || !res_group || !blk || !off || !k_out || !v_out) return ECHOKV_EINVAL;
+  ek::GatherArgs a{to_lay(L), pages, block_res, res_group, to_res(res), blk, off, k_out, v_out};
+  return launched(ek::launch_gather(a, n, (hipStream_t)stream));
+}
+
+int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* blocks, int64_t n, const float* k,
+                        const float* v, int32_t bits, echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (n < 0 || (bits != 2 && bits != 4 && bits != 8)) return ECHOKV_EINVAL;
+  if (n == 0) return ECHOKV_OK;
+  if (!pages || !blocks || !k || !v) return ECHOKV_EINVAL;
+  ek::StoreBlkArgs a{to_lay(L), pages, blocks, k, v, bits};
+  return launched(ek::launch_store_blocks(a, n, (hipStream_t)stream));
+}
+
+int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,
+                  const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
+                  int32_t num_q_heads, const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
+                  const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs, float softmax_scale,
+                  int32_t num_splits, int32_t blocks_per_split, float* acc, float* ml, void* out, int64_t o_s0,
+                  int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (L->head_size != 64 && L->head_size != 128) return ECHOKV_ESHAPE;
+  if ((L->head_size / 16) % 1 || L->v_group % (L->head_size / 16)) return ECHOKV_ESHAPE;
+  if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
+  const int gqa = num_q_heads / L->num_kv_heads;
+  if (gqa > 16) return ECHOKV_ESHAPE;
+  if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
+  if (num_seqs < 0 || num_splits <= 0 || blocks_per_split <= 0 || !res_ok(res)) return ECHOKV_EINVAL;
+  if (num_seqs == 0) return ECHOKV_OK;
+  if (!pages || !block_res || !res_group || !query || !block_table || !seq_lens || !acc || !ml || !out)
+    return ECHOKV_EINVAL;
+  ek::DecodeArgs a;
+  a.L = to_lay(L);
+  a.pages = pages;
+  a.block_res = block_res;
+  a.res_group = res_group;
+  a.res = to_res(res);
+  a.q = query;
+  a.q_s0 = q_s0;
+  a.q_s1 = q_s1;
+  a.q_dtype = q_dtype;
+  a.hq = num_q_heads;
+  a.gqa = gqa;
+  a.q_rows = q_rows;
+  a.bt = block_table;
+  a.bt_s0 = bt_s0;
+  a.bt_rows = bt_rows;
+  a.lens = seq_lens;
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  a.num_splits = num_splits;
+  a.bps = blocks_per_split;
+  a.acc = acc;
+  a.ml = ml;
+  hipError_t e = ek::launch_decode(a, num_seqs, (hipStream_t)stream);
+  if (e != hipSuccess) return ECHOKV_ELAUNCH;
+  ek::MergeArgs m{acc, ml, seq_lens, q_rows, out, o_s0, o_s1, out_dtype, num_q_heads, L->head_size,
+                  L->block_size, num_splits, blocks_per_split};
+  return launched(ek::launch_merge(m, num_seqs, (hipStream_t)stream));
+}
+
+int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,
+                   const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
+                   int32_t num_q_heads, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                   const int32_t* tiles, int64_t n_tiles, int32_t tile_m, const int32_t* block_table, int64_t bt_s0,
+                   float softmax_scale, echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (L->head_size != 64 && L->head_size != 128) return ECHOKV_ESHAPE;
+  if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
+  const int gqa = num_q_heads / L->num_kv_heads;
+  if (gqa > ek::kPrefillRows || tile_m != ek::prefill_tile_tokens(gqa)) return ECHOKV_ESHAPE;
+  if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
+  if (n_tiles < 0 || !res_ok(res)) return ECHOKV_EINVAL;
+  if (n_tiles == 0) return ECHOKV_OK;
+  if (!pages || !block_res || !res_group || !query || !out || !tiles || !block_table) return ECHOKV_EINVAL;
+  ek::PrefillArgs a;
+  a.L = to_lay(L);
+  a.pages = pages;
+  a.block_res = block_res;
+  a.res_group = res_group;
+  a.res = to_res(res);
+  a.q = query;
+  a.q_s0 = q_s0;
+  a.q_s1 = q_s1;
+  a.q_dtype = q_dtype;
+  a.hq = num_q_heads;
+  a.gqa = gqa;
+  a.out = out;
+  a.o_s0 = o_s0;
+  a.o_s1 = o_s1;
+  a.out_dtype = out_dtype;
+  a.tiles = tiles;
+  a.bt = block_table;
+  a.bt_s0 = bt_s0;
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  return launched(ek::launch_prefill(a, n_tiles, (hipStream_t)stream));
+}
+
+int echokv_dequant_dense(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                         const int64_t* res_group, const echokv_residual* res, const int32_t* work, int64_t n_work,
+                         const int32_t* block_table, int64_t bt_s0, void* k_out, void* v_out, int64_t o_s0,
+                         int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (!dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
+  if (n_work < 0 || !res_ok(res)) return ECHOKV_EINVAL;
+  if (n_work == 0) return ECHOKV_OK;
+  if (!pages || !block_res || !res_group || !work || !block_table || !k_out || !v_out) return ECHOKV_EINVAL;
+  ek::DenseArgs a{to_lay(L), pages, block_res, res_group, to_res(res), work, block_table, bt_s0,
+                  k_out, v_out, o_s0, o_s1, out_dtype};
+  return launched(ek::launch_dequant_dense(a, n_work, (hipStream_t)stream));
+}
+
+int echokv_canary_kl(const void* query, int32_t q_dtype, int64_t q_sl, int64_t q_s0, int64_t q_s1, const float* kref,
+                     int64_t k_sl, int64_t k_s0, int64_t k_s1, int32_t num_layers, int32_t nq, int32_t num_q_heads,
+                     int32_t num_kv_heads, int32_t head_size, int32_t window, int32_t nbits, int32_t bits_packed,
+                     int32_t k_group, float softmax_scale, float* out, echokv_stream_t stream) {
+  if (!dtype_ok(q_dtype)) return ECHOKV_EDTYPE;
+  if (num_layers < 0 || nq < 1 || num_kv_heads < 1 || num_q_heads % num_kv_heads || k_group < 1) return ECHOKV_EINVAL;
+  if (head_size < 1 || head_size > ek::kCanaryMaxD || window < k_group || window > ek::kCanaryMaxKeys)
+    return ECHOKV_ESHAPE;
+  if (nbits < 1 || nbits > ek::kCanaryMaxTiers) return ECHOKV_EINVAL;
+  for (int t = 0; t < nbits; ++t) {
+    const int b = (bits_packed >> (8 * t)) & 0xff;
+    if (b != 2 && b != 4 && b != 8) return ECHOKV_EINVAL;
+  }
+  if (num_layers == 0) return ECHOKV_OK;
+  if (!query || !kref || !out) return ECHOKV_EINVAL;
+  ek::CanaryArgs a{query, q_dtype, q_sl, q_s0, q_s1, kref, k_sl, k_s0, k_s1, nq, num_q_heads, num_kv_heads,
+                   head_size, window, nbits, bits_packed, k_group, softmax_scale, out};
+  return launched(ek::launch_canary(a, num_layers, (hipStream_t)stream));
+}
+
+}  // extern "C"

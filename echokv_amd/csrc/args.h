@@ -1,0 +1,156 @@
+// Kernel argument structs (passed by value) and launchers of libechokv.
+#pragma once
+
+#include "common.h"
+
+namespace ek {
+
+constexpr int kThreads = 256;        // store / dequant kernels
+constexpr int kCanaryMaxKeys = 64;   // canary: keys staged in LDS per KV head
+constexpr int kCanaryMaxTiers = 3;
+constexpr int kCanaryMaxD = 128;
+constexpr int kPrefillRows = 128;    // prefill: query rows (tokens x GQA heads) per workgroup
+
+// Query tokens per prefill tile for a GQA group size.
+inline int prefill_tile_tokens(int gqa) { return kPrefillRows / gqa; }
+
+struct WriteTokArgs {
+  Lay L;
+  uint8_t* pages;
+  const void* key;
+  long k_s0, k_s1;
+  const void* value;
+  long v_s0, v_s1;
+  int kv_dtype;
+  const int64_t* tok;
+  long tok_s0;
+  Res res;
+  float* kref;
+  long kref_s0, kref_s1;
+};
+
+struct FinArgs {
+  Lay L;
+  uint8_t* pages;
+  const void* key;
+  long k_s0, k_s1;
+  int kv_dtype;
+  const int64_t* fin;
+  const int64_t* fin_count;
+  Res res;
+};
+
+struct SealArgs {
+  Lay L;
+  uint8_t* pages;
+  const int64_t* ev;
+  Res res;
+};
+
+struct StoreBlkArgs {
+  Lay L;
+  uint8_t* pages;
+  const int64_t* blocks;
+  const float* k;
+  const float* v;
+  int bits;
+};
+
+struct GatherArgs {
+  Lay L;
+  const uint8_t* pages;
+  const int64_t* block_res;
+  const int64_t* res_group;
+  Res res;
+  const int64_t* blk;
+  const int64_t* off;
+  float* k_out;
+  float* v_out;
+};
+
+struct DenseArgs {
+  Lay L;
+  const uint8_t* pages;
+  const int64_t* block_res;
+  const int64_t* res_group;
+  Res res;
+  const int32_t* work;
+  const int32_t* bt;
+  long bt_s0;
+  void* k_out;
+  void* v_out;
+  long o_s0, o_s1;
+  int out_dtype;
+};
+
+struct DecodeArgs {
+  Lay L;
+  const uint8_t* pages;
+  const int64_t* block_res;
+  const int64_t* res_group;
+  Res res;
+  const void* q;
+  long q_s0, q_s1;
+  int q_dtype, hq, gqa;
+  const int64_t* q_rows;
+  const int32_t* bt;
+  long bt_s0;
+  const int64_t* bt_rows;
+  const int64_t* lens;
+  float scale_log2;  // softmax scale * log2(e)
+  int num_splits, bps;
+  float* acc;  // [S, Hq, splits, D]
+  float* ml;   // [S, Hq, splits, 2] = (running max in log2 units, sum)
+};
+
+struct MergeArgs {
+  const float* acc;
+  const float* ml;
+  const int64_t* lens;
+  const int64_t* q_rows;
+  void* out;
+  long o_s0, o_s1;
+  int out_dtype, hq, D, BS, num_splits, bps;
+};
+
+struct CanaryArgs {
+  const void* q;
+  int q_dtype;
+  long q_sl, q_s0, q_s1;
+  const float* kref;
+  long k_sl, k_s0, k_s1;
+  int nq, hq, h, d, window, nbits, bits_packed, kg;
+  float scale;
+  float* out;
+};
+
+struct PrefillArgs {
+  Lay L;
+  const uint8_t* pages;
+  const int64_t* block_res;
+  const int64_t* res_group;
+  Res res;
+  const void* q;
+  long q_s0, q_s1;
+  int q_dtype, hq, gqa;
+  void* out;
+  long o_s0, o_s1;
+  int out_dtype;
+  const int32_t* tiles;  // [n, 5]: first query row, tokens, first query position, ctx, block-table row
+  const int32_t* bt;
+  long bt_s0;
+  float scale_log2;
+};
+
+hipError_t launch_write_tokens(const WriteTokArgs& a, long n_rows, hipStream_t s);
+hipError_t launch_finalize_k(const FinArgs& a, long rows, hipStream_t s);
+hipError_t launch_seal(const SealArgs& a, long n, hipStream_t s);
+hipError_t launch_store_blocks(const StoreBlkArgs& a, long n, hipStream_t s);
+hipError_t launch_gather(const GatherArgs& a, long n, hipStream_t s);
+hipError_t launch_dequant_dense(const DenseArgs& a, long n, hipStream_t s);
+hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s);
+hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s);
+hipError_t launch_canary(const CanaryArgs& a, int num_layers, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs& a, long n_tiles, hipStream_t s);
+
+}  // namespace ek

@@ -1,0 +1,367 @@
+// Write-side and dequantization kernels of the tiered page store (gfx950).
+//
+// One workgroup of 256 threads per token row / K group / block; a thread owns
+// four consecutive channels of one KV head, so a V group of VG channels is a
+// segment of VG/4 lanes reduced with cross-lane shuffles, and every thread
+// stores its four packed codes (1, 2 or 4 bytes) next to its neighbours'
+// (coalesced). Numerics follow echokv_vllm/quant.py bit for bit: float32
+// extremes, fp16-rounded stats, IEEE division, round half to even.
+#include "args.h"
+
+namespace ek {
+
+
+// ---------------------------------------------------------------------------
+// write_tokens (echokv_vllm/kernels/write.py:170-202, 280-338)
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) {
+  const Lay& L = a.L;
+  const long t = blockIdx.x;
+  const long slot = a.tok[t];
+  if (slot < 0) return;
+  const long blk = slot / L.BS;
+  const int off = (int)(slot % L.BS);
+  if (blk >= L.nb) return;
+  const int bits = tier_of(a.pages[blk * L.stride]);
+  const long rb = row_base(a.pages, L, blk, off, bits);
+  const long rslot = a.tok[a.tok_s0 + t];
+  const int64_t sealed = a.tok[2 * a.tok_s0 + t];
+  const long kidx = a.kref ? a.tok[3 * a.tok_s0 + t] : -1;
+  const int quads = L.D / 4;
+  const int items = L.H * quads;
+  const int G = L.D / L.VG;
+  const int side = L.H * L.D * bits / 8;
+  for (int base = 0; base < items; base += kThreads) {
+    const int i = base + (int)threadIdx.x;
+    const bool act = i < items;
+    const int h = act ? i / quads : 0, c = act ? i % quads : 0;
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+    if (act) ld4(a.value, a.kv_dtype, t * a.v_s0 + h * a.v_s1 + 4 * c, x);
+    float mn = fminf(fminf(x[0], x[1]), fminf(x[2], x[3]));
+    float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    seg_minmax(mn, mx, L.VG / 4);  // all lanes take part: segments never straddle `act`
+    if (!act || rb < 0) continue;
+    _Float16 s16, m16;
+    float s, m;
+    group_stats(mn, mx, bits, s16, m16, s, m);
+    const int g = (4 * c) / L.VG;
+    if ((4 * c) % L.VG == 0) {
+      const long e = ((long)off * L.H + h) * G + g;
+      *f16p(a.pages, blk * L.stride + L.o_vs + 2 * e) = s16;
+      *f16p(a.pages, blk * L.stride + L.o_vm + 2 * e) = m16;
+    }
+    uint32_t q[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = quant_code(x[e], m, s, bits);
+    store_codes4(a.pages + rb + side + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
+
+    // K: residual (open group), codes under the sealed stats, K_ref ring.
+    float k[4];
+    ld4(a.key, a.kv_dtype, t * a.k_s0 + h * a.k_s1 + 4 * c, k);
+    if (rslot >= 0 && rslot < a.res.rows) {
+      const long r0 = rslot * a.res.s0 + (long)(off % L.KG) * a.res.s1 + h * a.res.s2 + 4 * c;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st(a.res.ptr, a.res.dtype, r0 + e, k[e]);
+    }
+    if (sealed != 0) {
+      const long se = ((long)(off / L.KG) * L.H + h) * L.D + 4 * c;
+      uint32_t kq[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float ks = (float)*f16p(a.pages, blk * L.stride + L.o_ks + 2 * (se + e));
+        const float km = (float)*f16p(a.pages, blk * L.stride + L.o_km + 2 * (se + e));
+        kq[e] = quant_code(k[e], km, ks, bits);
+      }
+      store_codes4(a.pages + rb + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(kq, bits), bits);
+    }
+    if (kidx >= 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a.kref[kidx * a.kref_s0 + h * a.kref_s1 + 4 * c + e] = k[e];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K-group quantization shared by finalize_k, seal and store_blocks: the group's
+// n tokens of (head h, channels 4c..4c+3) come from `fetch(p, x)`; per-channel
+// stats over the n tokens, then codes for each token at offset off0 + p.
+// ---------------------------------------------------------------------------
+template <typename Fetch>
+__device__ void quantize_k_group(const Lay& L, uint8_t* pages, long blk, int grp, int off0, int n, int bits, int h,
+                                 int c, Fetch fetch) {
+  float mn[4], mx[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    mn[e] = __builtin_inff();
+    mx[e] = -__builtin_inff();
+  }
+  for (int p = 0; p < n; ++p) {
+    float x[4];
+    fetch(p, x);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      mn[e] = fminf(mn[e], x[e]);
+      mx[e] = fmaxf(mx[e], x[e]);
+    }
+  }
+  float s[4], m[4];
+  const long se = ((long)grp * L.H + h) * L.D + 4 * c;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    _Float16 s16, m16;
+    group_stats(mn[e], mx[e], bits, s16, m16, s[e], m[e]);
+    *f16p(pages, blk * L.stride + L.o_ks + 2 * (se + e)) = s16;
+    *f16p(pages, blk * L.stride + L.o_km + 2 * (se + e)) = m16;
+  }
+  for (int p = 0; p < n; ++p) {
+    const long rb = row_base(pages, L, blk, off0 + p, bits);
+    if (rb < 0) continue;
+    float x[4];
+    fetch(p, x);
+    uint32_t q[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = quant_code(x[e], m[e], s[e], bits);
+    store_codes4(pages + rb + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// finalize_k (echokv_vllm/kernels/write.py:205-230, 340-396)
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void finalize_k_kernel(FinArgs a) {
+  const Lay& L = a.L;
+  const long f = blockIdx.x;
+  if (f >= *a.fin_count) return;
+  const int64_t* row = a.fin + f * (3 + L.KG);
+  const long blk = row[0];
+  const int grp = (int)row[1];
+  const long rs = row[2] < 0 ? 0 : row[2];
+  if (blk < 0 || blk >= L.nb || grp < 0 || grp >= L.BS / L.KG || rs >= a.res.rows) return;
+  const int bits = tier_of(a.pages[blk * L.stride]);
+  const int quads = L.D / 4;
+  for (int i = threadIdx.x; i < L.H * quads; i += kThreads) {
+    const int h = i / quads, c = i % quads;
+    auto fetch = [&](int p, float x[4]) {
+      const long r = row[3 + p];
+      if (r >= 0) ld4(a.key, a.kv_dtype, r * a.k_s0 + h * a.k_s1 + 4 * c, x);
+      else ld4(a.res.ptr, a.res.dtype, rs * a.res.s0 + (long)p * a.res.s1 + h * a.res.s2 + 4 * c, x);
+    };
+    quantize_k_group(L, a.pages, blk, grp, grp * L.KG, L.KG, bits, h, c, fetch);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// seal (echokv_vllm/tiered_cache.py:379-394): ev rows (slot, block, group, fill, bits, mask)
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void seal_kernel(SealArgs a) {
+  const Lay& L = a.L;
+  const int64_t* e = a.ev + blockIdx.x * 6;
+  const long slot = e[0], blk = e[1];
+  const int grp = (int)e[2], fill = (int)e[3], bits = tier_of((uint32_t)e[4]);
+  if (fill <= 0 || slot < 0 || slot >= a.res.rows || blk < 0 || blk >= L.nb || grp < 0 || grp >= L.BS / L.KG)
+    return;
+  const int n = fill < L.KG ? fill : L.KG;
+  const int quads = L.D / 4;
+  for (int i = threadIdx.x; i < L.H * quads; i += kThreads) {
+    const int h = i / quads, c = i % quads;
+    auto fetch = [&](int p, float x[4]) {
+      ld4(a.res.ptr, a.res.dtype, slot * a.res.s0 + (long)p * a.res.s1 + h * a.res.s2 + 4 * c, x);
+    };
+    quantize_k_group(L, a.pages, blk, grp, grp * L.KG, n, bits, h, c, fetch);
+  }
+  if (threadIdx.x == 0) a.pages[blk * L.stride + 1] = (uint8_t)e[5];
+}
+
+// ---------------------------------------------------------------------------
+// store_blocks: whole-block requantization from float32 K/V (demotion,
+// echokv_vllm/tiered_cache.py:322-340). K per channel over each K group, V per
+// token; the tag byte becomes `bits`.
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void store_blocks_kernel(StoreBlkArgs a) {
+  const Lay& L = a.L;
+  const long b = blockIdx.x;
+  const long blk = a.blocks[b];
+  if (blk < 0 || blk >= L.nb) return;
+  const int bits = a.bits;
+  if (threadIdx.x == 0) a.pages[blk * L.stride] = (uint8_t)bits;
+  const int quads = L.D / 4;
+  const long rowsz = (long)L.H * L.D;
+  const float* kb = a.k + b * L.BS * rowsz;
+  const float* vb = a.v + b * L.BS * rowsz;
+  for (int grp = 0; grp < L.BS / L.KG; ++grp) {
+    for (int i = threadIdx.x; i < L.H * quads; i += kThreads) {
+      const int h = i / quads, c = i % quads;
+      auto fetch = [&](int p, float x[4]) {
+        const float* src = kb + (long)(grp * L.KG + p) * rowsz + h * L.D + 4 * c;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = src[e];
+      };
+      quantize_k_group(L, a.pages, blk, grp, grp * L.KG, L.KG, bits, h, c, fetch);
+    }
+  }
+  const int G = L.D / L.VG;
+  const int side = L.H * L.D * bits / 8;
+  const int items = L.H * quads;
+  for (int off = 0; off < L.BS; ++off) {
+    const long rb = row_base(a.pages, L, blk, off, bits);
+    for (int base = 0; base < items; base += kThreads) {
+      const int i = base + (int)threadIdx.x;
+      const bool act = i < items;
+      const int h = act ? i / quads : 0, c = act ? i % quads : 0;
+      float x[4] = {0.f, 0.f, 0.f, 0.f};
+      if (act) {
+        const float* src = vb + (long)off * rowsz + h * L.D + 4 * c;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = src[e];
+      }
+      float mn = fminf(fminf(x[0], x[1]), fminf(x[2], x[3]));
+      float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      seg_minmax(mn, mx, L.VG / 4);
+      if (!act || rb < 0) continue;
+      _Float16 s16, m16;
+      float s, m;
+      group_stats(mn, mx, bits, s16, m16, s, m);
+      if ((4 * c) % L.VG == 0) {
+        const long e = ((long)off * L.H + h) * G + (4 * c) / L.VG;
+        *f16p(a.pages, blk * L.stride + L.o_vs + 2 * e) = s16;
+        *f16p(a.pages, blk * L.stride + L.o_vm + 2 * e) = m16;
+      }
+      uint32_t q[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[e] = quant_code(x[e], m, s, bits);
+      store_codes4(a.pages + rb + side + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dequantization of one token (head h, channels 4c..4c+3): K from the residual
+// when it is the block's open group, else codes x per-channel stats; V codes x
+// per-token stats. `bits` is already resolved by the caller.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void dequant_token4(const Lay& L, const uint8_t* pages, const int64_t* block_res,
+                                               const int64_t* res_group, const Res& res, long blk, int off,
+                                               int bits, int h, int c, float k[4], float v[4]) {
+  const long rb = row_base(pages, L, blk, off, bits);
+  const int G = L.D / L.VG;
+  if (rb < 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) k[e] = v[e] = 0.f;
+    return;
+  }
+  const long hb = (long)h * (L.D * bits / 8) + c * (bits / 2);
+  const uint32_t vc = load_codes4(pages + rb + L.H * L.D * bits / 8 + hb, bits);
+  const long ve = ((long)off * L.H + h) * G + (4 * c) / L.VG;
+  const float vs = (float)*f16p(pages, blk * L.stride + L.o_vs + 2 * ve);
+  const float vm = (float)*f16p(pages, blk * L.stride + L.o_vm + 2 * ve);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = code_at(vc, e, bits) * vs + vm;
+  const long rs = block_res[blk];
+  const int grp = off / L.KG;
+  if (rs >= 0 && rs < res.rows && res_group[rs] == grp) {
+    ld4(res.ptr, res.dtype, rs * res.s0 + (long)(off % L.KG) * res.s1 + h * res.s2 + 4 * c, k);
+    return;
+  }
+  const uint32_t kc = load_codes4(pages + rb + hb, bits);
+  const long se = ((long)grp * L.H + h) * L.D + 4 * c;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float ks = (float)*f16p(pages, blk * L.stride + L.o_ks + 2 * (se + e));
+    const float km = (float)*f16p(pages, blk * L.stride + L.o_km + 2 * (se + e));
+    k[e] = code_at(kc, e, bits) * ks + km;
+  }
+}
+
+// gather (echokv_vllm/tiered_cache.py:451-478): never-opened blocks read as zeros.
+
+__global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
+  const Lay& L = a.L;
+  const long i = blockIdx.x;
+  const long blk = a.blk[i];
+  const int off = (int)a.off[i];
+  const int quads = L.D / 4;
+  const long ob = i * (long)L.H * L.D;
+  const bool ok = blk >= 0 && blk < L.nb && off >= 0 && off < L.BS;
+  const uint32_t tag = ok ? a.pages[blk * L.stride] : 0u;
+  const bool opened = tag == 2u || tag == 4u || tag == 8u;
+  for (int it = threadIdx.x; it < L.H * quads; it += kThreads) {
+    const int h = it / quads, c = it % quads;
+    float k[4] = {0.f, 0.f, 0.f, 0.f}, v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (opened) dequant_token4(L, a.pages, a.block_res, a.res_group, a.res, blk, off, (int)tag, h, c, k, v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a.k_out[ob + h * L.D + 4 * c + e] = k[e];
+      a.v_out[ob + h * L.D + 4 * c + e] = v[e];
+    }
+  }
+}
+
+// dequant_dense (echokv_vllm/kernels/prefill.py:90-115, 330-369): work rows
+// (block-table row, block index, dense row of the block start, ctx).
+
+__global__ __launch_bounds__(kThreads) void dequant_dense_kernel(DenseArgs a) {
+  const Lay& L = a.L;
+  const int32_t* w = a.work + blockIdx.x * 4;
+  const long req = w[0];
+  const int bi = w[1];
+  const long row0 = w[2];
+  const int ctx = w[3];
+  const long blk = a.bt[req * a.bt_s0 + bi];
+  if (blk < 0 || blk >= L.nb) return;
+  const int bits = tier_of(a.pages[blk * L.stride]);
+  const int quads = L.D / 4;
+  int n = ctx - bi * L.BS;
+  n = n < L.BS ? n : L.BS;
+  const int items = n * L.H * quads;
+  for (int it = threadIdx.x; it < items; it += kThreads) {
+    const int t = it / (L.H * quads);
+    const int r = it % (L.H * quads);
+    const int h = r / quads, c = r % quads;
+    float k[4], v[4];
+    dequant_token4(L, a.pages, a.block_res, a.res_group, a.res, blk, t, bits, h, c, k, v);
+    const long o = (row0 + t) * a.o_s0 + h * a.o_s1 + 4 * c;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      st(a.k_out, a.out_dtype, o + e, k[e]);
+      st(a.v_out, a.out_dtype, o + e, v[e]);
+    }
+  }
+}
+
+}  // namespace ek
+
+// ---------------------------------------------------------------------------
+// Launchers (called from abi.hip)
+// ---------------------------------------------------------------------------
+namespace ek {
+
+hipError_t launch_write_tokens(const WriteTokArgs& a, long n_rows, hipStream_t s) {
+  hipLaunchKernelGGL(write_tokens_kernel, dim3((unsigned)n_rows), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+hipError_t launch_finalize_k(const FinArgs& a, long rows, hipStream_t s) {
+  hipLaunchKernelGGL(finalize_k_kernel, dim3((unsigned)rows), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+hipError_t launch_seal(const SealArgs& a, long n, hipStream_t s) {
+  hipLaunchKernelGGL(seal_kernel, dim3((unsigned)n), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+hipError_t launch_store_blocks(const StoreBlkArgs& a, long n, hipStream_t s) {
+  hipLaunchKernelGGL(store_blocks_kernel, dim3((unsigned)n), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+hipError_t launch_gather(const GatherArgs& a, long n, hipStream_t s) {
+  hipLaunchKernelGGL(gather_kernel, dim3((unsigned)n), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+hipError_t launch_dequant_dense(const DenseArgs& a, long n, hipStream_t s) {
+  hipLaunchKernelGGL(dequant_dense_kernel, dim3((unsigned)n), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace ek

@@ -1,0 +1,92 @@
+"""Paged decode attention over a ``TieredKVCache`` (one query token per sequence).
+
+Interface of ``echokv_vllm/kernels/decode.py:44-92`` (``decode_attention``).
+The work runs in two HIP kernels (``echokv_amd/csrc/decode.hip``): a split-KV
+MFMA kernel -- one workgroup per (sequence, split), one wave per KV head,
+each block's tier read from its page header -- and a log-sum-exp merge that
+writes each sequence's output row. A sequence is cut into at most
+``num_splits`` splits of ``max(blocks_per_split, ceil(blocks / num_splits))``
+blocks, a function of its own length, so its result does not depend on the
+rest of the batch.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from echokv_amd import _lib
+
+BLOCKS_PER_SPLIT = 16
+
+
+def _i64(t: torch.Tensor | None, device) -> torch.Tensor | None:
+    if t is None:
+        return None
+    if t.dtype != torch.int64 or not t.is_contiguous() or t.device != device:
+        t = t.to(device=device, dtype=torch.int64).contiguous()
+    return t
+
+
+def default_splits(block_table: torch.Tensor, block_size: int, blocks_per_split: int, max_len: int | None) -> int:
+    max_blocks = block_table.shape[1] if max_len is None else min(block_table.shape[1], -(-max_len // block_size))
+    return max(1, -(-max_blocks // blocks_per_split))
+
+
+def decode_attention(
+    store,
+    query: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: torch.Tensor,
+    softmax_scale: float,
+    blocks_per_split: int = BLOCKS_PER_SPLIT,
+    q_rows: torch.Tensor | None = None,
+    bt_rows: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    max_len: int | None = None,
+    num_splits: int | None = None,
+    workspace: tuple[torch.Tensor, torch.Tensor] | None = None,
+) -> torch.Tensor:
+    """Attention of one query token per sequence over each sequence's cache.
+
+    Sequence ``i`` uses query row ``q_rows[i]`` and block-table row ``bt_rows[i]``
+    (default: row ``i``) with cache length ``seq_lens[i]`` (its own token
+    included). Without ``out`` returns float32 ``[S, Hq, D]``; with ``out``
+    writes sequence ``i`` to ``out[q_rows[i]]`` in ``out``'s dtype; length-0
+    sequences (graph padding) leave their row untouched. ``workspace`` =
+    caller-owned ``(acc [S, Hq, splits, D], ml [S, Hq, splits, 2])`` float32.
+    """
+    L = store.layout
+    dev = query.device
+    _lib.require_device(query, block_table, seq_lens, store.pages)
+    s = seq_lens.shape[0]
+    hq, d = query.shape[1], query.shape[2]
+    if num_splits is None:
+        num_splits = default_splits(block_table, L.block_size, blocks_per_split, max_len)
+    if query.stride(2) != 1:
+        query = query.contiguous()
+    if block_table.dtype != torch.int32 or block_table.stride(1) != 1:
+        block_table = block_table.to(torch.int32).contiguous()
+    lens = _i64(seq_lens, dev)
+    q_rows = _i64(q_rows, dev)
+    bt_rows = _i64(bt_rows, dev)
+    if out is None:
+        out = torch.empty(s if q_rows is None else query.shape[0], hq, d, device=dev, dtype=torch.float32)
+    if out.stride(2) != 1:
+        raise ValueError("out rows must be contiguous along head_dim")
+    if workspace is None:
+        acc = torch.empty(s, hq, num_splits, d, device=dev, dtype=torch.float32)
+        ml = torch.empty(s, hq, num_splits, 2, device=dev, dtype=torch.float32)
+    else:
+        acc, ml = workspace
+        if acc.numel() < s * hq * num_splits * d or ml.numel() < s * hq * num_splits * 2:
+            raise ValueError("decode workspace is too small for this batch and split grid")
+    res = _lib.residual(store.res_k)
+    _lib.call(
+        "echokv_decode", _lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(store.block_res),
+        _lib.ptr(store.res_group), _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1),
+        _lib.dtype_code(query), hq, _lib.ptr(q_rows), _lib.ptr(block_table), block_table.stride(0),
+        _lib.ptr(bt_rows), _lib.ptr(lens), s, float(softmax_scale), int(num_splits), int(blocks_per_split),
+        _lib.ptr(acc), _lib.ptr(ml), _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out),
+        _lib.stream(),
+    )
+    return out

@@ -1,0 +1,68 @@
+"""Quantize-on-write entry points (``echokv_vllm/kernels/write.py:29-50``).
+
+``write_tokens`` stores every token row of a step in one launch (V per token,
+K to the residual / under sealed stats / into the K_ref ring); ``finalize_k``
+quantizes each completed K group per channel. Both read each block's tier
+from its page header on the device and everything else from ``WriteMeta``,
+so one launch covers INT2/INT4/INT8 blocks and a HIP graph can capture them.
+Kernels: ``echokv_amd/csrc/store.hip`` via ``echokv_write_tokens`` /
+``echokv_finalize_k``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from echokv_amd import _lib
+
+
+def _kv(t: torch.Tensor) -> torch.Tensor:
+    if t.stride(-1) != 1:
+        t = t.contiguous()
+    return t
+
+
+def write_tokens(store, key: torch.Tensor, value: torch.Tensor, meta, kref: torch.Tensor | None = None) -> None:
+    """Store the ``meta.n_rows`` token rows of ``key``/``value`` ``[T, H, D]`` as ``meta.tok`` says."""
+    if meta.n_rows == 0:
+        return
+    _lib.require_device(key, value, store.pages)
+    key, value = _kv(key), _kv(value)
+    if value.dtype != key.dtype:
+        value = value.to(key.dtype)
+    tok = meta.tok
+    if tok.stride(1) != 1 or tok.dtype != torch.int64:
+        raise ValueError("meta.tok must be int64 with contiguous rows")
+    if kref is not None:
+        if kref.dtype != torch.float32 or kref.stride(2) != 1:
+            raise ValueError("the K_ref ring must be float32 with contiguous rows")
+    res = _lib.residual(store.res_k)
+    _lib.call(
+        "echokv_write_tokens", _lib.byref(store.abi), _lib.ptr(store.pages),
+        _lib.ptr(key), key.stride(0), key.stride(1), _lib.ptr(value), value.stride(0), value.stride(1),
+        _lib.dtype_code(key), _lib.ptr(tok), tok.stride(0), meta.n_rows, _lib.byref(res),
+        _lib.ptr(kref), 0 if kref is None else kref.stride(0), 0 if kref is None else kref.stride(1),
+        _lib.stream(),
+    )
+
+
+def finalize_k(store, key: torch.Tensor, meta, full_grid: bool = False) -> None:
+    """Quantize each completed K group per channel and store its codes and stats.
+
+    ``full_grid`` launches one program per token row, masked on the device by
+    ``meta.fin_count`` (a captured graph does not know the count)."""
+    n = meta.n_rows if full_grid else meta.n_fin
+    if n == 0:
+        return
+    _lib.require_device(key, store.pages)
+    key = _kv(key)
+    fin = meta.fin
+    if fin.numel() and fin.stride(1) != 1:
+        raise ValueError("meta.fin must have contiguous rows")
+    # A full grid only reads rows below the device count (<= fin's rows).
+    res = _lib.residual(store.res_k)
+    _lib.call(
+        "echokv_finalize_k", _lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(key), key.stride(0),
+        key.stride(1), _lib.dtype_code(key), _lib.ptr(fin), _lib.ptr(meta.fin_count), n, _lib.byref(res),
+        _lib.stream(),
+    )

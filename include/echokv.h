@@ -1,0 +1,152 @@
+/*
+ * echokv.h -- C ABI of the MI355X (gfx950) EchoKV quantized KV-cache hot path.
+ *
+ * Every entry point launches HIP kernels asynchronously on the given stream and
+ * returns 0 on success or an ECHOKV_E* code (no launch happened) on a bad
+ * argument. The library never allocates, frees, synchronizes or reads device
+ * memory from the host; every buffer is caller-owned, so calls can be captured
+ * in a HIP graph. Pointers are device pointers unless noted; strides are in
+ * elements. Functions are reentrant (no mutable global state).
+ *
+ * Each entry point names the reference interface it replaces
+ * (paths relative to the zimo0110/echokv tree).
+ */
+#ifndef ECHOKV_H
+#define ECHOKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* echokv_stream_t; /* a hipStream_t */
+
+enum { ECHOKV_F32 = 0, ECHOKV_F16 = 1, ECHOKV_BF16 = 2 };
+
+enum {
+  ECHOKV_OK = 0,
+  ECHOKV_EINVAL = 1,     /* bad pointer / count / stride */
+  ECHOKV_ESHAPE = 2,     /* layout or head shape this build does not support */
+  ECHOKV_EDTYPE = 3,     /* unsupported dtype code */
+  ECHOKV_ELAUNCH = 4,    /* the HIP launch itself failed */
+};
+
+/* One layer's page layout (echokv_vllm/tiered_cache.py:76-147, TieredLayout):
+ * header [0, block_size); V scale/min fp16 [block_size, H, D/v_group];
+ * K scale/min fp16 [block_size/k_group, H, D]; then chunks_per_page chunks of
+ * chunk_bytes = block_size*H*D/2 bytes. Token rows are [K codes | V codes]. */
+typedef struct echokv_layout {
+  int32_t num_kv_heads, head_size, block_size, k_group, v_group, chunks_per_page;
+  int64_t num_blocks;   /* pages in this layer's view */
+  int64_t page_stride;  /* bytes between consecutive pages (16-byte multiple) */
+  int64_t o_v_scale, o_v_min, o_k_scale, o_k_min, o_data, chunk_bytes;
+} echokv_layout;
+
+/* Full-precision K of each block's open group: [rows, k_group, H, D]
+ * (echokv_vllm/tiered_cache.py:207-211, TieredKVCache.res_k). */
+typedef struct echokv_residual {
+  void* ptr;
+  int32_t dtype; /* ECHOKV_F32 / F16 / BF16 */
+  int32_t rows;  /* residual slots + 1 */
+  int64_t s0, s1, s2;
+} echokv_residual;
+
+const char* echokv_error_string(int code);
+
+/* Quantize-on-write of one step's token rows: V per token (groups of v_group),
+ * K to the residual / under sealed stats / to the K_ref ring.
+ * tok: [4, tok_s0] int64 = (slot, residual slot, sealed, kref row) per row.
+ * Replaces echokv_vllm/kernels/write.py:29-36 (write_tokens) and its kernel
+ * write.py:280-338 (_write_tokens_kernel). kref may be NULL. */
+int echokv_write_tokens(const echokv_layout* L, uint8_t* pages,
+                        const void* key, int64_t k_s0, int64_t k_s1,
+                        const void* value, int64_t v_s0, int64_t v_s1, int32_t kv_dtype,
+                        const int64_t* tok, int64_t tok_s0, int64_t n_rows,
+                        const echokv_residual* res, float* kref, int64_t kref_s0, int64_t kref_s1,
+                        echokv_stream_t stream);
+
+/* Per-channel quantization of each completed K group.
+ * fin: [>= grid_rows, 3 + k_group] int64 = (block, group, residual slot, token row per
+ * position or -1 = residual); rows >= *fin_count are skipped (graph full grid).
+ * Replaces echokv_vllm/kernels/write.py:39-50 (finalize_k), kernel write.py:340-396. */
+int echokv_finalize_k(const echokv_layout* L, uint8_t* pages,
+                      const void* key, int64_t k_s0, int64_t k_s1, int32_t kv_dtype,
+                      const int64_t* fin, const int64_t* fin_count, int64_t grid_rows,
+                      const echokv_residual* res, echokv_stream_t stream);
+
+/* Seal evicted residual groups: ev [n, 6] int64 = (slot, block, group, fill, bits, mask).
+ * Replaces the device ops of echokv_vllm/tiered_cache.py:379-394 (_seal). */
+int echokv_seal_groups(const echokv_layout* L, uint8_t* pages, const int64_t* ev, int64_t n,
+                       const echokv_residual* res, echokv_stream_t stream);
+
+/* Dequantized K and V (float32 [n, H, D]) of tokens (blk[i], off[i]); never-opened
+ * blocks read as zeros, a block's open K group reads the residual.
+ * Replaces echokv_vllm/tiered_cache.py:451-478 (gather). */
+int echokv_gather(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                  const int64_t* res_group, const echokv_residual* res,
+                  const int64_t* blk, const int64_t* off, int64_t n,
+                  float* k_out, float* v_out, echokv_stream_t stream);
+
+/* Requantize whole blocks from float32 K, V [n*block_size, H, D] at `bits`, setting
+ * the tag byte (K per channel over K groups, V per token).
+ * Replaces the device ops of echokv_vllm/tiered_cache.py:322-340 (_demote_lru). */
+int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* blocks, int64_t n,
+                        const float* k, const float* v, int32_t bits, echokv_stream_t stream);
+
+/* Split-KV paged decode attention + split merge: sequence i attends with query row
+ * q_rows[i] (NULL = i) over block-table row bt_rows[i] (NULL = i) for seq_lens[i]
+ * tokens and writes out[q_rows[i]]; seq_lens[i] == 0 leaves the row untouched.
+ * Split size = max(blocks_per_split, ceil(blocks / num_splits)) of the sequence's own
+ * length (batch invariant). acc: [num_seqs, Hq, num_splits, D] f32, ml:
+ * [num_seqs, Hq, num_splits, 2] f32 workspaces.
+ * Replaces echokv_vllm/kernels/decode.py:44-92 (decode_attention) with its kernels
+ * decode.py:135-224 (_decode_kernel) and decode.py:227-262 (_merge_kernel). */
+int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                  const int64_t* res_group, const echokv_residual* res,
+                  const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype, int32_t num_q_heads,
+                  const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
+                  const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs,
+                  float softmax_scale, int32_t num_splits, int32_t blocks_per_split,
+                  float* acc, float* ml, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                  echokv_stream_t stream);
+
+/* Chunked-prefill attention over the tiered pages (MFMA tiles), bottom-right causal:
+ * tiles [n_tiles, 5] int32 = (first query row, tokens, first query position, ctx,
+ * block-table row); each tile holds <= tile_m query tokens.
+ * Replaces echokv_vllm/kernels/prefill.py:170-207 (prefill_attention: the fused kernel
+ * prefill.py:242-327 and the dense dequant + flash-attention path prefill.py:133-167). */
+int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                   const int64_t* res_group, const echokv_residual* res,
+                   const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype, int32_t num_q_heads,
+                   void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                   const int32_t* tiles, int64_t n_tiles, int32_t tile_m,
+                   const int32_t* block_table, int64_t bt_s0, float softmax_scale,
+                   echokv_stream_t stream);
+
+/* Dense dequantization of prefill contexts: work [n, 4] int32 = (block-table row,
+ * block index, dense row of the block's first token, ctx) -> K, V [*, H, D].
+ * Replaces echokv_vllm/kernels/prefill.py:90-115 (dequant_dense), kernel 330-369. */
+int echokv_dequant_dense(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                         const int64_t* res_group, const echokv_residual* res,
+                         const int32_t* work, int64_t n_work, const int32_t* block_table, int64_t bt_s0,
+                         void* k_out, void* v_out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                         echokv_stream_t stream);
+
+/* Canary: for each layer and tier bits[j], the mean over query rows and heads of
+ * KL(softmax(q K~ᵀ s) || softmax(q K_refᵀ s)), K~ = per-channel storage round trip
+ * of the last floor(window/k_group)*k_group keys; clamped >= 0.
+ * query [L, nq, Hq, D] (strides q_sl, q_s0, q_s1), kref f32 [L, window, H, D]
+ * oldest first (strides k_sl, k_s0, k_s1) -> out f32 [L, nbits]; tier j is byte j of
+ * bits_packed (each 2, 4 or 8).
+ * Replaces echokv_vllm/canary.py:59-89 (canary_kl). */
+int echokv_canary_kl(const void* query, int32_t q_dtype, int64_t q_sl, int64_t q_s0, int64_t q_s1,
+                     const float* kref, int64_t k_sl, int64_t k_s0, int64_t k_s1,
+                     int32_t num_layers, int32_t nq, int32_t num_q_heads, int32_t num_kv_heads,
+                     int32_t head_size, int32_t window, int32_t nbits, int32_t bits_packed, int32_t k_group,
+                     float softmax_scale, float* out, echokv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ECHOKV_H */

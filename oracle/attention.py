@@ -1,0 +1,47 @@
+"""Decode and chunked-prefill attention over dequantized K/V (oracle; tests only).
+
+Restates ``echokv_vllm/kernels/decode.py:95-129`` (one query token per
+sequence over its cache, GQA by repeating KV heads) and
+``echokv_vllm/kernels/prefill.py:210-236`` (a chunk of ``nq`` queries over a
+context of ``ctx`` keys with the bottom-right causal mask: query ``i`` sees
+keys ``<= ctx - nq + i``). Softmax and products run in float64.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def attend(q, k, v, scale, limit=None):
+    """``q [Hq, D]``, ``k, v [n, H, D]`` -> ``[Hq, D]``; keys ``>= limit`` masked."""
+    hq, h = q.shape[0], k.shape[1]
+    rep = hq // h
+    kk = np.repeat(k.astype(np.float64), rep, axis=1)  # [n, Hq, D]
+    vv = np.repeat(v.astype(np.float64), rep, axis=1)
+    s = np.einsum("hd,nhd->hn", q.astype(np.float64), kk) * scale
+    if limit is not None:
+        s[:, limit:] = -np.inf
+    s -= s.max(axis=1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=1, keepdims=True)
+    return np.einsum("hn,nhd->hd", p, vv)
+
+
+def decode_attention(store, query, block_table, seq_lens, scale):
+    """decode.py:95-129: float ``[S, Hq, D]``."""
+    out = np.zeros(query.shape, np.float64)
+    for i, n in enumerate(np.asarray(seq_lens).tolist()):
+        k, v = store.gather_seq(block_table[i], n)
+        out[i] = attend(query[i], k, v, scale)
+    return out
+
+
+def prefill_attention(store, query, prefill, req_of, block_table, scale):
+    """prefill.py:210-236: ``prefill`` = [(q_start, q_end, ctx, _)], ``req_of`` = block-table rows."""
+    out = np.zeros(query.shape, np.float64)
+    for (qs, qe, ctx, _), r in zip(prefill, req_of):
+        k, v = store.gather_seq(block_table[r], ctx)
+        nq = qe - qs
+        for i in range(nq):
+            out[qs + i] = attend(query[qs + i], k, v, scale, limit=ctx - nq + i + 1)
+    return out
