@@ -225,7 +225,9 @@ int echokv_canary_kl(const void* query, int32_t q_dtype, int64_t q_sl, int64_t q
                      int32_t k_group, float softmax_scale, float* out, echokv_stream_t stream) {
   if (!dtype_ok(q_dtype)) return ECHOKV_EDTYPE;
   if (num_layers < 0 || nq < 1 || num_kv_heads < 1 || num_q_heads % num_kv_heads || k_group < 1) return ECHOKV_EINVAL;
-  if (head_size < 1 || head_size > ek::kCanaryMaxD || window < k_group || window > ek::kCanaryMaxKeys)
+  // Only the last floor(window / k_group) * k_group keys are scored and staged.
+  if (head_size < 1 || head_size > ek::kCanaryMaxD || window < k_group ||
+      (window / k_group) * k_group > ek::kCanaryMaxKeys)
     return ECHOKV_ESHAPE;
   if (nbits < 1 || nbits > ek::kCanaryMaxTiers) return ECHOKV_EINVAL;
   for (int t = 0; t < nbits; ++t) {

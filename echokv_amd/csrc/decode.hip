@@ -8,10 +8,14 @@
 // Per 16-token tile a wave runs two MFMA contractions with no transposes:
 //   S^T[t, q]  = sum_d codes[t, d] * (q[q, d] * k_scale[d]) + sum_d q[q, d] * k_min[d]
 //                (v_mfma_f32_16x16x32_f16; the K scale is folded into the query,
-//                 the K min into a per-query bias; the open K group reads the
-//                 full-precision residual instead, against the plain query)
+//                 the K min into a per-query float32 bias; the block's open K
+//                 group reads the full-precision residual instead)
 //   O^T[d, q] += V[t, d]^T * P^T[t, q]   (v_mfma_f32_16x16x16f16, V dequantized
 //                 to fp16 in registers with its per-token fp16 scale / min)
+// Codes are exact in fp16. The query-side operand (q * k_scale, and the residual
+// keys) is carried as an fp16 hi + lo pair -- lo = fma(q, s, -hi) rounded once --
+// and contracted twice, so S is accurate to ~2^-22 instead of fp16's 2^-11:
+// keys with large outlier channels would otherwise dominate the error.
 // The S^T accumulator layout (lane = 4 tokens x 1 query column) is exactly the
 // B-operand layout of the second MFMA, and the O^T accumulator keeps one query
 // column per lane, so the online softmax runs per lane with two cross-lane
@@ -25,7 +29,6 @@
 #include "args.h"
 
 namespace ek {
-
 
 __device__ __forceinline__ h2_t u2h(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 __device__ __forceinline__ uint32_t h2u(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
@@ -98,36 +101,48 @@ __device__ __forceinline__ void load_bytes(const uint8_t* p, uint32_t* w) {
   }
 }
 
-// Per-wave decode state for head_dim D.
-template <int D>
+// Per-wave decode state for head_dim D. QLO: the query has a low part (float32 input).
+template <int D, bool QLO>
 struct Wave {
   static constexpr int CPL = D / 4;   // K channels per lane in the QK fragments
-  static constexpr int NQK = D / 32;  // 16x16x32 MFMAs per tile for S^T
+  static constexpr int NQK = D / 32;  // 16x16x32 MFMAs per tile for S^T (per hi / lo part)
   static constexpr int CPM = D / 16;  // V channels per lane = 16x16x16 MFMAs per tile
-  uint32_t qn[CPL / 2];               // fp16 query pairs, natural channel order
-  h8_t qk[NQK];                       // scaled query fragments for the current K group
+  uint32_t qn[CPL / 2];               // fp16 query pairs (hi), natural channel order
+  uint32_t ql[QLO ? CPL / 2 : 1];     // fp16 query pairs (lo = q - hi)
+  h8_t qk[NQK], qkl[NQK];             // q * k_scale (hi, lo) fragments, current K group
   float bias;                         // sum_d q * k_min for the current K group
   f4_t acc[CPM];                      // O^T fragments
   float m_run, l_lane;
 };
 
-template <int D, int BITS>
-__device__ __forceinline__ void build_qk(Wave<D>& w, const uint8_t* pages, const Lay& L, long blk, int grp, int h,
-                                         int c) {
-  constexpr int CPL = Wave<D>::CPL;
+template <int D, bool QLO, int BITS>
+__device__ __forceinline__ void build_qk(Wave<D, QLO>& w, const uint8_t* pages, const Lay& L, long blk, int grp,
+                                         int h, int c) {
+  constexpr int CPL = Wave<D, QLO>::CPL;
   const long e0 = ((long)grp * L.H + h) * D + c * CPL;
   uint32_t ks[CPL / 2], km[CPL / 2];
   load_bytes<2 * CPL>(pages + blk * L.stride + L.o_ks + 2 * e0, ks);
   load_bytes<2 * CPL>(pages + blk * L.stride + L.o_km + 2 * e0, km);
   float b = 0.f;
-  uint32_t prod[CPL / 2];
+  uint32_t hi[CPL / 2], lo[CPL / 2];
 #pragma unroll
   for (int i = 0; i < CPL / 2; ++i) {
-    prod[i] = h2u(u2h(w.qn[i]) * u2h(ks[i]));
-    b = __builtin_amdgcn_fdot2(u2h(w.qn[i]), u2h(km[i]), b, false);
+    const h2_t q = u2h(w.qn[i]), s = u2h(ks[i]);
+    const h2_t ph = q * s;
+    h2_t pl = __builtin_elementwise_fma(q, s, -ph);  // exact product minus its rounding, rounded once
+    b = __builtin_amdgcn_fdot2(q, u2h(km[i]), b, false);
+    if constexpr (QLO) {
+      pl = __builtin_elementwise_fma(u2h(w.ql[i]), s, pl);
+      b = __builtin_amdgcn_fdot2(u2h(w.ql[i]), u2h(km[i]), b, false);
+    }
+    hi[i] = h2u(ph);
+    lo[i] = h2u(pl);
   }
 #pragma unroll
-  for (int j = 0; j < Wave<D>::NQK; ++j) w.qk[j] = reorder8<BITS>(prod + 4 * j);
+  for (int j = 0; j < Wave<D, QLO>::NQK; ++j) {
+    w.qk[j] = reorder8<BITS>(hi + 4 * j);
+    w.qkl[j] = reorder8<BITS>(lo + 4 * j);
+  }
   b += __shfl_xor(b, 16, 64);
   b += __shfl_xor(b, 32, 64);
   w.bias = b;
@@ -135,8 +150,8 @@ __device__ __forceinline__ void build_qk(Wave<D>& w, const uint8_t* pages, const
 
 // Online-softmax update with the tile's S^T fragment (already scaled to log2
 // units and masked), then O^T += V^T P^T.
-template <int D>
-__device__ __forceinline__ void softmax_pv(Wave<D>& w, f4_t s, const h4_t* va) {
+template <int D, bool QLO>
+__device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, f4_t s, const h4_t* va) {
   float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
   mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
   mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
@@ -149,7 +164,7 @@ __device__ __forceinline__ void softmax_pv(Wave<D>& w, f4_t s, const h4_t* va) {
   w.m_run = m_new;
   const h4_t pb = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
 #pragma unroll
-  for (int j = 0; j < Wave<D>::CPM; ++j) {
+  for (int j = 0; j < Wave<D, QLO>::CPM; ++j) {
     w.acc[j] *= alpha;
     w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j], pb, w.acc[j], 0, 0, 0);
   }
@@ -157,10 +172,11 @@ __device__ __forceinline__ void softmax_pv(Wave<D>& w, f4_t s, const h4_t* va) {
 
 // One 16-token tile [t0, t0 + 16) of block `blk` (tier BITS); tokens >= n_valid
 // are masked. in_res: the tile is the block's open K group (K from the residual).
-template <int D, int BITS>
-__device__ __forceinline__ void tile(Wave<D>& w, const DecodeArgs& a, long blk, int t0, int n_valid, long rslot,
+template <int D, bool QLO, int BITS>
+__device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long blk, int t0, int n_valid, long rslot,
                                      bool in_res, int h, int lane) {
-  constexpr int CPL = Wave<D>::CPL, NQK = Wave<D>::NQK, CPM = Wave<D>::CPM;
+  using W = Wave<D, QLO>;
+  constexpr int CPL = W::CPL, NQK = W::NQK, CPM = W::CPM;
   const Lay& L = a.L;
   const int c = lane >> 4, n = lane & 15;
   const uint8_t* pages = a.pages;
@@ -173,22 +189,33 @@ __device__ __forceinline__ void tile(Wave<D>& w, const DecodeArgs& a, long blk, 
   const bool kvalid = tk < n_valid;
   if (in_res) {
     const long r0 = rslot * a.res.s0 + (long)(tk % L.KG) * a.res.s1 + h * a.res.s2 + c * CPL;
+    const bool res_lo = a.res.dtype == ECHOKV_F32;  // fp16 / bf16 keys are exact in fp16
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
-      h8_t kf;
+      h8_t kh, kl;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) kf[e] = kvalid ? (_Float16)ld(a.res.ptr, a.res.dtype, r0 + 8 * j + e) : (_Float16)0.f;
-      const h8_t qf = cat8(u2h(w.qn[4 * j]), u2h(w.qn[4 * j + 1]), u2h(w.qn[4 * j + 2]), u2h(w.qn[4 * j + 3]));
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf, s, 0, 0, 0);
+      for (int e = 0; e < 8; ++e) {
+        const float x = kvalid ? ld(a.res.ptr, a.res.dtype, r0 + 8 * j + e) : 0.f;
+        kh[e] = (_Float16)x;
+        kl[e] = (_Float16)(x - (float)kh[e]);
+      }
+      const h8_t qh = cat8(u2h(w.qn[4 * j]), u2h(w.qn[4 * j + 1]), u2h(w.qn[4 * j + 2]), u2h(w.qn[4 * j + 3]));
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh, s, 0, 0, 0);
+      if (res_lo) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh, s, 0, 0, 0);
+      if constexpr (QLO) {
+        const h8_t ql = cat8(u2h(w.ql[4 * j]), u2h(w.ql[4 * j + 1]), u2h(w.ql[4 * j + 2]), u2h(w.ql[4 * j + 3]));
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql, s, 0, 0, 0);
+      }
     }
   } else {
     const long rb = row_base(pages, L, blk, tk, BITS);
-    uint32_t kw[CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1];
+    constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
+    uint32_t kw[KW];
     if (rb >= 0) {
       load_bytes<CPL * BITS / 8>(pages + rb + headb + (long)c * (CPL * BITS / 8), kw);
     } else {
 #pragma unroll
-      for (int i = 0; i < (CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1); ++i) kw[i] = 0;
+      for (int i = 0; i < KW; ++i) kw[i] = 0;
     }
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
@@ -202,7 +229,9 @@ __device__ __forceinline__ void tile(Wave<D>& w, const DecodeArgs& a, long blk, 
       } else {
         wj[0] = kw[j >> 1] >> (16 * (j & 1));
       }
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack8<BITS>(wj), w.qk[j], s, 0, 0, 0);
+      const h8_t kf = unpack8<BITS>(wj);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, w.qk[j], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, w.qkl[j], s, 0, 0, 0);
     }
   }
 #pragma unroll
@@ -215,7 +244,6 @@ __device__ __forceinline__ void tile(Wave<D>& w, const DecodeArgs& a, long blk, 
   constexpr int VB = CPM * BITS / 8;  // bytes per token of the lane's V slice
   constexpr int VW = VB >= 4 ? VB / 4 : 1;
   uint32_t vw[4][VW];
-  uint32_t sc2[2], mn2[2];
   const int G = D / L.VG;
   const int g = (n * CPM) / L.VG;
   _Float16 sv[4], mv[4];
@@ -249,17 +277,16 @@ __device__ __forceinline__ void tile(Wave<D>& w, const DecodeArgs& a, long blk, 
     const uint32_t mask = ((1u << BITS) - 1u) * 0x00010001u;
     const uint32_t x01 = (__builtin_amdgcn_perm(vw[1][wd], vw[0][wd], sel) >> sh) & mask;
     const uint32_t x23 = (__builtin_amdgcn_perm(vw[3][wd], vw[2][wd], sel) >> sh) & mask;
-    const h2_t v01 = code_pair(x01) * s01 + m01;
-    const h2_t v23 = code_pair(x23) * s23 + m23;
+    const h2_t v01 = __builtin_elementwise_fma(code_pair(x01), s01, m01);
+    const h2_t v23 = __builtin_elementwise_fma(code_pair(x23), s23, m23);
     va[j] = h4_t{v01[0], v01[1], v23[0], v23[1]};
   }
-  (void)sc2;
-  (void)mn2;
-  softmax_pv<D>(w, s, va);
+  softmax_pv<D, QLO>(w, s, va);
 }
 
-template <int D>
+template <int D, bool QLO>
 __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
+  using W = Wave<D, QLO>;
   const Lay& L = a.L;
   const int split = blockIdx.x;
   const long seq = blockIdx.y;
@@ -278,19 +305,24 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
   const long bt_row = a.bt_rows ? a.bt_rows[seq] : seq;
   const int c = lane >> 4, n = lane & 15;
 
-  Wave<D> w;
+  W w;
   {
     const bool qv = n < a.gqa;
-    const long qb = q_row * a.q_s0 + (long)(h * a.gqa + (qv ? n : 0)) * a.q_s1 + c * Wave<D>::CPL;
+    const long qb = q_row * a.q_s0 + (long)(h * a.gqa + (qv ? n : 0)) * a.q_s1 + c * W::CPL;
 #pragma unroll
-    for (int i = 0; i < Wave<D>::CPL / 2; ++i) {
-      const h2_t p = {(_Float16)(qv ? ld(a.q, a.q_dtype, qb + 2 * i) : 0.f),
-                      (_Float16)(qv ? ld(a.q, a.q_dtype, qb + 2 * i + 1) : 0.f)};
-      w.qn[i] = h2u(p);
+    for (int i = 0; i < W::CPL / 2; ++i) {
+      const float x0 = qv ? ld(a.q, a.q_dtype, qb + 2 * i) : 0.f;
+      const float x1 = qv ? ld(a.q, a.q_dtype, qb + 2 * i + 1) : 0.f;
+      const h2_t hi = {(_Float16)x0, (_Float16)x1};
+      w.qn[i] = h2u(hi);
+      if constexpr (QLO) {
+        const h2_t lo = {(_Float16)(x0 - (float)hi[0]), (_Float16)(x1 - (float)hi[1])};
+        w.ql[i] = h2u(lo);
+      }
     }
   }
 #pragma unroll
-  for (int j = 0; j < Wave<D>::CPM; ++j) w.acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < W::CPM; ++j) w.acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
   w.m_run = -__builtin_inff();
   w.l_lane = 0.f;
   w.bias = 0.f;
@@ -308,16 +340,16 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
       const int grp = t0 / L.KG;
       const bool in_res = rgrp == grp;
       if (!in_res && (blk != qk_blk || grp != qk_grp || bits != qk_bits)) {
-        if (bits == 4) build_qk<D, 4>(w, a.pages, L, blk, grp, h, c);
-        else if (bits == 8) build_qk<D, 8>(w, a.pages, L, blk, grp, h, c);
-        else build_qk<D, 2>(w, a.pages, L, blk, grp, h, c);
+        if (bits == 4) build_qk<D, QLO, 4>(w, a.pages, L, blk, grp, h, c);
+        else if (bits == 8) build_qk<D, QLO, 8>(w, a.pages, L, blk, grp, h, c);
+        else build_qk<D, QLO, 2>(w, a.pages, L, blk, grp, h, c);
         qk_blk = blk;
         qk_grp = grp;
         qk_bits = bits;
       }
-      if (bits == 4) tile<D, 4>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
-      else if (bits == 8) tile<D, 8>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
-      else tile<D, 2>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
+      if (bits == 4) tile<D, QLO, 4>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
+      else if (bits == 8) tile<D, QLO, 8>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
+      else tile<D, QLO, 2>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
     }
   }
 
@@ -333,7 +365,7 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int j = 0; j < Wave<D>::CPM; ++j) dst[(4 * c + i) * Wave<D>::CPM + j] = w.acc[j][i];
+      for (int j = 0; j < W::CPM; ++j) dst[(4 * c + i) * W::CPM + j] = w.acc[j][i];
     }
     if (c == 0) {
       a.ml[row * 2] = w.m_run;
@@ -341,8 +373,6 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
     }
   }
 }
-
-// Merge of one (sequence, query head)'s splits in split order.
 
 __global__ __launch_bounds__(64) void merge_kernel(MergeArgs a) {
   const long seq = blockIdx.x;
@@ -372,9 +402,16 @@ hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
   const int hpw = a.L.H < 8 ? a.L.H : 8;
   const dim3 grid((unsigned)a.num_splits, (unsigned)num_seqs, (unsigned)((a.L.H + hpw - 1) / hpw));
   const dim3 block(64 * hpw);
-  if (a.L.D == 128) hipLaunchKernelGGL(decode_kernel<128>, grid, block, 0, s, a);
-  else if (a.L.D == 64) hipLaunchKernelGGL(decode_kernel<64>, grid, block, 0, s, a);
-  else return hipErrorInvalidValue;
+  const bool qlo = a.q_dtype == ECHOKV_F32;
+  if (a.L.D == 128) {
+    if (qlo) hipLaunchKernelGGL((decode_kernel<128, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((decode_kernel<128, false>), grid, block, 0, s, a);
+  } else if (a.L.D == 64) {
+    if (qlo) hipLaunchKernelGGL((decode_kernel<64, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((decode_kernel<64, false>), grid, block, 0, s, a);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

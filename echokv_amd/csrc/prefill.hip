@@ -3,9 +3,10 @@
 // One workgroup (4 waves) per (query tile, KV head). A tile holds up to
 // 128 / GQA query tokens; its rows are (token, GQA head) pairs, 128 rows, 32
 // per wave (two 16-row blocks). The context is walked in 32-key tiles: the
-// workgroup dequantizes each key tile once into LDS as fp16 -- K row-major,
-// V transposed -- and every wave then runs, per 16-row block,
-//   S^T[key, row] = K Q^T         (v_mfma_f32_16x16x32_f16, 2 x D/32 per block)
+// workgroup dequantizes each key tile once into LDS -- K row-major as an fp16
+// hi + lo pair (exact to ~2^-22), V transposed in fp16 -- and every wave then
+// runs, per 16-row block,
+//   S^T[key, row] = K Q^T         (v_mfma_f32_16x16x32_f16 on K hi and K lo)
 //   O^T[d, row]  += V^T P^T       (v_mfma_f32_16x16x32_f16, D/16 per block)
 // with a per-row online softmax and the bottom-right causal limit
 // key <= query position (echokv_vllm/kernels/prefill.py:210-236 semantics).
@@ -24,14 +25,15 @@ constexpr int kVPad = 8;            // fp16 padding per V^T row
 __device__ __forceinline__ h2_t u2h_(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 }  // namespace
 
-template <int D>
+template <int D, bool QLO>
 __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   constexpr int KS = D + kKPad;       // K tile row stride (halves)
   constexpr int VS = kKeys + kVPad;   // V^T row stride (halves)
   constexpr int NQK = D / 32;
   constexpr int NPV = D / 16;
-  __shared__ _Float16 kt[kKeys * KS];
-  __shared__ _Float16 vt[D * VS];
+  __shared__ __attribute__((aligned(16))) _Float16 kt[kKeys * KS];   // K, fp16 hi part
+  __shared__ __attribute__((aligned(16))) _Float16 ktl[kKeys * KS];  // K, fp16 lo part
+  __shared__ __attribute__((aligned(16))) _Float16 vt[D * VS];
 
   const Lay& L = a.L;
   const int tile = blockIdx.x;
@@ -47,7 +49,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 
   // Query fragments (B operand of S^T): row = 32*wave + 16*rb + n, channels
   // 32j + 8c .. +8 in natural order.
-  h8_t qf[2][NQK];
+  h8_t qf[2][NQK], qfl[2][QLO ? NQK : 1];
   int qpos[2];
   bool rvalid[2];
 #pragma unroll
@@ -61,8 +63,11 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        qf[rb][j][e] = rvalid[rb] ? (_Float16)ld(a.q, a.q_dtype, qb + 32 * j + 8 * c + e) : (_Float16)0.f;
+      for (int e = 0; e < 8; ++e) {
+        const float x = rvalid[rb] ? ld(a.q, a.q_dtype, qb + 32 * j + 8 * c + e) : 0.f;
+        qf[rb][j][e] = (_Float16)x;
+        if constexpr (QLO) qfl[rb][j][e] = (_Float16)(x - (float)qf[rb][j][e]);
+      }
     }
   }
   f4_t acc[2][NPV];
@@ -127,7 +132,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
       }
 #pragma unroll
       for (int e = 0; e < CPT; ++e) {
-        kt[dt * KS + dcb * CPT + e] = (_Float16)kx[e];
+        const _Float16 khi = (_Float16)kx[e];
+        kt[dt * KS + dcb * CPT + e] = khi;
+        ktl[dt * KS + dcb * CPT + e] = (_Float16)(kx[e] - (float)khi);
         vt[(dcb * CPT + e) * VS + dt] = (_Float16)vx[e];
       }
     }
@@ -142,7 +149,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int j = 0; j < NQK; ++j) {
           const h8_t kf = *(const h8_t*)&kt[(16 * kh + n) * KS + 32 * j + 8 * c];
+          const h8_t kl = *(const h8_t*)&ktl[(16 * kh + n) * KS + 32 * j + 8 * c];
           s[kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[rb][j], s[kh], 0, 0, 0);
+          s[kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qf[rb][j], s[kh], 0, 0, 0);
+          if constexpr (QLO) s[kh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qfl[rb][j], s[kh], 0, 0, 0);
         }
       }
       float p[8];
@@ -205,9 +215,16 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 
 hipError_t launch_prefill(const PrefillArgs& a, long n_tiles, hipStream_t s) {
   const dim3 grid((unsigned)n_tiles, (unsigned)a.L.H);
-  if (a.L.D == 128) hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(256), 0, s, a);
-  else if (a.L.D == 64) hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(256), 0, s, a);
-  else return hipErrorInvalidValue;
+  const bool qlo = a.q_dtype == ECHOKV_F32;
+  if (a.L.D == 128) {
+    if (qlo) hipLaunchKernelGGL((prefill_kernel<128, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((prefill_kernel<128, false>), grid, dim3(256), 0, s, a);
+  } else if (a.L.D == 64) {
+    if (qlo) hipLaunchKernelGGL((prefill_kernel<64, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((prefill_kernel<64, false>), grid, dim3(256), 0, s, a);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -36,6 +36,8 @@ def write_tokens(store, key: torch.Tensor, value: torch.Tensor, meta, kref: torc
     if kref is not None:
         if kref.dtype != torch.float32 or kref.stride(2) != 1:
             raise ValueError("the K_ref ring must be float32 with contiguous rows")
+        if kref.shape[0] < store.planner.kref_window:
+            raise ValueError(f"the K_ref ring has {kref.shape[0]} rows, the planner writes {store.planner.kref_window}")
     res = _lib.residual(store.res_k)
     _lib.call(
         "echokv_write_tokens", _lib.byref(store.abi), _lib.ptr(store.pages),
@@ -52,7 +54,7 @@ def finalize_k(store, key: torch.Tensor, meta, full_grid: bool = False) -> None:
     ``full_grid`` launches one program per token row, masked on the device by
     ``meta.fin_count`` (a captured graph does not know the count)."""
     n = meta.n_rows if full_grid else meta.n_fin
-    if n == 0:
+    if n == 0 or meta.fin.shape[0] == 0:  # no rows staged: the device count is 0 too
         return
     _lib.require_device(key, store.pages)
     key = _kv(key)

@@ -27,11 +27,16 @@ def attend(q, k, v, scale, limit=None):
     return np.einsum("hn,nhd->hd", p, vv)
 
 
-def decode_attention(store, query, block_table, seq_lens, scale):
-    """decode.py:95-129: float ``[S, Hq, D]``."""
+def decode_attention(store, query, block_table, seq_lens, scale, vectorized=False):
+    """decode.py:95-129: float ``[S, Hq, D]``. ``vectorized`` reads the cache with the
+    store's vectorized gather (same values)."""
     out = np.zeros(query.shape, np.float64)
     for i, n in enumerate(np.asarray(seq_lens).tolist()):
-        k, v = store.gather_seq(block_table[i], n)
+        if vectorized:
+            pos = np.arange(n)
+            k, v = store.gather_vec(np.asarray(block_table[i], np.int64)[pos // store.L.bs], pos % store.L.bs)
+        else:
+            k, v = store.gather_seq(block_table[i], n)
         out[i] = attend(query[i], k, v, scale)
     return out
 

@@ -268,3 +268,46 @@ class PageStore:
         """K, V ``[n, H, D]`` of one sequence's first ``n`` tokens through its block-table row."""
         pos = np.arange(n)
         return self.gather(np.asarray(table_row, np.int64)[pos // self.L.bs], pos % self.L.bs)
+
+    def gather_vec(self, blk, off):
+        """``gather`` vectorized over tokens (numpy fancy indexing per tier); the same
+        values, used where the per-token loop is too slow (the CPU baseline)."""
+        L, o = self.L, self.L.offsets
+        blk = np.asarray(blk, np.int64).reshape(-1)
+        off = np.asarray(off, np.int64).reshape(-1)
+        n = blk.size
+        k_out = np.zeros((n, L.h, L.d), np.float32)
+        v_out = np.zeros((n, L.h, L.d), np.float32)
+        tags = self.pages[blk, 0].astype(np.int64)
+        slot = self.block_res[blk]
+        in_res = (slot >= 0) & (self.res_group[np.maximum(slot, 0)] == off // L.kg)
+        for bits in Q.SUPPORTED_BITS:
+            m = np.flatnonzero(tags == bits)
+            if not m.size:
+                continue
+            b, t = blk[m], off[m]
+            tpc = L.tokens_per_chunk(bits)
+            j = t // tpc
+            ids = self.pages[b, 4:16].copy().view(np.int32)[np.arange(m.size), np.maximum(j - 1, 0)].astype(np.int64)
+            page = np.where(j > 0, ids // L.kc, b)
+            cslot = np.where(j > 0, ids % L.kc, 0)
+            sb = L.side_bytes(bits)
+            base = o["data"] + cslot * L.chunk_bytes + (t % tpc) * 2 * sb
+            cols = np.arange(sb)
+            kraw = self.pages[page[:, None], base[:, None] + cols]
+            vraw = self.pages[page[:, None], base[:, None] + sb + cols]
+            kc = Q.unpack(kraw.reshape(m.size, L.h, -1), bits)
+            vc = Q.unpack(vraw.reshape(m.size, L.h, -1), bits)
+            ng = L.h * L.g
+            vs = self.pages[b[:, None], o["v_scale"] + (t * ng * 2)[:, None] + np.arange(2 * ng)].copy().view(np.float16)
+            vm = self.pages[b[:, None], o["v_min"] + (t * ng * 2)[:, None] + np.arange(2 * ng)].copy().view(np.float16)
+            v_out[m] = Q.dequantize(vc, vs.reshape(m.size, L.h, L.g), vm.reshape(m.size, L.h, L.g), L.vg)
+            nk = L.h * L.d
+            g = t // L.kg
+            ks = self.pages[b[:, None], o["k_scale"] + (g * nk * 2)[:, None] + np.arange(2 * nk)].copy().view(np.float16)
+            km = self.pages[b[:, None], o["k_min"] + (g * nk * 2)[:, None] + np.arange(2 * nk)].copy().view(np.float16)
+            k_out[m] = Q.dequantize_with(kc, ks.reshape(m.size, L.h, L.d), km.reshape(m.size, L.h, L.d))
+        r = np.flatnonzero(in_res & np.isin(tags, Q.SUPPORTED_BITS))
+        if r.size:
+            k_out[r] = self.res_k[slot[r], off[r] % L.kg].astype(np.float32)
+        return k_out, v_out

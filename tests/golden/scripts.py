@@ -188,3 +188,46 @@ def cfg1_prefill(s: Script):
         row += PREFILL_CHUNK
     q = np.random.default_rng(s.seed + 9).standard_normal((row, 32, s.d), dtype=np.float32)
     return prefill, req_of, q
+
+
+def case_script(name, h, d, bs, mem, lens, plan, seed=0, kg=32, vg=32, dtype="f32", extra_blocks=3):
+    """A store filled like the reference's decode-test fixture
+    (``tests/echokv_vllm/test_decode_kernel.py:21-48``): sequences over a seeded
+    block permutation, written block by block with sequences interleaved, block
+    ``bi`` of sequence ``s`` opened at ``plan[(bi + s) % len(plan)]``; K channel 1
+    carries a +30 outlier."""
+    rng = np.random.default_rng(seed + 500)
+    nbs = [-(-n // bs) for n in lens]
+    num_blocks = sum(nbs) + extra_blocks
+    perm = rng.permutation(num_blocks)
+    table = np.zeros((len(lens), max(nbs)), np.int64)
+    o = 0
+    for i, nb in enumerate(nbs):
+        table[i, :nb] = perm[o : o + nb]
+        o += nb
+    steps = []
+    for bi in range(max(nbs)):
+        for si, n in enumerate(lens):
+            lo, hi = bi * bs, min((bi + 1) * bs, n)
+            if lo >= hi:
+                continue
+            steps.append((table[si, bi] * bs + np.arange(hi - lo, dtype=np.int64), plan[(bi + si) % len(plan)]))
+    s = Script(name, h, d, bs, mem, kg, vg, num_blocks, len(lens) + 2, steps, seed=seed, dtype=dtype,
+               outliers=((1, 30.0),), full_bytes=False)
+    s.meta = {"table": table, "lens": np.array(lens, np.int64)}
+    return s
+
+
+DECODE_CASES = [
+    # name, h, d, bs, mem_bits, seq lens, tier plan, k_group
+    ("dec_h2_d64_bs64", 2, 64, 64, 8, [1, 40, 64, 65, 200], [8, 4, 2], 32),
+    ("dec_h1_d128_bs32_pool", 1, 128, 32, 4, [33, 97, 128], [8, 8, 4], 32),
+    ("dec_h4_d64_mem6", 4, 64, 64, 6, [500, 3], [2, 4], 32),
+    ("dec_h8_d128_bs64", 8, 128, 64, 8, [200, 70], [8, 4, 2], 32),
+    ("dec_h8_d128_bs16_kg16", 8, 128, 16, 8, [300, 17, 1, 129], [4, 8, 2], 16),
+]
+
+
+def decode_case(i, seed=1, dtype="f32"):
+    name, h, d, bs, mem, lens, plan, kg = DECODE_CASES[i]
+    return case_script(f"{name}_s{seed}", h, d, bs, mem, lens, plan, seed=seed, kg=kg, dtype=dtype)

@@ -1,0 +1,40 @@
+"""GPU: the canary KL kernel against the reference's own outputs and the float64
+oracle; batched layers equal per-layer calls (test_step_path.py:87-97)."""
+
+import numpy as np
+import pytest
+import torch
+
+import scripts as S
+from echokv_amd.canary import canary_kl
+from oracle import canary as OC
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(got, ref, rtol=2e-3, atol=2e-6):
+    got = got.cpu().numpy().astype(np.float64)
+    np.testing.assert_allclose(got, ref, rtol=rtol, atol=atol)
+
+
+def test_canary_matches_reference_outputs(device):
+    g = np.load(S.__file__.replace("scripts.py", "canary.npz"))
+    (q, kref), (q2, kref2) = S.canary_inputs()
+    got = canary_kl(torch.from_numpy(q).to(device), torch.from_numpy(kref).to(device), (2, 4, 8), 32, 64 ** -0.5)
+    _close(got, g["small_out"])
+    got2 = canary_kl(torch.from_numpy(q2).to(device), torch.from_numpy(kref2).to(device), (2, 4, 8), 16,
+                     128 ** -0.5)
+    _close(got2, g["cfg_out"])
+    _close(got2, OC.canary_kl(q2.astype(np.float32), kref2, (2, 4, 8), 16, 128 ** -0.5))
+
+
+def test_canary_batched_equals_per_layer_and_monotone(device):
+    (q, kref), _ = S.canary_inputs()
+    qd, kd = torch.from_numpy(q).to(device), torch.from_numpy(kref).to(device)
+    batched = canary_kl(qd, kd, (2, 4, 8), 32, 64 ** -0.5)
+    each = torch.stack([canary_kl(qd[i], kd[i], (2, 4, 8), 32, 64 ** -0.5) for i in range(3)])
+    torch.testing.assert_close(batched, each, rtol=1e-6, atol=1e-7)
+    d = batched.cpu().numpy()
+    assert (d[:, 0] > d[:, 1]).all() and (d[:, 1] > d[:, 2]).all() and (d >= 0).all()
+    low = canary_kl(qd.bfloat16(), kd, (2, 4, 8), 32, 64 ** -0.5)
+    assert low.dtype == torch.float32 and low.shape == (3, 3)

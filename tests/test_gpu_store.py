@@ -1,0 +1,108 @@
+"""GPU: the HIP write path (write_tokens, finalize_k, seal, demotion) stores the
+reference's exact page bytes for every golden script; the graph-style padded,
+full-grid step stores the same bytes as plain writes; gather reads back the
+reference's dequantized values bit for bit."""
+
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+import scripts as S
+from gpu_util import gpu_replay, gpu_store
+from host_sim import golden
+
+pytestmark = pytest.mark.gpu
+
+NAMES = [s.name for s in S.all_scripts()]
+
+
+def _script(name):
+    return next(s for s in S.all_scripts() if s.name == name)
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_hip_write_path_matches_reference_bytes(device, name):
+    print(f"[store] {name}", flush=True)
+    s = _script(name)
+    g = golden(name)
+    store, backing, stride, page, kref = gpu_replay(s, device)
+    pages = store.pages.cpu().numpy()
+    if s.full_bytes:
+        bad = np.flatnonzero((pages != g["pages"]).any(axis=1))
+        assert bad.size == 0, f"pages {bad.tolist()} differ"
+        raw = backing.cpu().numpy()
+        for b in range(s.num_blocks):  # nothing written past a page (0xAB guard)
+            assert (raw[b * stride + page : (b + 1) * stride] == 0xAB).all()
+    else:
+        got = np.array([hashlib.sha256(pages[b].tobytes()).hexdigest() for b in range(s.num_blocks)])
+        bad = np.flatnonzero(got != g["page_sha"])
+        assert bad.size == 0, f"pages {bad.tolist()} differ"
+    np.testing.assert_array_equal(store.block_res.cpu().numpy(), g["block_res"])
+    np.testing.assert_array_equal(store.res_group.cpu().numpy(), g["res_group"])
+    live = store.block_res[store.block_res >= 0]
+    np.testing.assert_array_equal(store.res_k[live].cpu().numpy(), g["res_live"])
+    if kref is not None:
+        np.testing.assert_array_equal(kref.cpu().numpy(), g["kref"])
+    tw = store.tokens_written
+    counters = [tw[2], tw[4], tw[8], *(store.blocks_opened[b] for b in (2, 4, 8)), store.downgraded_blocks,
+                store.demoted_blocks, store.sealed_groups, store.pool_free, store.residual_free]
+    np.testing.assert_array_equal(np.array(counters), g["counters"])
+
+
+def test_gather_reads_reference_values(device):
+    s = _script("cfg1_int4_bs16")
+    g = golden(s.name)
+    store, *_ = gpu_replay(s, device)
+    pos = torch.arange(64, device=device)
+    table = torch.from_numpy(s.meta["table"]).to(device)
+    k, v = store.gather(table[0][pos // s.bs], pos % s.bs)
+    np.testing.assert_array_equal(k.cpu().numpy(), g["gather0_k"])
+    np.testing.assert_array_equal(v.cpu().numpy(), g["gather0_v"])
+
+
+def test_padded_full_grid_step_matches_plain_write(device):
+    """As a captured decode graph runs the step (reference test_step_path.py:35-71):
+    3 padding rows (slot -1, garbage K/V) and a full-grid finalize masked by the
+    device count store exactly the plain writes' bytes; the K_ref ring too."""
+    from echokv_amd.write_plan import stage_plan
+
+    s = _script("step_path")
+    plain, *_ = gpu_replay(s, device)
+    graph, *_ = gpu_store(s, device)
+    kr = torch.zeros(s.kref_window, s.h, s.d, device=device)
+    gen = torch.Generator().manual_seed(0)
+    for slots, bits, k, v in S.script_inputs(s):
+        n = slots.size
+        kp = torch.cat([torch.from_numpy(k), torch.randn(3, s.h, s.d, generator=gen) * 1e3]).to(device)
+        vp = torch.cat([torch.from_numpy(v), torch.randn(3, s.h, s.d, generator=gen) * 1e3]).to(device)
+        padded = torch.cat([torch.from_numpy(slots), torch.full((3,), -1, dtype=torch.int64)])
+        plan = graph.planner.plan(padded)
+        opened = graph.prepare(plan, bits)
+        graph.shared.commit(plan)
+        meta, extra = stage_plan(plan, device, opened)
+        graph.shared.apply_res_map(*extra[:4])
+        if opened is not None:
+            graph.write_headers(extra[4], extra[5])
+        graph.apply(meta, kp, vp, kref=kr, capturing=True)
+        assert n + 3 == meta.n_rows
+    torch.cuda.synchronize()
+    assert torch.equal(plain.pages, graph.pages)
+    assert torch.equal(plain.block_res, graph.block_res)
+    live = plain.block_res[plain.block_res >= 0]
+    assert live.numel() and torch.equal(plain.res_k[live], graph.res_k[live])
+    np.testing.assert_array_equal(kr.cpu().numpy(), golden("step_path")["kref"])
+
+
+def test_decode_cases_store_oracle_bytes(device):
+    """The decode-case stores (bf16-free, mixed tiers, pool pressure) written on the
+    GPU equal the CPU oracle replay byte for byte."""
+    from host_sim import replay
+
+    for i in range(len(S.DECODE_CASES)):
+        s = S.decode_case(i)
+        sim = replay(s)
+        store, *_ = gpu_replay(s, device)
+        bad = np.flatnonzero((store.pages.cpu().numpy() != sim.ps.pages).any(axis=1))
+        assert bad.size == 0, f"{s.name}: pages {bad.tolist()} differ"

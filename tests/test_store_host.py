@@ -119,3 +119,15 @@ def test_triton_interpreter_bytes_agree():
     assert tri, "empty Triton hash record"
     for name, h in tri.items():
         assert h["triton_pages_sha"] == man[name]["pages_sha"], name
+
+
+@pytest.mark.parametrize("name", ["tier_change", "eviction_seal", "cfg1_int4_bs16", "pool_exhaustion"])
+def test_vectorized_gather_equals_loop(sims, name):
+    sim = _sim(sims, name)
+    rng = np.random.default_rng(0)
+    blk = rng.integers(0, sim.ps.n, 300)
+    off = rng.integers(0, sim.s.bs, 300)
+    k1, v1 = sim.ps.gather(blk, off)
+    k2, v2 = sim.ps.gather_vec(blk, off)
+    np.testing.assert_array_equal(k1, k2)
+    np.testing.assert_array_equal(v1, v2)
