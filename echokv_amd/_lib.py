@@ -53,8 +53,8 @@ _SIGS = {
     "echokv_seal_groups": [LP, P, P, I64, RP, P],
     "echokv_gather": [LP, P, P, P, RP, P, P, I64, P, P, P],
     "echokv_store_blocks": [LP, P, P, I64, P, P, I32, P],
-    "echokv_decode": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, P, P, P, I64, I64,
-                      I32, P],
+    "echokv_decode": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, P, P, P, I64,
+                      I64, I32, P],
     "echokv_prefill": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, I32, P, I64, FL, P],
     "echokv_dequant_dense": [LP, P, P, P, RP, P, I64, P, I64, P, P, I64, I64, I32, P],
     "echokv_canary_kl": [P, I32, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32, I32, I32, I32, I32, I32, FL, P, P],

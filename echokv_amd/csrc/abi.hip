@@ -126,8 +126,8 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
                   const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
                   int32_t num_q_heads, const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
                   const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs, float softmax_scale,
-                  int32_t num_splits, int32_t blocks_per_split, float* acc, float* ml, void* out, int64_t o_s0,
-                  int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
+                  int32_t num_splits, int32_t blocks_per_split, int32_t tier, float* acc, float* ml, void* out,
+                  int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;
   if (L->head_size != 64 && L->head_size != 128) return ECHOKV_ESHAPE;
   if ((L->head_size / 16) % 1 || L->v_group % (L->head_size / 16)) return ECHOKV_ESHAPE;
@@ -136,6 +136,7 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
   if (gqa > 16) return ECHOKV_ESHAPE;
   if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
   if (num_seqs < 0 || num_splits <= 0 || blocks_per_split <= 0 || !res_ok(res)) return ECHOKV_EINVAL;
+  if (tier != 2 && tier != 4 && tier != 8) return ECHOKV_EINVAL;
   if (num_seqs == 0) return ECHOKV_OK;
   if (!pages || !block_res || !res_group || !query || !block_table || !seq_lens || !acc || !ml || !out)
     return ECHOKV_EINVAL;
@@ -159,6 +160,15 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.num_splits = num_splits;
   a.bps = blocks_per_split;
+  a.tier = tier;
+  if ((L->block_size & (L->block_size - 1)) || (L->k_group & (L->k_group - 1)) || L->chunks_per_page > 4)
+    return ECHOKV_ESHAPE;
+  a.bs_shift = __builtin_ctz((unsigned)L->block_size);
+  a.kg_shift = __builtin_ctz((unsigned)L->k_group);
+  a.vg_shift = __builtin_ctz((unsigned)L->v_group);
+  // ceil(2^32 / KC) is exact for chunk ids < 2^24 (fractions of id / KC are multiples of 1 / KC >= 1/4).
+  a.kc_mul = L->chunks_per_page == 1 ? 0u : (uint32_t)((0x100000000ull + L->chunks_per_page - 1) / L->chunks_per_page);
+  if (L->num_blocks * L->chunks_per_page >= (1LL << 24)) return ECHOKV_ESHAPE;
   a.acc = acc;
   a.ml = ml;
   hipError_t e = ek::launch_decode(a, num_seqs, (hipStream_t)stream);

@@ -115,14 +115,20 @@ struct Wave {
   float m_run, l_lane;
 };
 
+// q * k_scale (hi / lo) fragments and the k_min bias of one K group, from the
+// lane's CPL channels of k_scale at ksp and of k_min at kmp (global or LDS).
+// Lanes of padding query columns (`active` false) hold zeros and skip the reads.
 template <int D, bool QLO, int BITS>
-__device__ __forceinline__ void build_qk(Wave<D, QLO>& w, const uint8_t* pages, const Lay& L, long blk, int grp,
-                                         int h, int c) {
+__device__ __forceinline__ void build_qk_at(Wave<D, QLO>& w, const uint8_t* ksp, const uint8_t* kmp, bool active) {
   constexpr int CPL = Wave<D, QLO>::CPL;
-  const long e0 = ((long)grp * L.H + h) * D + c * CPL;
   uint32_t ks[CPL / 2], km[CPL / 2];
-  load_bytes<2 * CPL>(pages + blk * L.stride + L.o_ks + 2 * e0, ks);
-  load_bytes<2 * CPL>(pages + blk * L.stride + L.o_km + 2 * e0, km);
+  if (active) {
+    load_bytes<2 * CPL>(ksp, ks);
+    load_bytes<2 * CPL>(kmp, km);
+  } else {
+#pragma unroll
+    for (int i = 0; i < CPL / 2; ++i) ks[i] = km[i] = 0;
+  }
   float b = 0.f;
   uint32_t hi[CPL / 2], lo[CPL / 2];
 #pragma unroll
@@ -146,6 +152,14 @@ __device__ __forceinline__ void build_qk(Wave<D, QLO>& w, const uint8_t* pages, 
   b += __shfl_xor(b, 16, 64);
   b += __shfl_xor(b, 32, 64);
   w.bias = b;
+}
+
+template <int D, bool QLO, int BITS>
+__device__ __forceinline__ void build_qk(Wave<D, QLO>& w, const uint8_t* pages, const Lay& L, long blk, int grp,
+                                         int h, int c, bool active) {
+  const long e0 = ((long)grp * L.H + h) * D + c * Wave<D, QLO>::CPL;
+  build_qk_at<D, QLO, BITS>(w, pages + blk * L.stride + L.o_ks + 2 * e0, pages + blk * L.stride + L.o_km + 2 * e0,
+                            active);
 }
 
 // Online-softmax update with the tile's S^T fragment (already scaled to log2
@@ -284,14 +298,238 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
   softmax_pv<D, QLO>(w, s, va);
 }
 
-template <int D, bool QLO>
+// ---------------------------------------------------------------------------
+// Tier-specialised pipelined path. Each wave streams its KV head's tiles of the
+// split through an NBUF-slot ring in LDS, filled by direct global->LDS DMA
+// (global_load_lds_dword{,x4}: lane L's bytes land at slot + size * L), so the
+// bytes in flight per CU are set by the ring size, not by VGPRs. The DMAs are
+// issued from inline asm: the compiler neither sees them nor inserts waits for
+// them; the wave waits with an explicit s_waitcnt vmcnt(n) for the tile it is
+// about to read (loads retire in order, so waiting for "at most n outstanding"
+// covers every older load). Every tile issues the same number of DMA
+// instructions (a tile the fast path does not take -- the open K group, a block
+// of another tier -- loads a dummy 16 bytes per lane from its page header), so
+// n is a compile-time count.
+// ---------------------------------------------------------------------------
+#pragma clang diagnostic ignored "-Winline-asm"
+
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int D, int BITS>
+struct Ring {
+  static constexpr int KB = D * BITS / 8;                 // code bytes per token, one side, one head
+  static constexpr int KCB = 16 * KB;                     // per tile
+  static constexpr int KI = (KCB / 16 + 63) / 64;         // dwordx4 DMAs per side
+  static constexpr int OFF_V = KCB, OFF_S = 2 * KCB;      // K codes | V codes | k_scale, k_min | V stats
+  static constexpr int OFF_VS = 2 * KCB + 4 * D;
+  static constexpr int SLOT = OFF_VS + 16 * 4 * 4;        // V stats for G <= 4 groups
+  static constexpr int NBUF = BITS == 8 ? 3 : 4;
+  static constexpr int M = 2 * KI + 2;                    // DMA instructions per tile
+  static constexpr int WAVE_BYTES = NBUF * SLOT;
+};
+
+// Per-block facts of the split's next <= 64 blocks, one block per lane: chunk
+// byte offsets (chunk 0 is the block's own page), tier and residual mapping.
+struct BlockLane {
+  long cb0, cb1, cb2, cb3;
+  int blk;    // -1: not a valid block id
+  int tier;
+  int fast;   // stored at the kernel's tier with every chunk it needs in range
+  int rslot, rgrp;
+};
+
+__device__ __forceinline__ long mul32(long a, long b) { return (long)((uint64_t)(uint32_t)a * (uint32_t)b); }
+
+template <int BITS>
+__device__ __forceinline__ BlockLane load_block(const DecodeArgs& a, long blk) {
+  const Lay& L = a.L;
+  BlockLane b{0, 0, 0, 0, -1, 2, 0, -1, -1};
+  if (blk < 0 || blk >= L.nb) return b;
+  const long pg = mul32(blk, L.stride);
+  const uint4 hd = *(const uint4*)(a.pages + pg);
+  b.blk = (int)blk;
+  b.tier = tier_of(hd.x & 0xffu);
+  b.cb0 = pg + L.o_data;
+  const uint32_t ids[3] = {hd.y, hd.z, hd.w};
+  long cbs[3];
+  bool ok = true;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const uint32_t id = ids[j];
+    const uint32_t page = a.kc_mul ? __umulhi(id, a.kc_mul) : id;
+    const uint32_t slot = id - page * (uint32_t)L.KC;
+    const bool in = (int)id >= 0 && (long)page < L.nb;
+    cbs[j] = in ? mul32(page, L.stride) + L.o_data + mul32(slot, L.cb) : b.cb0;
+    if (j < (BITS == 8 ? 3 : (BITS == 4 ? 1 : 0))) ok = ok && in;
+  }
+  b.cb1 = cbs[0];
+  b.cb2 = cbs[1];
+  b.cb3 = cbs[2];
+  b.fast = ok && b.tier == BITS;
+  const long rs = a.block_res[blk];
+  if (rs >= 0 && rs < a.res.rows) {
+    b.rslot = (int)rs;
+    b.rgrp = (int)a.res_group[rs];
+  }
+  return b;
+}
+
+__device__ __forceinline__ long readlane64(long v, int lane) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, lane);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), lane);
+  return (long)(((uint64_t)hi << 32) | lo);
+}
+
+// DMA one tile (16 tokens from block offset t0) of head h into ring slot `slot`;
+// a non-fast tile issues the same number of DMAs, each lane 0 copying 4 header bytes.
+template <int D, int BITS>
+__device__ __forceinline__ void issue_tile(const DecodeArgs& a, uint32_t slot, bool fast, int t0, int h, int lane,
+                                           long cb0, long cb1, long cb2, long cb3) {
+  using R = Ring<D, BITS>;
+  const Lay& L = a.L;
+  const uint8_t* page = a.pages + (cb0 - L.o_data);
+  if (!fast) {
+#pragma unroll
+    for (int i = 0; i < R::M; ++i) {
+      if (lane == 0) dma4(page, slot);
+    }
+    return;
+  }
+  constexpr int LB = BITS == 8 ? 3 : (BITS == 4 ? 2 : 1);
+  const int tpc_shift = a.bs_shift + 1 - LB;  // tokens per chunk = 2 * BS / BITS
+  constexpr long ROWB = 2L * D * BITS / 8;     // per head; a row holds all heads
+  const long rowb = ROWB * L.H;
+  const long side = rowb / 2;
+  const long headb = (long)h * R::KB;
+  constexpr int QPT = R::KB / 16;
+#pragma unroll
+  for (int r = 0; r < R::KI; ++r) {
+    const int idx = lane + 64 * r;
+    const int t = t0 + idx / QPT;
+    const int j = t >> tpc_shift;
+    long cb = cb0;
+    if constexpr (BITS >= 4) cb = j == 1 ? cb1 : cb;
+    if constexpr (BITS == 8) cb = j == 2 ? cb2 : (j == 3 ? cb3 : cb);
+    const uint8_t* src = a.pages + cb + (long)(t & ((1 << tpc_shift) - 1)) * rowb + headb + 16 * (idx % QPT);
+    if (idx < R::KCB / 16) {
+      dma16(src, slot + 1024 * r);
+      dma16(src + side, slot + R::OFF_V + 1024 * r);
+    }
+  }
+  {  // k_scale / k_min of the tile's K group: D/8 lanes each
+    const long e0 = (long)((t0 >> a.kg_shift) * L.H + h) * D * 2;
+    const uint8_t* src = lane < D / 8 ? page + L.o_ks + e0 + 16 * lane : page + L.o_km + e0 + 16 * (lane - D / 8);
+    if (lane < D / 4) dma16(src, slot + R::OFF_S);
+  }
+  {  // V scale / min: G halves per token each, moved as G/2 dwords
+    const int G = D >> a.vg_shift;
+    const int sp = G == 4 ? 1 : 0;  // log2(dwords per token per stat)
+    const int which = lane >> (4 + sp);
+    const int r = lane & ((16 << sp) - 1);
+    const int t = t0 + (r >> sp);
+    const uint8_t* src = page + (which ? L.o_vm : L.o_vs) + (long)(t * L.H + h) * G * 2 + 4 * (r & ((1 << sp) - 1));
+    if (lane < (32 << sp)) dma4(src, slot + R::OFF_VS);
+  }
+}
+
+// One fast tile from LDS slot `sp` (tier BITS, K from codes).
+template <int D, bool QLO, int BITS>
+__device__ __forceinline__ void compute_tile(Wave<D, QLO>& w, const DecodeArgs& a, const uint8_t* sp, int t0,
+                                             int n_valid, bool new_group, int lane) {
+  using W = Wave<D, QLO>;
+  using R = Ring<D, BITS>;
+  constexpr int CPL = W::CPL, NQK = W::NQK, CPM = W::CPM;
+  const int c = lane >> 4, n = lane & 15;
+  if (new_group)
+    build_qk_at<D, QLO, BITS>(w, sp + R::OFF_S + 2 * c * CPL, sp + R::OFF_S + 2 * D + 2 * c * CPL, n < a.gqa);
+  f4_t s = {0.f, 0.f, 0.f, 0.f};
+  {
+    constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
+    uint32_t kw[KW];
+    load_bytes<CPL * BITS / 8>(sp + n * R::KB + c * (CPL * BITS / 8), kw);
+#pragma unroll
+    for (int j = 0; j < NQK; ++j) {
+      uint32_t wj[2];
+      if constexpr (BITS == 8) {
+        wj[0] = kw[2 * j];
+        wj[1] = kw[2 * j + 1];
+      } else if constexpr (BITS == 4) {
+        wj[0] = kw[j];
+      } else {
+        wj[0] = kw[j >> 1] >> (16 * (j & 1));
+      }
+      const h8_t kf = unpack8<BITS>(wj);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, w.qk[j], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, w.qkl[j], s, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = (t0 + 4 * c + i < n_valid) ? (s[i] + w.bias) * a.scale_log2 : -__builtin_inff();
+
+  constexpr int VB = CPM * BITS / 8;
+  constexpr int VW = VB >= 4 ? VB / 4 : 1;
+  uint32_t vw[4][VW];
+  const int G = D >> a.vg_shift;
+  const int g = (n * CPM) >> a.vg_shift;
+  const _Float16* vs = (const _Float16*)(sp + R::OFF_VS);
+  _Float16 sv[4], mv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tv = 4 * c + i;
+    load_bytes<VB>(sp + R::OFF_V + tv * R::KB + n * VB, vw[i]);
+    const bool ok = t0 + tv < n_valid;
+    sv[i] = ok ? vs[tv * G + g] : (_Float16)0.f;
+    mv[i] = ok ? vs[16 * G + tv * G + g] : (_Float16)0.f;
+  }
+  const h2_t s01 = {sv[0], sv[1]}, s23 = {sv[2], sv[3]};
+  const h2_t m01 = {mv[0], mv[1]}, m23 = {mv[2], mv[3]};
+  h4_t va[CPM];
+#pragma unroll
+  for (int j = 0; j < CPM; ++j) {
+    constexpr int PER = 8 / BITS;
+    const int byte = j / PER, sh = (j % PER) * BITS;
+    const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + (byte & 3)) << 16) | (uint32_t)(byte & 3);
+    const int wd = byte >> 2;
+    const uint32_t mask = ((1u << BITS) - 1u) * 0x00010001u;
+    const uint32_t x01 = (__builtin_amdgcn_perm(vw[1][wd], vw[0][wd], sel) >> sh) & mask;
+    const uint32_t x23 = (__builtin_amdgcn_perm(vw[3][wd], vw[2][wd], sel) >> sh) & mask;
+    const h2_t v01 = __builtin_elementwise_fma(code_pair(x01), s01, m01);
+    const h2_t v23 = __builtin_elementwise_fma(code_pair(x23), s23, m23);
+    va[j] = h4_t{v01[0], v01[1], v23[0], v23[1]};
+  }
+  softmax_pv<D, QLO>(w, s, va);
+}
+
+template <int D, int BITS, int NB>
+__device__ __forceinline__ void wait_tile(int ahead) {
+  // `ahead` tiles were issued after the one about to be read.
+  constexpr int M = Ring<D, BITS>::M;
+  if (NB >= 4 && ahead >= 3) wait_vmcnt<3 * M>();
+  else if (ahead >= 2) wait_vmcnt<2 * M>();
+  else if (ahead == 1) wait_vmcnt<M>();
+  else wait_vmcnt<0>();
+}
+
+template <int D, int BITS, bool QLO>
 __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
   using W = Wave<D, QLO>;
+  using R = Ring<D, BITS>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
   const Lay& L = a.L;
   const int split = blockIdx.x;
   const long seq = blockIdx.y;
   const int lane = threadIdx.x & 63;
-  const int h = blockIdx.z * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int wv = threadIdx.x >> 6;
+  const int h = blockIdx.z * (blockDim.x >> 6) + wv;
   if (h >= L.H) return;
   const int seq_len = (int)a.lens[seq];
   if (seq_len <= 0) return;
@@ -304,6 +542,8 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
   const long q_row = a.q_rows ? a.q_rows[seq] : seq;
   const long bt_row = a.bt_rows ? a.bt_rows[seq] : seq;
   const int c = lane >> 4, n = lane & 15;
+  uint8_t* my_ring = ring_lds + wv * R::WAVE_BYTES;
+  const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)my_ring);
 
   W w;
   {
@@ -327,33 +567,69 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
   w.l_lane = 0.f;
   w.bias = 0.f;
 
-  long qk_blk = -1;
-  int qk_grp = -1, qk_bits = 0;
-  for (int bi = b_start; bi < b_end; ++bi) {
-    const long blk = a.bt[bt_row * a.bt_s0 + bi];
-    if (blk < 0 || blk >= L.nb) continue;
-    const int bits = tier_of(a.pages[blk * L.stride]);
-    const long rslot = a.block_res[blk];
-    const long rgrp = (rslot >= 0 && rslot < a.res.rows) ? a.res_group[rslot] : -1;
-    const int n_valid = seq_len - bi * L.BS;
-    for (int t0 = 0; t0 < L.BS && t0 < n_valid; t0 += 16) {
-      const int grp = t0 / L.KG;
-      const bool in_res = rgrp == grp;
-      if (!in_res && (blk != qk_blk || grp != qk_grp || bits != qk_bits)) {
-        if (bits == 4) build_qk<D, QLO, 4>(w, a.pages, L, blk, grp, h, c);
-        else if (bits == 8) build_qk<D, QLO, 8>(w, a.pages, L, blk, grp, h, c);
-        else build_qk<D, QLO, 2>(w, a.pages, L, blk, grp, h, c);
+  const int tpb_shift = a.bs_shift - 4;  // tiles per block = BS / 16
+  const bool stats_ok = (D >> a.vg_shift) == 2 || (D >> a.vg_shift) == 4;
+  for (int c0 = b_start; c0 < b_end; c0 += 64) {
+    const int nb = b_end - c0 < 64 ? b_end - c0 : 64;
+    const BlockLane bl = load_block<BITS>(a, lane < nb ? (long)a.bt[bt_row * a.bt_s0 + c0 + lane] : -1L);
+    const int last_tok = (c0 + nb) * L.BS < seq_len ? (c0 + nb) * L.BS : seq_len;
+    const int n_tiles = (last_tok - c0 * L.BS + 15) >> 4;
+
+    auto issue = [&](int tt) {
+      const int b = tt >> tpb_shift;
+      const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
+      const bool fast = __builtin_amdgcn_readlane(bl.fast, b) && __builtin_amdgcn_readlane(bl.rgrp, b) != (t0 >> a.kg_shift) && stats_ok;
+      const long cb0 = readlane64(bl.cb0, b);
+      const long cb1 = BITS >= 4 ? readlane64(bl.cb1, b) : cb0;
+      const long cb2 = BITS == 8 ? readlane64(bl.cb2, b) : cb0;
+      const long cb3 = BITS == 8 ? readlane64(bl.cb3, b) : cb0;
+      const uint32_t slot = ring0 + (uint32_t)((tt % R::NBUF) * R::SLOT);
+      issue_tile<D, BITS>(a, slot, fast, t0, h, lane, cb0, cb1, cb2, cb3);
+    };
+
+#pragma unroll 1
+    for (int tt = 0; tt < R::NBUF - 1 && tt < n_tiles; ++tt) issue(tt);
+    long qk_blk = -1;
+    int qk_grp = -1, qk_bits = 0;
+#pragma unroll 1
+    for (int tt = 0; tt < n_tiles; ++tt) {
+      if (tt + R::NBUF - 1 < n_tiles) issue(tt + R::NBUF - 1);
+      const int ahead = (n_tiles - 1 - tt) < (R::NBUF - 1) ? (n_tiles - 1 - tt) : (R::NBUF - 1);
+      const int b = tt >> tpb_shift;
+      const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
+      const long blk = __builtin_amdgcn_readlane(bl.blk, b);
+      if (blk < 0) continue;
+      const int grp = t0 >> a.kg_shift;
+      const int rgrp = __builtin_amdgcn_readlane(bl.rgrp, b);
+      const bool fast = __builtin_amdgcn_readlane(bl.fast, b) && rgrp != grp && stats_ok;
+      const int n_valid = seq_len - ((c0 + b) << a.bs_shift);
+      if (fast) {
+        wait_tile<D, BITS, R::NBUF>(ahead);
+        const bool new_group = blk != qk_blk || grp != qk_grp || qk_bits != BITS;
+        compute_tile<D, QLO, BITS>(w, a, my_ring + (tt % R::NBUF) * R::SLOT, t0, n_valid, new_group, lane);
         qk_blk = blk;
         qk_grp = grp;
-        qk_bits = bits;
+        qk_bits = BITS;
+      } else {
+        const int tier = __builtin_amdgcn_readlane(bl.tier, b);
+        const long rslot = __builtin_amdgcn_readlane(bl.rslot, b);
+        const bool in_res = rslot >= 0 && rgrp == grp;
+        if (!in_res && (blk != qk_blk || grp != qk_grp || tier != qk_bits)) {
+          if (tier == 4) build_qk<D, QLO, 4>(w, a.pages, L, blk, grp, h, c, n < a.gqa);
+          else if (tier == 8) build_qk<D, QLO, 8>(w, a.pages, L, blk, grp, h, c, n < a.gqa);
+          else build_qk<D, QLO, 2>(w, a.pages, L, blk, grp, h, c, n < a.gqa);
+          qk_blk = blk;
+          qk_grp = grp;
+          qk_bits = tier;
+        }
+        if (tier == 4) tile<D, QLO, 4>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
+        else if (tier == 8) tile<D, QLO, 8>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
+        else tile<D, QLO, 2>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
       }
-      if (bits == 4) tile<D, QLO, 4>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
-      else if (bits == 8) tile<D, QLO, 8>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
-      else tile<D, QLO, 2>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
     }
+    wait_vmcnt<0>();  // nothing of this chunk may still be landing in the ring
   }
 
-  // Row sums live per lane (4 tokens each); reduce across the 4 lane groups.
   float l = w.l_lane;
   l += __shfl_xor(l, 16, 64);
   l += __shfl_xor(l, 32, 64);
@@ -361,7 +637,6 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
     const long qh = (long)h * a.gqa + n;
     const long row = (seq * a.hq + qh) * a.num_splits + split;
     float* dst = a.acc + row * D;
-    // lane holds channels (4c + i) * CPM + j
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -398,21 +673,35 @@ __global__ __launch_bounds__(64) void merge_kernel(MergeArgs a) {
   }
 }
 
+template <int D, int BITS, bool QLO>
+hipError_t launch_decode_t(const DecodeArgs& a, dim3 grid, dim3 block, hipStream_t s) {
+  const size_t lds = (size_t)(block.x / 64) * Ring<D, BITS>::WAVE_BYTES;
+  static bool attr = false;  // idempotent; set once per instantiation
+  if (!attr) {
+    if (hipFuncSetAttribute((const void*)decode_kernel<D, BITS, QLO>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return hipErrorInvalidValue;
+    attr = true;
+  }
+  hipLaunchKernelGGL((decode_kernel<D, BITS, QLO>), grid, block, lds, s, a);
+  return hipGetLastError();
+}
+
+template <int D, bool QLO>
+hipError_t launch_decode_d(const DecodeArgs& a, dim3 grid, dim3 block, hipStream_t s) {
+  if (a.tier == 8) return launch_decode_t<D, 8, QLO>(a, grid, block, s);
+  if (a.tier == 2) return launch_decode_t<D, 2, QLO>(a, grid, block, s);
+  return launch_decode_t<D, 4, QLO>(a, grid, block, s);
+}
+
 hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
   const int hpw = a.L.H < 8 ? a.L.H : 8;
   const dim3 grid((unsigned)a.num_splits, (unsigned)num_seqs, (unsigned)((a.L.H + hpw - 1) / hpw));
   const dim3 block(64 * hpw);
   const bool qlo = a.q_dtype == ECHOKV_F32;
-  if (a.L.D == 128) {
-    if (qlo) hipLaunchKernelGGL((decode_kernel<128, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((decode_kernel<128, false>), grid, block, 0, s, a);
-  } else if (a.L.D == 64) {
-    if (qlo) hipLaunchKernelGGL((decode_kernel<64, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((decode_kernel<64, false>), grid, block, 0, s, a);
-  } else {
-    return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  if (a.L.D == 128) return qlo ? launch_decode_d<128, true>(a, grid, block, s) : launch_decode_d<128, false>(a, grid, block, s);
+  if (a.L.D == 64) return qlo ? launch_decode_d<64, true>(a, grid, block, s) : launch_decode_d<64, false>(a, grid, block, s);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s) {

@@ -45,6 +45,7 @@ def decode_attention(
     max_len: int | None = None,
     num_splits: int | None = None,
     workspace: tuple[torch.Tensor, torch.Tensor] | None = None,
+    tier: int | None = None,
 ) -> torch.Tensor:
     """Attention of one query token per sequence over each sequence's cache.
 
@@ -54,6 +55,9 @@ def decode_attention(
     writes sequence ``i`` to ``out[q_rows[i]]`` in ``out``'s dtype; length-0
     sequences (graph padding) leave their row untouched. ``workspace`` =
     caller-owned ``(acc [S, Hq, splits, D], ml [S, Hq, splits, 2])`` float32.
+    ``tier`` selects the kernel specialised for the layer's tier (the backend passes
+    the layer controller's tier); by default the store's most common opened tier.
+    Blocks of other tiers are read correctly either way.
     """
     L = store.layout
     dev = query.device
@@ -80,13 +84,15 @@ def decode_attention(
         acc, ml = workspace
         if acc.numel() < s * hq * num_splits * d or ml.numel() < s * hq * num_splits * 2:
             raise ValueError("decode workspace is too small for this batch and split grid")
+    if tier is None:
+        tier = store.pool.majority_tier()
     res = _lib.residual(store.res_k)
     _lib.call(
         "echokv_decode", _lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(store.block_res),
         _lib.ptr(store.res_group), _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1),
         _lib.dtype_code(query), hq, _lib.ptr(q_rows), _lib.ptr(block_table), block_table.stride(0),
         _lib.ptr(bt_rows), _lib.ptr(lens), s, float(softmax_scale), int(num_splits), int(blocks_per_split),
-        _lib.ptr(acc), _lib.ptr(ml), _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out),
+        int(tier), _lib.ptr(acc), _lib.ptr(ml), _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out),
         _lib.stream(),
     )
     return out

@@ -215,6 +215,12 @@ class ChunkPool:
         mask = planner.sealed.get(ev.block, 1 << ev.group)
         return [ev.slot, ev.block, ev.group, ev.fill, bits, mask]
 
+    def majority_tier(self) -> int:
+        """The tier most of the opened blocks are stored at (4 when nothing is open)."""
+        counts = np.bincount(self.tag_h, minlength=9)
+        best = max(SUPPORTED_BITS, key=lambda b: (counts[b], b == 4))
+        return best if counts[best] else 4
+
     def fresh_opens(self, plan: WritePlan) -> np.ndarray:
         """Blocks to open this step: offset-0 writes plus writes into never-opened blocks."""
         opens = plan.open_np

@@ -99,7 +99,9 @@ int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* b
  * tokens and writes out[q_rows[i]]; seq_lens[i] == 0 leaves the row untouched.
  * Split size = max(blocks_per_split, ceil(blocks / num_splits)) of the sequence's own
  * length (batch invariant). acc: [num_seqs, Hq, num_splits, D] f32, ml:
- * [num_seqs, Hq, num_splits, 2] f32 workspaces.
+ * [num_seqs, Hq, num_splits, 2] f32 workspaces. tier (2, 4 or 8) selects the kernel
+ * specialised for the layer's tier; blocks stored at another tier, and each block's
+ * open K group, are still read correctly on a slower path.
  * Replaces echokv_vllm/kernels/decode.py:44-92 (decode_attention) with its kernels
  * decode.py:135-224 (_decode_kernel) and decode.py:227-262 (_merge_kernel). */
 int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
@@ -107,7 +109,7 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
                   const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype, int32_t num_q_heads,
                   const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
                   const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs,
-                  float softmax_scale, int32_t num_splits, int32_t blocks_per_split,
+                  float softmax_scale, int32_t num_splits, int32_t blocks_per_split, int32_t tier,
                   float* acc, float* ml, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
                   echokv_stream_t stream);
 
