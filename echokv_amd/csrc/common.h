@@ -56,6 +56,26 @@ __device__ __forceinline__ void ld4(const void* p, int dtype, long i, float x[4]
   for (int e = 0; e < 4; ++e) x[e] = ld(p, dtype, i + e);
 }
 
+// N consecutive elements starting at element i. The dtype branch sits outside
+// the element loop, so the N loads issue back to back and the wave waits once
+// (a branch per element would wait for each load before issuing the next).
+template <int N>
+__device__ __forceinline__ void ld_n(const void* p, int dtype, long i, float* x) {
+  if (dtype == ECHOKV_F16) {
+    const _Float16* s = (const _Float16*)p + i;
+#pragma unroll
+    for (int e = 0; e < N; ++e) x[e] = (float)s[e];
+  } else if (dtype == ECHOKV_BF16) {
+    const uint16_t* s = (const uint16_t*)p + i;
+#pragma unroll
+    for (int e = 0; e < N; ++e) x[e] = bf16_to_f32(s[e]);
+  } else {
+    const float* s = (const float*)p + i;
+#pragma unroll
+    for (int e = 0; e < N; ++e) x[e] = s[e];
+  }
+}
+
 // ---- tiers and addressing ------------------------------------------------
 // A block's tier from its header tag: 4 and 8 as stored; 0 (never opened)
 // and anything else are addressed as INT2, which stays inside the own page.

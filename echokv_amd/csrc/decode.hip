@@ -204,12 +204,19 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
   if (in_res) {
     const long r0 = rslot * a.res.s0 + (long)(tk % L.KG) * a.res.s1 + h * a.res.s2 + c * CPL;
     const bool res_lo = a.res.dtype == ECHOKV_F32;  // fp16 / bf16 keys are exact in fp16
+    float xr[CPL];
+    if (kvalid) {
+      ld_n<CPL>(a.res.ptr, a.res.dtype, r0, xr);
+    } else {
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) xr[e] = 0.f;
+    }
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
       h8_t kh, kl;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = kvalid ? ld(a.res.ptr, a.res.dtype, r0 + 8 * j + e) : 0.f;
+        const float x = xr[8 * j + e];
         kh[e] = (_Float16)x;
         kl[e] = (_Float16)(x - (float)kh[e]);
       }
@@ -343,16 +350,22 @@ struct BlockLane {
   long cb0, cb1, cb2, cb3;
   int blk;    // -1: not a valid block id
   int tier;
-  int fast;   // stored at the kernel's tier with every chunk it needs in range
+  // kNotFast unless the block is stored at the kernel's tier with every chunk it
+  // needs in range; else the K group read from the residual (-1: none), whose
+  // tile takes the generic path. Derived from the loads (not a loaded register
+  // itself), so the compiler waits for them once, before the tile loop, rather
+  // than with a vmcnt(0) -- which would drain the DMA ring -- at a use inside it.
+  int fast_rg;
   int rslot, rgrp;
 };
+constexpr int kNotFast = -0x7fffffff;
 
 __device__ __forceinline__ long mul32(long a, long b) { return (long)((uint64_t)(uint32_t)a * (uint32_t)b); }
 
 template <int BITS>
 __device__ __forceinline__ BlockLane load_block(const DecodeArgs& a, long blk) {
   const Lay& L = a.L;
-  BlockLane b{0, 0, 0, 0, -1, 2, 0, -1, -1};
+  BlockLane b{0, 0, 0, 0, -1, 2, kNotFast, -1, -1};
   if (blk < 0 || blk >= L.nb) return b;
   const long pg = mul32(blk, L.stride);
   const uint4 hd = *(const uint4*)(a.pages + pg);
@@ -374,12 +387,12 @@ __device__ __forceinline__ BlockLane load_block(const DecodeArgs& a, long blk) {
   b.cb1 = cbs[0];
   b.cb2 = cbs[1];
   b.cb3 = cbs[2];
-  b.fast = ok && b.tier == BITS;
   const long rs = a.block_res[blk];
   if (rs >= 0 && rs < a.res.rows) {
     b.rslot = (int)rs;
     b.rgrp = (int)a.res_group[rs];
   }
+  b.fast_rg = ok && b.tier == BITS ? (b.rgrp < 0 ? -1 : b.rgrp) : kNotFast;
   return b;
 }
 
@@ -549,10 +562,16 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
   {
     const bool qv = n < a.gqa;
     const long qb = q_row * a.q_s0 + (long)(h * a.gqa + (qv ? n : 0)) * a.q_s1 + c * W::CPL;
+    float xq[W::CPL];
+    if (qv) {
+      ld_n<W::CPL>(a.q, a.q_dtype, qb, xq);
+    } else {
+#pragma unroll
+      for (int e = 0; e < W::CPL; ++e) xq[e] = 0.f;
+    }
 #pragma unroll
     for (int i = 0; i < W::CPL / 2; ++i) {
-      const float x0 = qv ? ld(a.q, a.q_dtype, qb + 2 * i) : 0.f;
-      const float x1 = qv ? ld(a.q, a.q_dtype, qb + 2 * i + 1) : 0.f;
+      const float x0 = xq[2 * i], x1 = xq[2 * i + 1];
       const h2_t hi = {(_Float16)x0, (_Float16)x1};
       w.qn[i] = h2u(hi);
       if constexpr (QLO) {
@@ -578,7 +597,8 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
     auto issue = [&](int tt) {
       const int b = tt >> tpb_shift;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
-      const bool fast = __builtin_amdgcn_readlane(bl.fast, b) && __builtin_amdgcn_readlane(bl.rgrp, b) != (t0 >> a.kg_shift) && stats_ok;
+      const int frg = __builtin_amdgcn_readlane(bl.fast_rg, b);
+      const bool fast = frg != kNotFast && frg != (t0 >> a.kg_shift) && stats_ok;
       const long cb0 = readlane64(bl.cb0, b);
       const long cb1 = BITS >= 4 ? readlane64(bl.cb1, b) : cb0;
       const long cb2 = BITS == 8 ? readlane64(bl.cb2, b) : cb0;
@@ -600,8 +620,8 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
       const long blk = __builtin_amdgcn_readlane(bl.blk, b);
       if (blk < 0) continue;
       const int grp = t0 >> a.kg_shift;
-      const int rgrp = __builtin_amdgcn_readlane(bl.rgrp, b);
-      const bool fast = __builtin_amdgcn_readlane(bl.fast, b) && rgrp != grp && stats_ok;
+      const int frg = __builtin_amdgcn_readlane(bl.fast_rg, b);
+      const bool fast = frg != kNotFast && frg != grp && stats_ok;
       const int n_valid = seq_len - ((c0 + b) << a.bs_shift);
       if (fast) {
         wait_tile<D, BITS, R::NBUF>(ahead);
@@ -612,6 +632,7 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
         qk_bits = BITS;
       } else {
         const int tier = __builtin_amdgcn_readlane(bl.tier, b);
+        const int rgrp = __builtin_amdgcn_readlane(bl.rgrp, b);
         const long rslot = __builtin_amdgcn_readlane(bl.rslot, b);
         const bool in_res = rslot >= 0 && rgrp == grp;
         if (!in_res && (blk != qk_blk || grp != qk_grp || tier != qk_bits)) {

@@ -1,0 +1,77 @@
+"""CPU: the C-ABI library loads and exports every entry point ``include/echokv.h``
+declares, and its host-side argument checks reject bad input before any launch
+(no GPU needed: nothing below reaches a kernel)."""
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from echokv_amd import _lib
+from echokv_amd.tiered_cache import TieredLayout
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "echokv.h"
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(echokv_[a-z_0-9]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} is not built: run python -c 'import __graft_entry__ as g; g.build()'")
+    return _lib.lib()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.EXPORTS)
+    assert set(_lib._SIGS) == set(names) - {"echokv_error_string"}
+
+
+def test_error_strings(lib):
+    for code in range(5):
+        assert lib.echokv_error_string(code)
+    assert lib.echokv_error_string(0) != lib.echokv_error_string(1)
+
+
+def _layout(**kw):
+    lay = TieredLayout(8, 128, 16, 8, 16, 32)
+    L = lay.abi(100, lay.page_bytes)
+    for k, v in kw.items():
+        setattr(L, k, v)
+    return L
+
+
+def _decode(lib, L, tier=4, splits=4, seqs=1):
+    res = _lib.Residual(C.c_void_p(16), 1, 2, 16 * 8 * 128, 8 * 128, 128)
+    p = C.c_void_p(64)  # never dereferenced: every call below fails its checks first
+    return lib.echokv_decode(C.byref(L), p, p, p, C.byref(res), p, 4096, 128, 1, 32, None, p, 64, None, p, seqs,
+                             0.088, splits, 16, tier, p, p, p, 4096, 128, 1, None)
+
+
+def test_decode_rejects_bad_arguments_before_launching(lib):
+    assert _decode(lib, _layout(head_size=96)) == 2          # D must be 64 or 128
+    assert _decode(lib, _layout(block_size=24)) == 2         # block not a multiple of 16
+    assert _decode(lib, _layout(block_size=48, k_group=16)) == 2  # decode needs a power-of-2 block
+    assert _decode(lib, _layout(), tier=3) != 0
+    assert _decode(lib, _layout(), splits=0) != 0
+    assert _decode(lib, _layout(), seqs=-1) != 0
+    assert _decode(lib, _layout(), seqs=0) == 0              # nothing to do: no launch
+
+
+def test_store_entry_points_reject_bad_layouts(lib):
+    L = _layout(chunk_bytes=12345)
+    p = C.c_void_p(64)
+    res = _lib.Residual(C.c_void_p(16), 1, 2, 16 * 8 * 128, 8 * 128, 128)
+    rc = lib.echokv_write_tokens(C.byref(L), p, p, 1024, 128, p, 1024, 128, 1, p, 64, 4, C.byref(res), None, 0, 0,
+                                 None)
+    assert rc == 2
+    rc = lib.echokv_store_blocks(C.byref(_layout()), p, p, 1, p, p, 3, None)
+    assert rc != 0  # bits must be 2, 4 or 8
