@@ -169,12 +169,14 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
   // ceil(2^32 / KC) is exact for chunk ids < 2^24 (fractions of id / KC are multiples of 1 / KC >= 1/4).
   a.kc_mul = L->chunks_per_page == 1 ? 0u : (uint32_t)((0x100000000ull + L->chunks_per_page - 1) / L->chunks_per_page);
   if (L->num_blocks * L->chunks_per_page >= (1LL << 24)) return ECHOKV_ESHAPE;
+  // The kernel addresses the layer's pages with 32-bit byte offsets.
+  if (L->num_blocks * L->page_stride > 0xFFFFFFFFLL) return ECHOKV_ESHAPE;
   a.acc = acc;
   a.ml = ml;
   hipError_t e = ek::launch_decode(a, num_seqs, (hipStream_t)stream);
   if (e != hipSuccess) return ECHOKV_ELAUNCH;
   ek::MergeArgs m{acc, ml, seq_lens, q_rows, out, o_s0, o_s1, out_dtype, num_q_heads, L->head_size,
-                  L->block_size, num_splits, blocks_per_split};
+                  L->block_size, num_splits, blocks_per_split, num_seqs * num_q_heads};
   return launched(ek::launch_merge(m, num_seqs, (hipStream_t)stream));
 }
 

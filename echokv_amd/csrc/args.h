@@ -116,6 +116,7 @@ struct MergeArgs {
   void* out;
   long o_s0, o_s1;
   int out_dtype, hq, D, BS, num_splits, bps;
+  long rows;  // num_seqs * hq
 };
 
 struct CanaryArgs {

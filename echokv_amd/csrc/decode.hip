@@ -1,6 +1,6 @@
 // Split-KV paged decode attention over the tiered (INT2/INT4/INT8) pages, gfx950.
 //
-// Work decomposition: one workgroup per (sequence, split, group of <= 8 KV
+// Work decomposition: one workgroup per (split, sequence, group of <= 4 KV
 // heads), one 64-wide wave per KV head. The heads of a token row sit side by
 // side in a page ([K codes of all heads | V codes of all heads]), so the waves
 // of a workgroup read neighbouring slices of the same cache lines together.
@@ -14,65 +14,125 @@
 //                 to fp16 in registers with its per-token fp16 scale / min)
 // Codes are exact in fp16. The query-side operand (q * k_scale, and the residual
 // keys) is carried as an fp16 hi + lo pair -- lo = fma(q, s, -hi) rounded once --
-// and contracted twice, so S is accurate to ~2^-22 instead of fp16's 2^-11:
-// keys with large outlier channels would otherwise dominate the error.
-// The S^T accumulator layout (lane = 4 tokens x 1 query column) is exactly the
-// B-operand layout of the second MFMA, and the O^T accumulator keeps one query
-// column per lane, so the online softmax runs per lane with two cross-lane
-// max reductions per tile. Query columns are the GQA heads of the KV head,
-// padded to 16. Codes become fp16 by OR-ing them under the exponent of 1024
-// (0x6400) and subtracting 1024 (exact).
+// and contracted in two MFMA chains, so S is accurate to ~2^-22 instead of fp16's
+// 2^-11: keys with large outlier channels would otherwise dominate the error.
+// Lane (c, n) = (lane / 16, lane % 16) of the S^T product holds token n and
+// channels [c * D/4, (c+1) * D/4) in natural order; the S^T accumulator layout
+// (lane = 4 tokens x 1 query column) is exactly the B-operand layout of the
+// second MFMA, and the O^T accumulator keeps one query column per lane, so the
+// online softmax runs per lane with two cross-row max reductions per tile
+// (v_permlane16_swap / v_permlane32_swap). Query columns are the GQA heads of
+// the KV head, padded to 16. Codes become fp16 by placing them under the
+// exponent of 1024 (0x6400) and subtracting 1024 (exact); v_perm_b32 picks the
+// byte of each code pair, the low nibble of a pre-shifted copy gives odd codes.
+// The running max is rescaled lazily: only when some column's max grows by more
+// than 2^8 (probabilities stay <= 256, far inside fp16).
 //
 // A split covers max(blocks_per_split, ceil(blocks / num_splits)) blocks of
 // the sequence's own length, so results do not depend on the rest of the
-// batch; a second kernel merges the splits in order (log-sum-exp).
+// batch; a second kernel merges the splits in order (log-sum-exp, log2 units).
 #include "args.h"
 
 namespace ek {
 
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ h2_t u2h(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 __device__ __forceinline__ uint32_t h2u(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ h8_t w2h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_bit_cast(h8_t, u4_t{a, b, c, d});
+}
 
-// 0x6400 = fp16 1024.0; (1024 + c) - 1024 is exact for codes c < 1024.
-__device__ __forceinline__ h2_t code_pair(uint32_t bits16x2) {
+constexpr float kLazyRescale = 8.0f;  // log2 units
+// KV heads (waves) per workgroup: 4 lets two or three workgroups share a CU, so
+// one's start-up (query, block table and header loads) overlaps another's tiles.
+constexpr int kHeadsPerGroup = 4;
+
+// v_perm_b32 selector: byte `a` of the low source to bits 0-7, byte `b` of the
+// high source to bits 16-23, zeros elsewhere (perm(hi, lo, sel)).
+constexpr uint32_t pair_sel(int a, int b) { return 0x0C000C00u | ((uint32_t)(4 + b) << 16) | (uint32_t)a; }
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// (x & mask) holds two codes at bits 0.. and 16..; as fp16 (1024 + c) - 1024, exact.
+__device__ __forceinline__ h2_t code_pair(uint32_t x, uint32_t mask) {
   const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-  return u2h(bits16x2 | 0x64006400u) - k1024;
+  return u2h((x & mask) | 0x64006400u) - k1024;
 }
 
-__device__ __forceinline__ h8_t cat8(h2_t a, h2_t b, h2_t c, h2_t d) {
-  return h8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-// Eight channels (e0..e7, natural order) of a K row as an MFMA fragment in the
-// tier's pair order: INT4 / INT2 give (e0,e4),(e1,e5),(e2,e6),(e3,e7); INT8 gives
-// (e0,e2),(e1,e3),(e4,e6),(e5,e7). The query side uses the same order.
+// Eight consecutive channels of a K row, natural order, as an MFMA fragment.
+// INT4: one word (8 nibbles); INT8: two words; INT2: bytes 2*hf, 2*hf+1 of one word.
 template <int BITS>
-__device__ __forceinline__ h8_t unpack8(const uint32_t* w) {
+__device__ __forceinline__ h8_t kfrag(const uint32_t* w, int hf) {
   if constexpr (BITS == 4) {
-    const uint32_t x = w[0];
-    return cat8(code_pair(x & 0x000F000Fu), code_pair((x >> 4) & 0x000F000Fu), code_pair((x >> 8) & 0x000F000Fu),
-                code_pair((x >> 12) & 0x000F000Fu));
+    const uint32_t x = w[0], x4 = x >> 4;
+    return w2h8(h2u(code_pair(perm(x4, x, pair_sel(0, 0)), 0x000F000Fu)),
+                h2u(code_pair(perm(x4, x, pair_sel(1, 1)), 0x000F000Fu)),
+                h2u(code_pair(perm(x4, x, pair_sel(2, 2)), 0x000F000Fu)),
+                h2u(code_pair(perm(x4, x, pair_sel(3, 3)), 0x000F000Fu)));
   } else if constexpr (BITS == 8) {
-    const uint32_t x = w[0], y = w[1];
-    return cat8(code_pair(x & 0x00FF00FFu), code_pair((x >> 8) & 0x00FF00FFu), code_pair(y & 0x00FF00FFu),
-                code_pair((y >> 8) & 0x00FF00FFu));
+    const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const uint32_t m = 0x64646464u;  // perm(m, x, ...) puts 0x64 above each code byte
+    return w2h8(h2u(u2h(perm(m, w[0], 0x04010400u)) - k1024), h2u(u2h(perm(m, w[0], 0x04030402u)) - k1024),
+                h2u(u2h(perm(m, w[1], 0x04010400u)) - k1024), h2u(u2h(perm(m, w[1], 0x04030402u)) - k1024));
   } else {
-    const uint32_t u = w[0] & 0xFFFFu;
-    const uint32_t x = (u & 0xFFu) | ((u & 0xFF00u) << 8);
-    return cat8(code_pair(x & 0x00030003u), code_pair((x >> 2) & 0x00030003u), code_pair((x >> 4) & 0x00030003u),
-                code_pair((x >> 6) & 0x00030003u));
+    const uint32_t x = w[0], x2 = x >> 2, x4 = x >> 4, x6 = x >> 6;
+    const int b0 = 2 * hf, b1 = 2 * hf + 1;
+    return w2h8(h2u(code_pair(perm(x2, x, pair_sel(b0, b0)), 0x00030003u)),
+                h2u(code_pair(perm(x6, x4, pair_sel(b0, b0)), 0x00030003u)),
+                h2u(code_pair(perm(x2, x, pair_sel(b1, b1)), 0x00030003u)),
+                h2u(code_pair(perm(x6, x4, pair_sel(b1, b1)), 0x00030003u)));
   }
 }
 
-// Natural pairs n[0..3] = (e0,e1),(e2,e3),(e4,e5),(e6,e7) -> the tier's order.
+// Fragment j (channels 8j..8j+7 of the lane's slice) from the lane's K words.
 template <int BITS>
-__device__ __forceinline__ h8_t reorder8(const uint32_t* n) {
-  if constexpr (BITS == 8) {
-    return cat8(u2h(__builtin_amdgcn_perm(n[1], n[0], 0x05040100u)), u2h(__builtin_amdgcn_perm(n[1], n[0], 0x07060302u)),
-                u2h(__builtin_amdgcn_perm(n[3], n[2], 0x05040100u)), u2h(__builtin_amdgcn_perm(n[3], n[2], 0x07060302u)));
+__device__ __forceinline__ h8_t kfrag_j(const uint32_t* kw, int j) {
+  if constexpr (BITS == 4) return kfrag<4>(kw + j, 0);
+  else if constexpr (BITS == 8) return kfrag<8>(kw + 2 * j, 0);
+  else return kfrag<2>(kw + (j >> 1), j & 1);
+}
+
+// V^T operand of the lane's channel j for its 4 tokens: v[i] = token i's slice
+// words, x4 / x2.. = pre-shifted copies; dequantized as c * s + m (one rounding).
+template <int BITS, int VW>
+__device__ __forceinline__ h4_t vfrag(int j, const uint32_t (*v)[VW], const uint32_t (*vs)[4], h2_t s01, h2_t s23,
+                                      h2_t m01, h2_t m23) {
+  uint32_t x01, x23, mask;
+  if constexpr (BITS == 4) {
+    const int by = j >> 1, sh = j & 1;  // odd channels: low nibble of the word >> 4
+    x01 = perm(vs[1][sh], vs[0][sh], pair_sel(by, by));
+    x23 = perm(vs[3][sh], vs[2][sh], pair_sel(by, by));
+    mask = 0x000F000Fu;
+  } else if constexpr (BITS == 8) {
+    const int wd = j >> 2, by = j & 3;
+    x01 = perm(v[1][wd], v[0][wd], pair_sel(by, by));
+    x23 = perm(v[3][wd], v[2][wd], pair_sel(by, by));
+    mask = 0x00FF00FFu;
   } else {
-    return cat8(u2h(__builtin_amdgcn_perm(n[2], n[0], 0x05040100u)), u2h(__builtin_amdgcn_perm(n[2], n[0], 0x07060302u)),
-                u2h(__builtin_amdgcn_perm(n[3], n[1], 0x05040100u)), u2h(__builtin_amdgcn_perm(n[3], n[1], 0x07060302u)));
+    const int by = j >> 2, sh = j & 3;  // code j at bits 2*sh of byte by
+    x01 = perm(vs[1][sh], vs[0][sh], pair_sel(by, by));
+    x23 = perm(vs[3][sh], vs[2][sh], pair_sel(by, by));
+    mask = 0x00030003u;
+  }
+  const h2_t v01 = __builtin_elementwise_fma(code_pair(x01, mask), s01, m01);
+  const h2_t v23 = __builtin_elementwise_fma(code_pair(x23, mask), s23, m23);
+  return h4_t{v01[0], v01[1], v23[0], v23[1]};
+}
+
+// Shifted copies of the V words that vfrag reads (INT4: >> 0, 4; INT2: >> 0, 2, 4, 6).
+template <int BITS, int VW>
+__device__ __forceinline__ void vshift(const uint32_t (*v)[VW], uint32_t (*vs)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    vs[i][0] = v[i][0];
+    if constexpr (BITS == 4) vs[i][1] = v[i][0] >> 4;
+    if constexpr (BITS == 2) {
+      vs[i][1] = v[i][0] >> 2;
+      vs[i][2] = v[i][0] >> 4;
+      vs[i][3] = v[i][0] >> 6;
+    }
   }
 }
 
@@ -101,41 +161,55 @@ __device__ __forceinline__ void load_bytes(const uint8_t* p, uint32_t* w) {
   }
 }
 
+// Cross-row (lanes l, l^16, l^32, l^48) reductions; every lane gets the result.
+__device__ __forceinline__ float rows_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
 // Per-wave decode state for head_dim D. QLO: the query has a low part (float32 input).
 template <int D, bool QLO>
 struct Wave {
   static constexpr int CPL = D / 4;   // K channels per lane in the QK fragments
-  static constexpr int NQK = D / 32;  // 16x16x32 MFMAs per tile for S^T (per hi / lo part)
+  static constexpr int NQK = D / 32;  // 16x16x32 MFMAs per tile for S^T (per hi / lo chain)
   static constexpr int CPM = D / 16;  // V channels per lane = 16x16x16 MFMAs per tile
   uint32_t qn[CPL / 2];               // fp16 query pairs (hi), natural channel order
   uint32_t ql[QLO ? CPL / 2 : 1];     // fp16 query pairs (lo = q - hi)
-  h8_t qk[NQK], qkl[NQK];             // q * k_scale (hi, lo) fragments, current K group
-  float bias;                         // sum_d q * k_min for the current K group
   f4_t acc[CPM];                      // O^T fragments
   float m_run, l_lane;
 };
 
-// q * k_scale (hi / lo) fragments and the k_min bias of one K group, from the
-// lane's CPL channels of k_scale at ksp and of k_min at kmp (global or LDS).
-// Lanes of padding query columns (`active` false) hold zeros and skip the reads.
-template <int D, bool QLO, int BITS>
-__device__ __forceinline__ void build_qk_at(Wave<D, QLO>& w, const uint8_t* ksp, const uint8_t* kmp, bool active) {
+// One K group's query-side operand: q * k_scale as fp16 hi / lo MFMA fragments
+// and scale_log2 * sum_d q * k_min (built per tile: a per-tile temporary keeps
+// it out of the registers that live across the tile loop).
+template <int D>
+struct QK {
+  h8_t hi[D / 32], lo[D / 32];
+  float bias_s;
+};
+
+// q * k_scale (hi / lo) fragments and the scaled k_min bias of one K group from
+// the lane's CPL channels of k_scale (ks) and k_min (km), natural order.
+template <int D, bool QLO>
+__device__ __forceinline__ void build_qk(QK<D>& qk, const Wave<D, QLO>& w, const uint32_t* ks, const uint32_t* km,
+                                         float scale_log2) {
   constexpr int CPL = Wave<D, QLO>::CPL;
-  uint32_t ks[CPL / 2], km[CPL / 2];
-  if (active) {
-    load_bytes<2 * CPL>(ksp, ks);
-    load_bytes<2 * CPL>(kmp, km);
-  } else {
-#pragma unroll
-    for (int i = 0; i < CPL / 2; ++i) ks[i] = km[i] = 0;
-  }
-  float b = 0.f;
+  float b0 = 0.f, b1 = 0.f;
   uint32_t hi[CPL / 2], lo[CPL / 2];
 #pragma unroll
   for (int i = 0; i < CPL / 2; ++i) {
     const h2_t q = u2h(w.qn[i]), s = u2h(ks[i]);
     const h2_t ph = q * s;
     h2_t pl = __builtin_elementwise_fma(q, s, -ph);  // exact product minus its rounding, rounded once
+    float& b = (i & 1) ? b1 : b0;
     b = __builtin_amdgcn_fdot2(q, u2h(km[i]), b, false);
     if constexpr (QLO) {
       pl = __builtin_elementwise_fma(u2h(w.ql[i]), s, pl);
@@ -146,44 +220,70 @@ __device__ __forceinline__ void build_qk_at(Wave<D, QLO>& w, const uint8_t* ksp,
   }
 #pragma unroll
   for (int j = 0; j < Wave<D, QLO>::NQK; ++j) {
-    w.qk[j] = reorder8<BITS>(hi + 4 * j);
-    w.qkl[j] = reorder8<BITS>(lo + 4 * j);
+    qk.hi[j] = w2h8(hi[4 * j], hi[4 * j + 1], hi[4 * j + 2], hi[4 * j + 3]);
+    qk.lo[j] = w2h8(lo[4 * j], lo[4 * j + 1], lo[4 * j + 2], lo[4 * j + 3]);
   }
-  b += __shfl_xor(b, 16, 64);
-  b += __shfl_xor(b, 32, 64);
-  w.bias = b;
+  qk.bias_s = rows_sum(b0 + b1) * scale_log2;
 }
 
-template <int D, bool QLO, int BITS>
-__device__ __forceinline__ void build_qk(Wave<D, QLO>& w, const uint8_t* pages, const Lay& L, long blk, int grp,
-                                         int h, int c, bool active) {
-  const long e0 = ((long)grp * L.H + h) * D + c * Wave<D, QLO>::CPL;
-  build_qk_at<D, QLO, BITS>(w, pages + blk * L.stride + L.o_ks + 2 * e0, pages + blk * L.stride + L.o_km + 2 * e0,
-                            active);
-}
-
-// Online-softmax update with the tile's S^T fragment (already scaled to log2
-// units and masked), then O^T += V^T P^T.
+// S^T of a tile whose keys are the block's open K group, read from the
+// full-precision residual (row = token % KG) and split into fp16 hi + lo
+// (fp16 / bf16 keys are exact in fp16: lo = 0 is skipped). Lane (c, n): token
+// t0 + n, channels [c * D/4, (c+1) * D/4), eight at a time.
 template <int D, bool QLO>
-__device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, f4_t s, const h4_t* va) {
-  float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-  mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-  mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+__device__ __forceinline__ void s_from_residual(const Wave<D, QLO>& w, const DecodeArgs& a, long rslot, int t0, int h,
+                                                int lane, f4_t& sh, f4_t& sl) {
+  constexpr int CPL = D / 4;
+  const int c = lane >> 4, n = lane & 15;
+  const long r0 = rslot * a.res.s0 + (long)((t0 + n) & (a.L.KG - 1)) * a.res.s1 + h * a.res.s2 + c * CPL;
+  const bool res_lo = a.res.dtype == ECHOKV_F32;
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) {
+    float xr[8];
+    ld_n<8>(a.res.ptr, a.res.dtype, r0 + 8 * j, xr);
+    h8_t kh, kl;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      kh[e] = (_Float16)xr[e];
+      kl[e] = (_Float16)(xr[e] - (float)kh[e]);
+    }
+    const h8_t qh = w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2], w.qn[4 * j + 3]);
+    sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh, sh, 0, 0, 0);
+    if (res_lo) sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh, sl, 0, 0, 0);
+    if constexpr (QLO) {
+      const h8_t ql = w2h8(w.ql[4 * j], w.ql[4 * j + 1], w.ql[4 * j + 2], w.ql[4 * j + 3]);
+      sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql, sl, 0, 0, 0);
+    }
+  }
+}
+
+// Online-softmax update with the tile's scores x (log2 units, masked), then O^T += V^T P^T.
+template <int D, bool QLO>
+__device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, const h4_t* va) {
+  const float mt = rows_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
   const float m_new = fmaxf(w.m_run, mt);
-  const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
+  if (__builtin_amdgcn_ballot_w64(m_new > w.m_run + kLazyRescale)) {
+    const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);  // m_run = -inf at the start: 0
+    w.l_lane *= alpha;
+#pragma unroll
+    for (int j = 0; j < Wave<D, QLO>::CPM; ++j) w.acc[j] *= alpha;
+    w.m_run = m_new;
+  }
   float p[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(s[i] - m_new);
-  w.l_lane = w.l_lane * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-  w.m_run = m_new;
+  for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(x[i] - w.m_run);
+  w.l_lane += (p[0] + p[1]) + (p[2] + p[3]);
   const h4_t pb = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
 #pragma unroll
-  for (int j = 0; j < Wave<D, QLO>::CPM; ++j) {
-    w.acc[j] *= alpha;
+  for (int j = 0; j < Wave<D, QLO>::CPM; ++j)
     w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j], pb, w.acc[j], 0, 0, 0);
-  }
 }
 
+// ---------------------------------------------------------------------------
+// Generic register path: a tile of a block stored at another tier than the
+// kernel's (or whose chunk table names a chunk out of range), including its
+// open K group. Rare: only blocks demoted or downgraded under pool pressure.
+// ---------------------------------------------------------------------------
 // One 16-token tile [t0, t0 + 16) of block `blk` (tier BITS); tokens >= n_valid
 // are masked. in_res: the tile is the block's open K group (K from the residual).
 template <int D, bool QLO, int BITS>
@@ -198,38 +298,21 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
   const long headb = (long)h * (D * BITS / 8);
 
   // ---- S^T = K Q'^T (+ bias) -------------------------------------------
-  f4_t s = {0.f, 0.f, 0.f, 0.f};
-  const int tk = t0 + n;
-  const bool kvalid = tk < n_valid;
+  f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
+  float bias_s = 0.f;
   if (in_res) {
-    const long r0 = rslot * a.res.s0 + (long)(tk % L.KG) * a.res.s1 + h * a.res.s2 + c * CPL;
-    const bool res_lo = a.res.dtype == ECHOKV_F32;  // fp16 / bf16 keys are exact in fp16
-    float xr[CPL];
-    if (kvalid) {
-      ld_n<CPL>(a.res.ptr, a.res.dtype, r0, xr);
-    } else {
-#pragma unroll
-      for (int e = 0; e < CPL; ++e) xr[e] = 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < NQK; ++j) {
-      h8_t kh, kl;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = xr[8 * j + e];
-        kh[e] = (_Float16)x;
-        kl[e] = (_Float16)(x - (float)kh[e]);
-      }
-      const h8_t qh = cat8(u2h(w.qn[4 * j]), u2h(w.qn[4 * j + 1]), u2h(w.qn[4 * j + 2]), u2h(w.qn[4 * j + 3]));
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh, s, 0, 0, 0);
-      if (res_lo) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh, s, 0, 0, 0);
-      if constexpr (QLO) {
-        const h8_t ql = cat8(u2h(w.ql[4 * j]), u2h(w.ql[4 * j + 1]), u2h(w.ql[4 * j + 2]), u2h(w.ql[4 * j + 3]));
-        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql, s, 0, 0, 0);
-      }
-    }
+    s_from_residual<D, QLO>(w, a, rslot, t0, h, lane, sh, sl);
   } else {
-    const long rb = row_base(pages, L, blk, tk, BITS);
+    QK<D> qk;
+    {
+      const long e0 = ((long)(t0 / L.KG) * L.H + h) * D + c * CPL;
+      uint32_t ks[CPL / 2], km[CPL / 2];
+      load_bytes<2 * CPL>(pages + blk * L.stride + L.o_ks + 2 * e0, ks);
+      load_bytes<2 * CPL>(pages + blk * L.stride + L.o_km + 2 * e0, km);
+      build_qk<D, QLO>(qk, w, ks, km, a.scale_log2);
+    }
+    bias_s = qk.bias_s;
+    const long rb = row_base(pages, L, blk, t0 + n, BITS);
     constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
     uint32_t kw[KW];
     if (rb >= 0) {
@@ -240,31 +323,23 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
     }
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
-      // 8 channels = BITS bytes of the lane's slice.
-      uint32_t wj[2];
-      if constexpr (BITS == 8) {
-        wj[0] = kw[2 * j];
-        wj[1] = kw[2 * j + 1];
-      } else if constexpr (BITS == 4) {
-        wj[0] = kw[j];
-      } else {
-        wj[0] = kw[j >> 1] >> (16 * (j & 1));
-      }
-      const h8_t kf = unpack8<BITS>(wj);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, w.qk[j], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, w.qkl[j], s, 0, 0, 0);
+      const h8_t kf = kfrag_j<BITS>(kw, j);
+      sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.hi[j], sh, 0, 0, 0);
+      sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.lo[j], sl, 0, 0, 0);
     }
   }
+  float x[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float v = in_res ? s[i] : s[i] + w.bias;
-    s[i] = (t0 + 4 * c + i < n_valid) ? v * a.scale_log2 : -__builtin_inff();
+    const float s = sh[i] + sl[i];
+    const float v = __builtin_fmaf(s, a.scale_log2, bias_s);  // bias_s = 0 for residual keys
+    x[i] = (t0 + 4 * c + i < n_valid) ? v : -__builtin_inff();
   }
 
   // ---- V fragments: tokens t0+4c+i, channels n*CPM + j -------------------
   constexpr int VB = CPM * BITS / 8;  // bytes per token of the lane's V slice
   constexpr int VW = VB >= 4 ? VB / 4 : 1;
-  uint32_t vw[4][VW];
+  uint32_t vw[4][VW], vsh[4][4];
   const int G = D / L.VG;
   const int g = (n * CPM) / L.VG;
   _Float16 sv[4], mv[4];
@@ -285,24 +360,13 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
       mv[i] = (_Float16)0.f;
     }
   }
+  vshift<BITS, VW>(vw, vsh);
   const h2_t s01 = {sv[0], sv[1]}, s23 = {sv[2], sv[3]};
   const h2_t m01 = {mv[0], mv[1]}, m23 = {mv[2], mv[3]};
   h4_t va[CPM];
 #pragma unroll
-  for (int j = 0; j < CPM; ++j) {
-    // byte / shift of channel j inside the lane's slice
-    constexpr int PER = 8 / BITS;
-    const int byte = j / PER, sh = (j % PER) * BITS;
-    const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + (byte & 3)) << 16) | (uint32_t)(byte & 3);
-    const int wd = byte >> 2;
-    const uint32_t mask = ((1u << BITS) - 1u) * 0x00010001u;
-    const uint32_t x01 = (__builtin_amdgcn_perm(vw[1][wd], vw[0][wd], sel) >> sh) & mask;
-    const uint32_t x23 = (__builtin_amdgcn_perm(vw[3][wd], vw[2][wd], sel) >> sh) & mask;
-    const h2_t v01 = __builtin_elementwise_fma(code_pair(x01), s01, m01);
-    const h2_t v23 = __builtin_elementwise_fma(code_pair(x23), s23, m23);
-    va[j] = h4_t{v01[0], v01[1], v23[0], v23[1]};
-  }
-  softmax_pv<D, QLO>(w, s, va);
+  for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23);
+  softmax_pv<D, QLO>(w, x, va);
 }
 
 // ---------------------------------------------------------------------------
@@ -310,21 +374,22 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
 // split through an NBUF-slot ring in LDS, filled by direct global->LDS DMA
 // (global_load_lds_dword{,x4}: lane L's bytes land at slot + size * L), so the
 // bytes in flight per CU are set by the ring size, not by VGPRs. The DMAs are
-// issued from inline asm: the compiler neither sees them nor inserts waits for
-// them; the wave waits with an explicit s_waitcnt vmcnt(n) for the tile it is
-// about to read (loads retire in order, so waiting for "at most n outstanding"
-// covers every older load). Every tile issues the same number of DMA
-// instructions (a tile the fast path does not take -- the open K group, a block
-// of another tier -- loads a dummy 16 bytes per lane from its page header), so
-// n is a compile-time count.
+// issued from inline asm with a 64-bit scalar base (the layer's pages) and a
+// 32-bit per-lane byte offset; the compiler neither sees them nor inserts waits
+// for them; the wave waits with an explicit s_waitcnt vmcnt(n) for the tile it
+// is about to read (loads retire in order, so waiting for "at most n
+// outstanding" covers every older load). Every tile issues the same number of
+// DMA instructions (a tile the fast path does not take -- the open K group, a
+// block of another tier -- loads 4 dummy bytes from its page header into its
+// slot), so n is a compile-time count.
 // ---------------------------------------------------------------------------
 #pragma clang diagnostic ignored "-Winline-asm"
 
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, %2" ::"v"(off), "s"(lds), "s"(base) : "memory", "m0");
 }
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+__device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, %2" ::"v"(off), "s"(lds), "s"(base) : "memory", "m0");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -344,15 +409,16 @@ struct Ring {
   static constexpr int WAVE_BYTES = NBUF * SLOT;
 };
 
-// Per-block facts of the split's next <= 64 blocks, one block per lane: chunk
-// byte offsets (chunk 0 is the block's own page), tier and residual mapping.
+// Per-block facts of the split's next <= 64 blocks, one block per lane: byte
+// offsets (from the layer's pages) of the block's page and of its chunks
+// (chunk 0 is in the block's own page), tier and residual mapping.
 struct BlockLane {
-  long cb0, cb1, cb2, cb3;
+  uint32_t pg, cb1, cb2, cb3;
   int blk;    // -1: not a valid block id
   int tier;
   // kNotFast unless the block is stored at the kernel's tier with every chunk it
   // needs in range; else the K group read from the residual (-1: none), whose
-  // tile takes the generic path. Derived from the loads (not a loaded register
+  // tile takes K from the residual. Derived from the loads (not a loaded register
   // itself), so the compiler waits for them once, before the tile loop, rather
   // than with a vmcnt(0) -- which would drain the DMA ring -- at a use inside it.
   int fast_rg;
@@ -360,20 +426,18 @@ struct BlockLane {
 };
 constexpr int kNotFast = -0x7fffffff;
 
-__device__ __forceinline__ long mul32(long a, long b) { return (long)((uint64_t)(uint32_t)a * (uint32_t)b); }
-
 template <int BITS>
 __device__ __forceinline__ BlockLane load_block(const DecodeArgs& a, long blk) {
   const Lay& L = a.L;
   BlockLane b{0, 0, 0, 0, -1, 2, kNotFast, -1, -1};
   if (blk < 0 || blk >= L.nb) return b;
-  const long pg = mul32(blk, L.stride);
+  const uint32_t pg = (uint32_t)blk * (uint32_t)L.stride;  // the pages span < 4 GiB (checked on the host)
   const uint4 hd = *(const uint4*)(a.pages + pg);
   b.blk = (int)blk;
+  b.pg = pg;
   b.tier = tier_of(hd.x & 0xffu);
-  b.cb0 = pg + L.o_data;
   const uint32_t ids[3] = {hd.y, hd.z, hd.w};
-  long cbs[3];
+  uint32_t cbs[3];
   bool ok = true;
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
@@ -381,7 +445,7 @@ __device__ __forceinline__ BlockLane load_block(const DecodeArgs& a, long blk) {
     const uint32_t page = a.kc_mul ? __umulhi(id, a.kc_mul) : id;
     const uint32_t slot = id - page * (uint32_t)L.KC;
     const bool in = (int)id >= 0 && (long)page < L.nb;
-    cbs[j] = in ? mul32(page, L.stride) + L.o_data + mul32(slot, L.cb) : b.cb0;
+    cbs[j] = in ? page * (uint32_t)L.stride + (uint32_t)L.o_data + slot * (uint32_t)L.cb : pg + (uint32_t)L.o_data;
     if (j < (BITS == 8 ? 3 : (BITS == 4 ? 1 : 0))) ok = ok && in;
   }
   b.cb1 = cbs[0];
@@ -396,130 +460,155 @@ __device__ __forceinline__ BlockLane load_block(const DecodeArgs& a, long blk) {
   return b;
 }
 
-__device__ __forceinline__ long readlane64(long v, int lane) {
-  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, lane);
-  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)v >> 32), lane);
-  return (long)(((uint64_t)hi << 32) | lo);
-}
-
-// DMA one tile (16 tokens from block offset t0) of head h into ring slot `slot`;
-// a non-fast tile issues the same number of DMAs, each lane 0 copying 4 header bytes.
+// Per-lane constants of the pipelined path (byte offsets; LDS ones from the slot).
 template <int D, int BITS>
-__device__ __forceinline__ void issue_tile(const DecodeArgs& a, uint32_t slot, bool fast, int t0, int h, int lane,
-                                           long cb0, long cb1, long cb2, long cb3) {
+struct LaneConst {
+  // DMA sources
+  uint32_t kv_tl[Ring<D, BITS>::KI];   // token (within the tile) of K/V DMA r
+  uint32_t kv_off[Ring<D, BITS>::KI];  // head + 16-byte piece within the row
+  uint32_t ks_off;                     // k_scale / k_min piece (without the page and group)
+  uint32_t vs_off;                     // V stats piece (without the page and first token)
+  // LDS reads
+  uint32_t k_rd, v_rd, s_rd, vs_rd, vm_rd;
+};
+
+template <int D, int BITS>
+__device__ __forceinline__ LaneConst<D, BITS> lane_const(const DecodeArgs& a, int h, int lane) {
   using R = Ring<D, BITS>;
   const Lay& L = a.L;
-  const uint8_t* page = a.pages + (cb0 - L.o_data);
+  constexpr int QPT = R::KB / 16;  // 16-byte pieces per token row (one side, one head)
+  constexpr int CPL = D / 4, CPM = D / 16, VB = CPM * BITS / 8;
+  LaneConst<D, BITS> k;
+#pragma unroll
+  for (int r = 0; r < R::KI; ++r) {
+    const int idx = lane + 64 * r;
+    k.kv_tl[r] = idx / QPT;
+    k.kv_off[r] = (uint32_t)(h * R::KB + 16 * (idx % QPT));
+  }
+  k.ks_off = (uint32_t)((lane < D / 8 ? L.o_ks : L.o_km) + 2L * h * D + 16 * (lane % (D / 8)));
+  const int G = D >> a.vg_shift;
+  const int sp = G == 4 ? 1 : 0;  // log2(dwords per token per stat)
+  const int which = lane >> (4 + sp);
+  const int r = lane & ((16 << sp) - 1);
+  k.vs_off = (uint32_t)((which ? L.o_vm : L.o_vs) + 2L * ((r >> sp) * L.H + h) * G + 4 * (r & ((1 << sp) - 1)));
+  const int c = lane >> 4, n = lane & 15;
+  k.k_rd = (uint32_t)(n * R::KB + c * (CPL * BITS / 8));
+  k.v_rd = (uint32_t)(R::OFF_V + 4 * c * R::KB + n * VB);
+  k.s_rd = (uint32_t)(R::OFF_S + 2 * c * CPL);
+  const int g = (n * CPM) >> a.vg_shift;
+  k.vs_rd = (uint32_t)(R::OFF_VS + 2 * (4 * c * G + g));
+  k.vm_rd = k.vs_rd + 2 * 16 * G;
+  return k;
+}
+
+// DMA one tile (16 tokens from block offset t0) of the wave's head into ring
+// slot `slot`. pg / cb: the block's page and chunk byte offsets.
+template <int D, int BITS>
+__device__ __forceinline__ void issue_tile(const DecodeArgs& a, const LaneConst<D, BITS>& k, uint32_t slot, bool fast,
+                                           int t0, int lane, uint32_t pg, uint32_t cb1, uint32_t cb2, uint32_t cb3) {
+  using R = Ring<D, BITS>;
+  const Lay& L = a.L;
   if (!fast) {
 #pragma unroll
     for (int i = 0; i < R::M; ++i) {
-      if (lane == 0) dma4(page, slot);
+      if (lane == 0) dma4(a.pages, pg, slot);
     }
     return;
   }
   constexpr int LB = BITS == 8 ? 3 : (BITS == 4 ? 2 : 1);
   const int tpc_shift = a.bs_shift + 1 - LB;  // tokens per chunk = 2 * BS / BITS
-  constexpr long ROWB = 2L * D * BITS / 8;     // per head; a row holds all heads
-  const long rowb = ROWB * L.H;
-  const long side = rowb / 2;
-  const long headb = (long)h * R::KB;
-  constexpr int QPT = R::KB / 16;
+  const uint32_t rowb = (uint32_t)(2 * D * BITS / 8) * (uint32_t)L.H;
+  const uint32_t side = rowb / 2;
+  const uint32_t cb0 = pg + (uint32_t)L.o_data;
 #pragma unroll
   for (int r = 0; r < R::KI; ++r) {
-    const int idx = lane + 64 * r;
-    const int t = t0 + idx / QPT;
-    const int j = t >> tpc_shift;
-    long cb = cb0;
+    const uint32_t t = (uint32_t)t0 + k.kv_tl[r];
+    const uint32_t j = t >> tpc_shift;
+    uint32_t cb = cb0;
     if constexpr (BITS >= 4) cb = j == 1 ? cb1 : cb;
     if constexpr (BITS == 8) cb = j == 2 ? cb2 : (j == 3 ? cb3 : cb);
-    const uint8_t* src = a.pages + cb + (long)(t & ((1 << tpc_shift) - 1)) * rowb + headb + 16 * (idx % QPT);
-    if (idx < R::KCB / 16) {
-      dma16(src, slot + 1024 * r);
-      dma16(src + side, slot + R::OFF_V + 1024 * r);
+    const uint32_t off = cb + (t & ((1u << tpc_shift) - 1)) * rowb + k.kv_off[r];
+    if (lane + 64 * r < R::KCB / 16) {
+      dma16(a.pages, off, slot + 1024 * r);
+      dma16(a.pages, off + side, slot + R::OFF_V + 1024 * r);
     }
   }
-  {  // k_scale / k_min of the tile's K group: D/8 lanes each
-    const long e0 = (long)((t0 >> a.kg_shift) * L.H + h) * D * 2;
-    const uint8_t* src = lane < D / 8 ? page + L.o_ks + e0 + 16 * lane : page + L.o_km + e0 + 16 * (lane - D / 8);
-    if (lane < D / 4) dma16(src, slot + R::OFF_S);
-  }
-  {  // V scale / min: G halves per token each, moved as G/2 dwords
-    const int G = D >> a.vg_shift;
-    const int sp = G == 4 ? 1 : 0;  // log2(dwords per token per stat)
-    const int which = lane >> (4 + sp);
-    const int r = lane & ((16 << sp) - 1);
-    const int t = t0 + (r >> sp);
-    const uint8_t* src = page + (which ? L.o_vm : L.o_vs) + (long)(t * L.H + h) * G * 2 + 4 * (r & ((1 << sp) - 1));
-    if (lane < (32 << sp)) dma4(src, slot + R::OFF_VS);
-  }
+  // k_scale / k_min of the tile's K group: D/8 lanes each
+  const uint32_t ks = pg + (uint32_t)((t0 >> a.kg_shift) * L.H * D * 2);
+  if (lane < D / 4) dma16(a.pages, ks + k.ks_off, slot + R::OFF_S);
+  // V scale / min: G halves per token each, moved as G/2 dwords
+  const int G = D >> a.vg_shift;
+  const uint32_t vs = pg + (uint32_t)(t0 * L.H * G * 2);
+  if (lane < (G == 4 ? 64 : 32)) dma4(a.pages, vs + k.vs_off, slot + R::OFF_VS);
 }
 
-// One fast tile from LDS slot `sp` (tier BITS, K from codes).
+// One pipelined tile from LDS slot `sp` (tier BITS, K from codes); n_rel =
+// valid tokens of the tile counted from its first token.
+// in_res: the tile is the block's open K group (K from residual slot rslot;
+// its V, in the page, still comes through the ring).
 template <int D, bool QLO, int BITS>
-__device__ __forceinline__ void compute_tile(Wave<D, QLO>& w, const DecodeArgs& a, const uint8_t* sp, int t0,
-                                             int n_valid, bool new_group, int lane) {
+__device__ __forceinline__ void compute_tile(Wave<D, QLO>& w, const DecodeArgs& a, const LaneConst<D, BITS>& k,
+                                             const uint8_t* sp, int t0, int n_rel, bool in_res, long rslot, int h,
+                                             int lane) {
   using W = Wave<D, QLO>;
   using R = Ring<D, BITS>;
   constexpr int CPL = W::CPL, NQK = W::NQK, CPM = W::CPM;
-  const int c = lane >> 4, n = lane & 15;
-  if (new_group)
-    build_qk_at<D, QLO, BITS>(w, sp + R::OFF_S + 2 * c * CPL, sp + R::OFF_S + 2 * D + 2 * c * CPL, n < a.gqa);
-  f4_t s = {0.f, 0.f, 0.f, 0.f};
-  {
+  const int c = lane >> 4;
+  f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
+  float bias_s = 0.f;
+  if (in_res) {
+    s_from_residual<D, QLO>(w, a, rslot, t0, h, lane, sh, sl);
+  } else {
+    QK<D> qk;
+    {
+      uint32_t ks[CPL / 2], km[CPL / 2];
+      load_bytes<2 * CPL>(sp + k.s_rd, ks);
+      load_bytes<2 * CPL>(sp + k.s_rd + 2 * D, km);
+      build_qk<D, QLO>(qk, w, ks, km, a.scale_log2);
+    }
+    bias_s = qk.bias_s;
     constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
     uint32_t kw[KW];
-    load_bytes<CPL * BITS / 8>(sp + n * R::KB + c * (CPL * BITS / 8), kw);
+    load_bytes<CPL * BITS / 8>(sp + k.k_rd, kw);
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
-      uint32_t wj[2];
-      if constexpr (BITS == 8) {
-        wj[0] = kw[2 * j];
-        wj[1] = kw[2 * j + 1];
-      } else if constexpr (BITS == 4) {
-        wj[0] = kw[j];
-      } else {
-        wj[0] = kw[j >> 1] >> (16 * (j & 1));
-      }
-      const h8_t kf = unpack8<BITS>(wj);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, w.qk[j], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, w.qkl[j], s, 0, 0, 0);
+      const h8_t kf = kfrag_j<BITS>(kw, j);
+      sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.hi[j], sh, 0, 0, 0);
+      sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.lo[j], sl, 0, 0, 0);
     }
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) s[i] = (t0 + 4 * c + i < n_valid) ? (s[i] + w.bias) * a.scale_log2 : -__builtin_inff();
 
   constexpr int VB = CPM * BITS / 8;
   constexpr int VW = VB >= 4 ? VB / 4 : 1;
-  uint32_t vw[4][VW];
-  const int G = D >> a.vg_shift;
-  const int g = (n * CPM) >> a.vg_shift;
-  const _Float16* vs = (const _Float16*)(sp + R::OFF_VS);
-  _Float16 sv[4], mv[4];
+  uint32_t vw[4][VW], vsh[4][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int tv = 4 * c + i;
-    load_bytes<VB>(sp + R::OFF_V + tv * R::KB + n * VB, vw[i]);
-    const bool ok = t0 + tv < n_valid;
-    sv[i] = ok ? vs[tv * G + g] : (_Float16)0.f;
-    mv[i] = ok ? vs[16 * G + tv * G + g] : (_Float16)0.f;
+  for (int i = 0; i < 4; ++i) load_bytes<VB>(sp + k.v_rd + i * R::KB, vw[i]);
+  const int G = D >> a.vg_shift;
+  const _Float16* vs = (const _Float16*)(sp + k.vs_rd);
+  const _Float16* vm = (const _Float16*)(sp + k.vm_rd);
+  h2_t s01 = {vs[0], vs[G]}, s23 = {vs[2 * G], vs[3 * G]};
+  h2_t m01 = {vm[0], vm[G]}, m23 = {vm[2 * G], vm[3 * G]};
+  float x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = __builtin_fmaf(sh[i] + sl[i], a.scale_log2, bias_s);
+  if (n_rel < 16) {
+    // The block's last tile: tokens past the sequence get p = 0 and V = 0 (their
+    // page bytes are arbitrary and 0 * inf would poison the sum).
+    const int t = 4 * c;
+    const uint32_t k01 = t + 1 < n_rel ? ~0u : (t < n_rel ? 0xFFFFu : 0u);
+    const uint32_t k23 = t + 3 < n_rel ? ~0u : (t + 2 < n_rel ? 0xFFFFu : 0u);
+    s01 = u2h(h2u(s01) & k01);
+    m01 = u2h(h2u(m01) & k01);
+    s23 = u2h(h2u(s23) & k23);
+    m23 = u2h(h2u(m23) & k23);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = t + i < n_rel ? x[i] : -__builtin_inff();
   }
-  const h2_t s01 = {sv[0], sv[1]}, s23 = {sv[2], sv[3]};
-  const h2_t m01 = {mv[0], mv[1]}, m23 = {mv[2], mv[3]};
+  vshift<BITS, VW>(vw, vsh);
   h4_t va[CPM];
 #pragma unroll
-  for (int j = 0; j < CPM; ++j) {
-    constexpr int PER = 8 / BITS;
-    const int byte = j / PER, sh = (j % PER) * BITS;
-    const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + (byte & 3)) << 16) | (uint32_t)(byte & 3);
-    const int wd = byte >> 2;
-    const uint32_t mask = ((1u << BITS) - 1u) * 0x00010001u;
-    const uint32_t x01 = (__builtin_amdgcn_perm(vw[1][wd], vw[0][wd], sel) >> sh) & mask;
-    const uint32_t x23 = (__builtin_amdgcn_perm(vw[3][wd], vw[2][wd], sel) >> sh) & mask;
-    const h2_t v01 = __builtin_elementwise_fma(code_pair(x01), s01, m01);
-    const h2_t v23 = __builtin_elementwise_fma(code_pair(x23), s23, m23);
-    va[j] = h4_t{v01[0], v01[1], v23[0], v23[1]};
-  }
-  softmax_pv<D, QLO>(w, s, va);
+  for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23);
+  softmax_pv<D, QLO>(w, x, va);
 }
 
 template <int D, int BITS, int NB>
@@ -532,8 +621,12 @@ __device__ __forceinline__ void wait_tile(int ahead) {
   else wait_vmcnt<0>();
 }
 
+__device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
 template <int D, int BITS, bool QLO>
-__global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
+// Three waves per SIMD (<= 168 VGPRs) where the ring leaves LDS for three
+// workgroups per CU; INT8's larger ring and the float32-query variant get two.
+__global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_kernel(DecodeArgs a) {
   using W = Wave<D, QLO>;
   using R = Ring<D, BITS>;
   extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
@@ -584,8 +677,8 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
   for (int j = 0; j < W::CPM; ++j) w.acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
   w.m_run = -__builtin_inff();
   w.l_lane = 0.f;
-  w.bias = 0.f;
 
+  const LaneConst<D, BITS> kc = lane_const<D, BITS>(a, h, lane);
   const int tpb_shift = a.bs_shift - 4;  // tiles per block = BS / 16
   const bool stats_ok = (D >> a.vg_shift) == 2 || (D >> a.vg_shift) == 4;
   for (int c0 = b_start; c0 < b_end; c0 += 64) {
@@ -597,52 +690,40 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
     auto issue = [&](int tt) {
       const int b = tt >> tpb_shift;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
-      const int frg = __builtin_amdgcn_readlane(bl.fast_rg, b);
-      const bool fast = frg != kNotFast && frg != (t0 >> a.kg_shift) && stats_ok;
-      const long cb0 = readlane64(bl.cb0, b);
-      const long cb1 = BITS >= 4 ? readlane64(bl.cb1, b) : cb0;
-      const long cb2 = BITS == 8 ? readlane64(bl.cb2, b) : cb0;
-      const long cb3 = BITS == 8 ? readlane64(bl.cb3, b) : cb0;
+      const bool fast = (int)rl((uint32_t)bl.fast_rg, b) != kNotFast && stats_ok;
+      const uint32_t pg = rl(bl.pg, b);
+      const uint32_t cb1 = BITS >= 4 ? rl(bl.cb1, b) : 0u;
+      const uint32_t cb2 = BITS == 8 ? rl(bl.cb2, b) : 0u;
+      const uint32_t cb3 = BITS == 8 ? rl(bl.cb3, b) : 0u;
       const uint32_t slot = ring0 + (uint32_t)((tt % R::NBUF) * R::SLOT);
-      issue_tile<D, BITS>(a, slot, fast, t0, h, lane, cb0, cb1, cb2, cb3);
+      issue_tile<D, BITS>(a, kc, slot, fast, t0, lane, pg, cb1, cb2, cb3);
     };
 
 #pragma unroll 1
     for (int tt = 0; tt < R::NBUF - 1 && tt < n_tiles; ++tt) issue(tt);
-    long qk_blk = -1;
-    int qk_grp = -1, qk_bits = 0;
 #pragma unroll 1
     for (int tt = 0; tt < n_tiles; ++tt) {
       if (tt + R::NBUF - 1 < n_tiles) issue(tt + R::NBUF - 1);
       const int ahead = (n_tiles - 1 - tt) < (R::NBUF - 1) ? (n_tiles - 1 - tt) : (R::NBUF - 1);
       const int b = tt >> tpb_shift;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
-      const long blk = __builtin_amdgcn_readlane(bl.blk, b);
+      const long blk = (int)rl((uint32_t)bl.blk, b);
       if (blk < 0) continue;
       const int grp = t0 >> a.kg_shift;
-      const int frg = __builtin_amdgcn_readlane(bl.fast_rg, b);
-      const bool fast = frg != kNotFast && frg != grp && stats_ok;
+      const int frg = (int)rl((uint32_t)bl.fast_rg, b);
+      const bool fast = frg != kNotFast && stats_ok;
       const int n_valid = seq_len - ((c0 + b) << a.bs_shift);
       if (fast) {
+        const bool in_res = frg == grp;  // frg = the block's residual group, -1: none
+        const long rslot = in_res ? (int)rl((uint32_t)bl.rslot, b) : -1;
         wait_tile<D, BITS, R::NBUF>(ahead);
-        const bool new_group = blk != qk_blk || grp != qk_grp || qk_bits != BITS;
-        compute_tile<D, QLO, BITS>(w, a, my_ring + (tt % R::NBUF) * R::SLOT, t0, n_valid, new_group, lane);
-        qk_blk = blk;
-        qk_grp = grp;
-        qk_bits = BITS;
+        compute_tile<D, QLO, BITS>(w, a, kc, my_ring + (tt % R::NBUF) * R::SLOT, t0, n_valid - t0, in_res, rslot, h,
+                                   lane);
       } else {
-        const int tier = __builtin_amdgcn_readlane(bl.tier, b);
-        const int rgrp = __builtin_amdgcn_readlane(bl.rgrp, b);
-        const long rslot = __builtin_amdgcn_readlane(bl.rslot, b);
+        const int tier = (int)rl((uint32_t)bl.tier, b);
+        const int rgrp = (int)rl((uint32_t)bl.rgrp, b);
+        const long rslot = (int)rl((uint32_t)bl.rslot, b);
         const bool in_res = rslot >= 0 && rgrp == grp;
-        if (!in_res && (blk != qk_blk || grp != qk_grp || tier != qk_bits)) {
-          if (tier == 4) build_qk<D, QLO, 4>(w, a.pages, L, blk, grp, h, c, n < a.gqa);
-          else if (tier == 8) build_qk<D, QLO, 8>(w, a.pages, L, blk, grp, h, c, n < a.gqa);
-          else build_qk<D, QLO, 2>(w, a.pages, L, blk, grp, h, c, n < a.gqa);
-          qk_blk = blk;
-          qk_grp = grp;
-          qk_bits = tier;
-        }
         if (tier == 4) tile<D, QLO, 4>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
         else if (tier == 8) tile<D, QLO, 8>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
         else tile<D, QLO, 2>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
@@ -651,9 +732,7 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
     wait_vmcnt<0>();  // nothing of this chunk may still be landing in the ring
   }
 
-  float l = w.l_lane;
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  const float l = rows_sum(w.l_lane);
   if (n < a.gqa) {
     const long qh = (long)h * a.gqa + n;
     const long row = (seq * a.hq + qh) * a.num_splits + split;
@@ -670,27 +749,67 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeArgs a) {
   }
 }
 
-__global__ __launch_bounds__(64) void merge_kernel(MergeArgs a) {
-  const long seq = blockIdx.x;
-  const int head = blockIdx.y;
+// Merge of the splits: one wave per (sequence, query head). Lanes read the
+// splits' (m, l) in parallel, then every lane sums its channels over the splits
+// in split order.
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);  // seq * hq + head
+  if (row >= a.rows) return;
+  const long seq = row / a.hq;
+  const int head = (int)(row % a.hq);
   const int seq_len = (int)a.lens[seq];
   if (seq_len <= 0) return;
   const int n_blocks = (seq_len + a.BS - 1) / a.BS;
   const int per = (n_blocks + a.num_splits - 1) / a.num_splits;
   const int bps = a.bps > per ? a.bps : per;
   const int used = (n_blocks + bps - 1) / bps;
-  const long base = (seq * a.hq + head) * a.num_splits;
+  const long base = row * a.num_splits;
   float m = -__builtin_inff();
-  for (int sp = 0; sp < used; ++sp) m = fmaxf(m, a.ml[(base + sp) * 2]);
-  const long o_row = a.q_rows ? a.q_rows[seq] : seq;
-  for (int d = threadIdx.x; d < a.D; d += 64) {
-    float num = 0.f, den = 0.f;
-    for (int sp = 0; sp < used; ++sp) {
-      const float wgt = __builtin_amdgcn_exp2f(a.ml[(base + sp) * 2] - m);
-      den += a.ml[(base + sp) * 2 + 1] * wgt;
-      num += a.acc[(base + sp) * a.D + d] * wgt;
+  for (int s0 = 0; s0 < used; s0 += 64) {
+    const float mi = s0 + lane < used ? a.ml[(base + s0 + lane) * 2] : -__builtin_inff();
+    m = fmaxf(m, mi);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  float den = 0.f;
+  float num[2] = {0.f, 0.f};
+  const int nd = (a.D + 63) / 64;  // channels per lane (D <= 128)
+  for (int s0 = 0; s0 < used; s0 += 64) {
+    const bool in = s0 + lane < used;
+    const float wl = in ? __builtin_amdgcn_exp2f(a.ml[(base + s0 + lane) * 2] - m) : 0.f;
+    den += in ? a.ml[(base + s0 + lane) * 2 + 1] * wl : 0.f;
+    const int cnt = used - s0 < 64 ? used - s0 : 64;
+    int i = 0;
+    for (; i + 8 <= cnt; i += 8) {  // 8 splits' loads in flight per lane
+      const float* src = a.acc + (base + s0 + i) * a.D;
+      for (int e = 0; e < nd; ++e) {
+        const int d = lane + 64 * e;
+        if (d < a.D) {
+          float x[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) x[u] = src[u * a.D + d];
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            num[e] += x[u] * __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(wl), i + u));
+        }
+      }
     }
-    st(a.out, a.out_dtype, o_row * a.o_s0 + head * a.o_s1 + d, num / den);
+    for (; i < cnt; ++i) {
+      const float wsp = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(wl), i));
+      const float* src = a.acc + (base + s0 + i) * a.D;
+      for (int e = 0; e < nd; ++e) {
+        const int d = lane + 64 * e;
+        if (d < a.D) num[e] += src[d] * wsp;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+  const long o_row = a.q_rows ? a.q_rows[seq] : seq;
+  for (int e = 0; e < nd; ++e) {
+    const int d = lane + 64 * e;
+    if (d < a.D) st(a.out, a.out_dtype, o_row * a.o_s0 + head * a.o_s1 + d, num[e] / den);
   }
 }
 
@@ -716,7 +835,7 @@ hipError_t launch_decode_d(const DecodeArgs& a, dim3 grid, dim3 block, hipStream
 }
 
 hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
-  const int hpw = a.L.H < 8 ? a.L.H : 8;
+  const int hpw = a.L.H < kHeadsPerGroup ? a.L.H : kHeadsPerGroup;
   const dim3 grid((unsigned)a.num_splits, (unsigned)num_seqs, (unsigned)((a.L.H + hpw - 1) / hpw));
   const dim3 block(64 * hpw);
   const bool qlo = a.q_dtype == ECHOKV_F32;
@@ -726,7 +845,9 @@ hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
 }
 
 hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s) {
-  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)num_seqs, (unsigned)a.hq), dim3(64), 0, s, a);
+  (void)num_seqs;
+  const long wgs = (a.rows + 3) / 4;
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)wgs), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
