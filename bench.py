@@ -11,9 +11,12 @@ device; the host plans the step's writes once for all layers.
 
 Prints one JSON line. ``value`` = INT4 paged-decode attention throughput in
 GB/s of algorithmic bytes (K/V codes, stats, residual, Q, O that the math
-needs) over the timed steps' INT4-layer decode launches, timed with HIP
-events on the launch stream; ``roofline`` puts it against 8 TB/s; the e2e
-decode rate of the whole 32-layer step is reported beside it.
+needs): the 16 INT4 layers' decode (decode + merge kernels, each layer over its
+own pages, at the lengths the timed steps reached) captured as one HIP graph
+and replayed ``--reps`` times between HIP events on the launch stream, so the
+time is GPU work only; ``roofline`` puts it against 8 TB/s. ``ms_per_step`` and
+``e2e_decode_tok_s`` time the whole 32-layer step (host planning included) over
+the ``--steps`` timed steps.
 """
 
 from __future__ import annotations
@@ -117,12 +120,12 @@ def run(args) -> dict:
     vn = [torch.randn(S, H, D, device=dev, dtype=torch.float16, generator=gen) for _ in range(LAYERS)]
     out = [torch.empty(S, HQ, D, device=dev, dtype=torch.float16) for _ in range(LAYERS)]
     max_blocks = table.shape[1]
-    num_splits = max(1, min(-(-max_blocks // args.bps), 32))
+    num_splits = max(1, min(-(-max_blocks // args.bps), args.max_splits))
     ws = (torch.empty(S, HQ, num_splits, D, device=dev), torch.empty(S, HQ, num_splits, 2, device=dev))
     int4 = [li for li in range(LAYERS) if tiers[li] == 4]
     scale = D ** -0.5
 
-    def step(i, events=None):
+    def step(i):
         pos = ctx - 1 + i  # position of this step's new token
         slots = table[np.arange(S), pos // BS] * BS + pos % BS
         plan = shared.planner.plan(slots)
@@ -136,32 +139,50 @@ def run(args) -> dict:
             if opened[li] is not None:
                 s.write_headers(torch.from_numpy(opened[li][0]).to(dev), torch.from_numpy(opened[li][1]).to(dev))
             s.apply(meta, kn[li], vn[li], krefs[li])
-            if events is not None and li in events:
-                events[li][0].record()
             decode_attention(s, q[li], table_d, lens_d, scale, blocks_per_split=args.bps, out=out[li],
-                             num_splits=num_splits, workspace=ws)
-            if events is not None and li in events:
-                events[li][1].record()
+                             num_splits=num_splits, workspace=ws, tier=int(tiers[li]))
         return lens
 
+    # End to end: the host plans every step; all 32 layers write and attend.
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    ev = []
     t0 = time.perf_counter()
-    bytes_int4 = 0
     for i in range(args.warmup, args.warmup + args.steps):
-        e = {li: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for li in int4}
-        lens = step(i, e)
-        ev.append(e)
-        bytes_int4 += alg_bytes(lens, 4) * len(int4)
+        lens = step(i)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    int4_ms = sum(a.elapsed_time(b) for e in ev for a, b in e.values())
-    n_launch = len(int4) * args.steps
+
+    # The metric: the 16 INT4 layers' decode attention (decode + merge kernels) over
+    # their own pages, at the lengths the last step reached, replayed as one HIP
+    # graph so the events time GPU work only (no host launch gaps).
+    lens_d = torch.from_numpy(lens).to(dev)
+
+    def int4_decode():
+        for li in int4:
+            decode_attention(stores[li], q[li], table_d, lens_d, scale, blocks_per_split=args.bps, out=out[li],
+                             num_splits=num_splits, workspace=ws, tier=4)
+
+    int4_decode()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        int4_decode()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = args.reps
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    int4_ms = e0.elapsed_time(e1)
+    n_launch = len(int4) * reps
     avg_ms = int4_ms / n_launch
-    achieved = bytes_int4 / (int4_ms * 1e-3) / 1e9
-    per_layer_bytes = bytes_int4 / n_launch
+    per_layer_bytes = alg_bytes(lens, 4)
+    achieved = per_layer_bytes / (avg_ms * 1e-3) / 1e9
     res = {
         "metric": METRIC,
         "value": round(achieved, 1),
@@ -191,7 +212,7 @@ def run(args) -> dict:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "decode_kernel<128> + merge_kernel (one INT4 layer-step)",
+            "kernel": "decode_kernel<128, 4> + merge_kernel (one INT4 layer-step, graph replay over the 16 INT4 layers)",
             "alg_bytes_per_launch": int(per_layer_bytes),
         },
     }
@@ -208,7 +229,7 @@ def cpu_baseline(store, q, table, lens) -> dict:
     from oracle.attention import decode_attention as oracle_decode
     from oracle.store import Layout, PageStore
 
-    n_seq = 16
+    n_seq = S
     L = Layout(H, D, BS, MEM, KG, VG)
     ps = PageStore.__new__(PageStore)
     ps.L, ps.n = L, store.num_blocks
@@ -235,7 +256,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--bps", type=int, default=16, help="blocks per decode split")
+    ap.add_argument("--bps", type=int, default=8, help="blocks per decode split")
+    ap.add_argument("--max-splits", type=int, default=64, help="cap on decode splits per sequence")
+    ap.add_argument("--reps", type=int, default=50, help="graph replays of the 16 INT4 layers' decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -50,12 +50,6 @@ __device__ __forceinline__ void st(void* p, int dtype, long i, float v) {
   else ((uint16_t*)p)[i] = f32_to_bf16(v);
 }
 
-// Four consecutive elements (channels) starting at element i.
-__device__ __forceinline__ void ld4(const void* p, int dtype, long i, float x[4]) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) x[e] = ld(p, dtype, i + e);
-}
-
 // N consecutive elements starting at element i. The dtype branch sits outside
 // the element loop, so the N loads issue back to back and the wave waits once
 // (a branch per element would wait for each load before issuing the next).
@@ -73,6 +67,27 @@ __device__ __forceinline__ void ld_n(const void* p, int dtype, long i, float* x)
     const float* s = (const float*)p + i;
 #pragma unroll
     for (int e = 0; e < N; ++e) x[e] = s[e];
+  }
+}
+
+// Four consecutive elements (channels) starting at element i.
+__device__ __forceinline__ void ld4(const void* p, int dtype, long i, float x[4]) { ld_n<4>(p, dtype, i, x); }
+
+// N consecutive elements stored from x at element i (dtype branch outside the loop).
+template <int N>
+__device__ __forceinline__ void st_n(void* p, int dtype, long i, const float* x) {
+  if (dtype == ECHOKV_F16) {
+    _Float16* d = (_Float16*)p + i;
+#pragma unroll
+    for (int e = 0; e < N; ++e) d[e] = (_Float16)x[e];
+  } else if (dtype == ECHOKV_BF16) {
+    uint16_t* d = (uint16_t*)p + i;
+#pragma unroll
+    for (int e = 0; e < N; ++e) d[e] = f32_to_bf16(x[e]);
+  } else {
+    float* d = (float*)p + i;
+#pragma unroll
+    for (int e = 0; e < N; ++e) d[e] = x[e];
   }
 }
 
@@ -99,6 +114,31 @@ __device__ __forceinline__ long row_base(const uint8_t* pages, const Lay& L, lon
   const long cb = chunk_base(pages, L, blk, off, bits);
   if (cb < 0) return -1;
   const int tpc = 2 * L.BS / bits;
+  return cb + (long)(off % tpc) * (2L * L.H * L.D * bits / 8);
+}
+
+// A block's 16 header bytes, read once: [0] tag, [4:16] pool chunk ids.
+struct Hdr {
+  uint32_t tag;
+  int32_t id[3];
+};
+
+__device__ __forceinline__ Hdr load_hdr(const uint8_t* pages, const Lay& L, long blk) {
+  const uint4 h = *(const uint4*)(pages + blk * L.stride);
+  return Hdr{h.x & 0xffu, {(int32_t)h.y, (int32_t)h.z, (int32_t)h.w}};
+}
+
+// row_base from a header already in registers.
+__device__ __forceinline__ long row_base_h(const Lay& L, long blk, const Hdr& hd, int off, int bits) {
+  const int tpc = 2 * L.BS / bits;
+  const int j = off / tpc;
+  long cb = blk * L.stride + L.o_data;
+  if (j > 0) {
+    const int id = j == 1 ? hd.id[0] : (j == 2 ? hd.id[1] : hd.id[2]);
+    const long page = id / L.KC, slot = id % L.KC;
+    if (id < 0 || page >= L.nb) return -1;
+    cb = page * L.stride + L.o_data + slot * L.cb;
+  }
   return cb + (long)(off % tpc) * (2L * L.H * L.D * bits / 8);
 }
 

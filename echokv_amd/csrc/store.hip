@@ -23,21 +23,36 @@ __global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) 
   const long blk = slot / L.BS;
   const int off = (int)(slot % L.BS);
   if (blk >= L.nb) return;
-  const int bits = tier_of(a.pages[blk * L.stride]);
-  const long rb = row_base(a.pages, L, blk, off, bits);
+  // Every load this row needs is independent of the others: issue them together
+  // (the kernel is a chain of memory round trips, not of arithmetic).
+  const Hdr hd = load_hdr(a.pages, L, blk);
   const long rslot = a.tok[a.tok_s0 + t];
   const int64_t sealed = a.tok[2 * a.tok_s0 + t];
   const long kidx = a.kref ? a.tok[3 * a.tok_s0 + t] : -1;
   const int quads = L.D / 4;
   const int items = L.H * quads;
   const int G = L.D / L.VG;
-  const int side = L.H * L.D * bits / 8;
   for (int base = 0; base < items; base += kThreads) {
     const int i = base + (int)threadIdx.x;
     const bool act = i < items;
     const int h = act ? i / quads : 0, c = act ? i % quads : 0;
-    float x[4] = {0.f, 0.f, 0.f, 0.f};
-    if (act) ld4(a.value, a.kv_dtype, t * a.v_s0 + h * a.v_s1 + 4 * c, x);
+    float x[4] = {0.f, 0.f, 0.f, 0.f}, k[4] = {0.f, 0.f, 0.f, 0.f};
+    if (act) {
+      ld_n<4>(a.value, a.kv_dtype, t * a.v_s0 + h * a.v_s1 + 4 * c, x);
+      ld_n<4>(a.key, a.kv_dtype, t * a.k_s0 + h * a.k_s1 + 4 * c, k);
+    }
+    _Float16 ks16[4], km16[4];  // the sealed group's stats (K codes under them)
+    if (act && sealed != 0) {
+      const long se = ((long)(off / L.KG) * L.H + h) * L.D + 4 * c;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ks16[e] = *f16p(a.pages, blk * L.stride + L.o_ks + 2 * (se + e));
+        km16[e] = *f16p(a.pages, blk * L.stride + L.o_km + 2 * (se + e));
+      }
+    }
+    const int bits = tier_of(hd.tag);
+    const long rb = row_base_h(L, blk, hd, off, bits);
+    const int side = L.H * L.D * bits / 8;
     float mn = fminf(fminf(x[0], x[1]), fminf(x[2], x[3]));
     float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
     seg_minmax(mn, mx, L.VG / 4);  // all lanes take part: segments never straddle `act`
@@ -57,22 +72,12 @@ __global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) 
     store_codes4(a.pages + rb + side + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
 
     // K: residual (open group), codes under the sealed stats, K_ref ring.
-    float k[4];
-    ld4(a.key, a.kv_dtype, t * a.k_s0 + h * a.k_s1 + 4 * c, k);
-    if (rslot >= 0 && rslot < a.res.rows) {
-      const long r0 = rslot * a.res.s0 + (long)(off % L.KG) * a.res.s1 + h * a.res.s2 + 4 * c;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) st(a.res.ptr, a.res.dtype, r0 + e, k[e]);
-    }
+    if (rslot >= 0 && rslot < a.res.rows)
+      st_n<4>(a.res.ptr, a.res.dtype, rslot * a.res.s0 + (long)(off % L.KG) * a.res.s1 + h * a.res.s2 + 4 * c, k);
     if (sealed != 0) {
-      const long se = ((long)(off / L.KG) * L.H + h) * L.D + 4 * c;
       uint32_t kq[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float ks = (float)*f16p(a.pages, blk * L.stride + L.o_ks + 2 * (se + e));
-        const float km = (float)*f16p(a.pages, blk * L.stride + L.o_km + 2 * (se + e));
-        kq[e] = quant_code(k[e], km, ks, bits);
-      }
+      for (int e = 0; e < 4; ++e) kq[e] = quant_code(k[e], (float)km16[e], (float)ks16[e], bits);
       store_codes4(a.pages + rb + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(kq, bits), bits);
     }
     if (kidx >= 0) {
@@ -90,19 +95,28 @@ __global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) 
 template <typename Fetch>
 __device__ void quantize_k_group(const Lay& L, uint8_t* pages, long blk, int grp, int off0, int n, int bits, int h,
                                  int c, Fetch fetch) {
+  // Tokens are fetched eight at a time so their loads are in flight together.
+  const Hdr hd = load_hdr(pages, L, blk);
   float mn[4], mx[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     mn[e] = __builtin_inff();
     mx[e] = -__builtin_inff();
   }
-  for (int p = 0; p < n; ++p) {
-    float x[4];
-    fetch(p, x);
+  for (int p0 = 0; p0 < n; p0 += 8) {
+    float x[8][4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      mn[e] = fminf(mn[e], x[e]);
-      mx[e] = fmaxf(mx[e], x[e]);
+    for (int u = 0; u < 8; ++u)
+      if (p0 + u < n) fetch(p0 + u, x[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (p0 + u < n) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          mn[e] = fminf(mn[e], x[u][e]);
+          mx[e] = fmaxf(mx[e], x[u][e]);
+        }
+      }
     }
   }
   float s[4], m[4];
@@ -114,15 +128,21 @@ __device__ void quantize_k_group(const Lay& L, uint8_t* pages, long blk, int grp
     *f16p(pages, blk * L.stride + L.o_ks + 2 * (se + e)) = s16;
     *f16p(pages, blk * L.stride + L.o_km + 2 * (se + e)) = m16;
   }
-  for (int p = 0; p < n; ++p) {
-    const long rb = row_base(pages, L, blk, off0 + p, bits);
-    if (rb < 0) continue;
-    float x[4];
-    fetch(p, x);
-    uint32_t q[4];
+  for (int p0 = 0; p0 < n; p0 += 8) {
+    float x[8][4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) q[e] = quant_code(x[e], m[e], s[e], bits);
-    store_codes4(pages + rb + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
+    for (int u = 0; u < 8; ++u)
+      if (p0 + u < n) fetch(p0 + u, x[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (p0 + u >= n) continue;
+      const long rb = row_base_h(L, blk, hd, off0 + p0 + u, bits);
+      if (rb < 0) continue;
+      uint32_t q[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[e] = quant_code(x[u][e], m[e], s[e], bits);
+      store_codes4(pages + rb + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
+    }
   }
 }
 

@@ -16,7 +16,8 @@ import torch
 
 from echokv_amd import _lib
 
-BLOCKS_PER_SPLIT = 16
+BLOCKS_PER_SPLIT = 8
+MAX_SPLITS = 64  # default cap: more, shorter splits keep every CU busy at small batch
 
 
 def _i64(t: torch.Tensor | None, device) -> torch.Tensor | None:
@@ -29,7 +30,7 @@ def _i64(t: torch.Tensor | None, device) -> torch.Tensor | None:
 
 def default_splits(block_table: torch.Tensor, block_size: int, blocks_per_split: int, max_len: int | None) -> int:
     max_blocks = block_table.shape[1] if max_len is None else min(block_table.shape[1], -(-max_len // block_size))
-    return max(1, -(-max_blocks // blocks_per_split))
+    return max(1, min(-(-max_blocks // blocks_per_split), MAX_SPLITS))
 
 
 def decode_attention(
