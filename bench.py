@@ -256,7 +256,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--bps", type=int, default=8, help="blocks per decode split")
+    ap.add_argument("--bps", type=int, default=16, help="blocks per decode split")
     ap.add_argument("--max-splits", type=int, default=64, help="cap on decode splits per sequence")
     ap.add_argument("--reps", type=int, default=50, help="graph replays of the 16 INT4 layers' decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -160,6 +160,7 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.num_splits = num_splits;
   a.bps = blocks_per_split;
+  a.num_seqs = num_seqs;
   a.tier = tier;
   if ((L->block_size & (L->block_size - 1)) || (L->k_group & (L->k_group - 1)) || L->chunks_per_page > 4)
     return ECHOKV_ESHAPE;

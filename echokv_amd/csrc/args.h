@@ -99,6 +99,7 @@ struct DecodeArgs {
   const int64_t* lens;
   float scale_log2;  // softmax scale * log2(e)
   int num_splits, bps;
+  long num_seqs;
   int tier;    // the layer's tier: selects the kernel specialised for it (2, 4 or 8)
   // log2 of block size, K group and V group (powers of two), and a reciprocal for
   // chunk id / chunks_per_page: floor(id / KC) = umulhi(id, kc_mul) (kc_mul 0: KC = 1).

@@ -1,9 +1,11 @@
 // Split-KV paged decode attention over the tiered (INT2/INT4/INT8) pages, gfx950.
 //
-// Work decomposition: one workgroup per (split, sequence, group of <= 4 KV
-// heads), one 64-wide wave per KV head. The heads of a token row sit side by
-// side in a page ([K codes of all heads | V codes of all heads]), so the waves
-// of a workgroup read neighbouring slices of the same cache lines together.
+// Work decomposition: a work item is (sequence, split, group of <= 4 KV heads),
+// one 64-wide wave per KV head; a persistent grid of as many workgroups as the
+// device holds at once walks the batch's non-empty items. The heads of a token
+// row sit side by side in a page ([K codes of all heads | V codes of all
+// heads]), so the waves of a workgroup read neighbouring slices of the same
+// cache lines together.
 //
 // Per 16-token tile a wave runs two MFMA contractions with no transposes:
 //   S^T[t, q]  = sum_d codes[t, d] * (q[q, d] * k_scale[d]) + sum_d q[q, d] * k_min[d]
@@ -623,33 +625,72 @@ __device__ __forceinline__ void wait_tile(int ahead) {
 
 __device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 
+// Blocks per split of a sequence of `len` tokens and the number of its splits
+// (0 for an empty sequence): max(blocks_per_split, ceil(blocks / num_splits)).
+__device__ __forceinline__ int split_blocks(const DecodeArgs& a, int n_blocks) {
+  const int per = (n_blocks + a.num_splits - 1) / a.num_splits;
+  return a.bps > per ? a.bps : per;
+}
+__device__ __forceinline__ int used_splits(const DecodeArgs& a, int len) {
+  if (len <= 0) return 0;
+  const int nb = (len + a.L.BS - 1) >> a.bs_shift;
+  const int bps = split_blocks(a, nb);
+  return (nb + bps - 1) / bps;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+// Inclusive prefix of the split counts of sequences [s0, s0 + 64), one per lane.
+__device__ __forceinline__ int scan_chunk(const DecodeArgs& a, long s0, int lane) {
+  const long s = s0 + lane;
+  return wave_incl_scan(s < a.num_seqs ? used_splits(a, (int)a.lens[s]) : 0, lane);
+}
+
+// The si-th split (in sequence order) of the batch's non-empty splits; false
+// past the last one. incl0 / tot0: the scan of the first 64 sequences.
+__device__ __forceinline__ bool locate(const DecodeArgs& a, long si, int lane, int incl0, int tot0, long& seq,
+                                       int& split) {
+  long base = 0;
+  int incl = incl0, tot = tot0;
+  for (long s0 = 0; s0 < a.num_seqs; s0 += 64) {
+    if (s0 > 0) {
+      incl = scan_chunk(a, s0, lane);
+      tot = __builtin_amdgcn_readlane(incl, 63);
+    }
+    if (si < base + tot) {
+      const int k = __builtin_popcountll(__builtin_amdgcn_ballot_w64(base + incl <= si));
+      const int excl = k == 0 ? 0 : __builtin_amdgcn_readlane(incl, k - 1);
+      seq = s0 + k;
+      split = (int)(si - base - excl);
+      return true;
+    }
+    base += tot;
+  }
+  return false;
+}
+
+// One work item: split `split` of sequence `seq` for KV head h (one wave).
 template <int D, int BITS, bool QLO>
-// Three waves per SIMD (<= 168 VGPRs) where the ring leaves LDS for three
-// workgroups per CU; INT8's larger ring and the float32-query variant get two.
-__global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int split, int h, int lane,
+                                            uint8_t* my_ring, uint32_t ring0) {
   using W = Wave<D, QLO>;
   using R = Ring<D, BITS>;
-  extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
   const Lay& L = a.L;
-  const int split = blockIdx.x;
-  const long seq = blockIdx.y;
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int h = blockIdx.z * (blockDim.x >> 6) + wv;
-  if (h >= L.H) return;
   const int seq_len = (int)a.lens[seq];
-  if (seq_len <= 0) return;
-  const int n_blocks = (seq_len + L.BS - 1) / L.BS;
-  const int per = (n_blocks + a.num_splits - 1) / a.num_splits;
-  const int bps = a.bps > per ? a.bps : per;
+  const int n_blocks = (seq_len + L.BS - 1) >> a.bs_shift;
+  const int bps = split_blocks(a, n_blocks);
   const int b_start = split * bps;
-  if (b_start >= n_blocks) return;
   const int b_end = b_start + bps < n_blocks ? b_start + bps : n_blocks;
   const long q_row = a.q_rows ? a.q_rows[seq] : seq;
   const long bt_row = a.bt_rows ? a.bt_rows[seq] : seq;
   const int c = lane >> 4, n = lane & 15;
-  uint8_t* my_ring = ring_lds + wv * R::WAVE_BYTES;
-  const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)my_ring);
 
   W w;
   {
@@ -749,6 +790,33 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   }
 }
 
+// Workgroup g takes work item g of the batch's non-empty (split, head group)
+// pairs in sequence order (head groups of a split adjacent, so they read the
+// same token rows together). The grid is sized for every sequence at its
+// maximum split count; workgroups past the last non-empty item exit at once,
+// and they come last in dispatch order instead of between the busy ones.
+// Three waves per SIMD (<= 168 VGPRs) where the ring leaves LDS for three
+// workgroups per CU; INT8's larger ring and the float32-query variant get two.
+template <int D, int BITS, bool QLO>
+__global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_kernel(DecodeArgs a) {
+  using R = Ring<D, BITS>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  uint8_t* my_ring = ring_lds + wv * R::WAVE_BYTES;
+  const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)my_ring);
+  const int n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  const long item = blockIdx.x;
+  const int incl0 = scan_chunk(a, 0, lane);
+  const int tot0 = __builtin_amdgcn_readlane(incl0, 63);
+  if (a.num_seqs <= 64 && item >= (long)tot0 * n_hg) return;  // past the last non-empty split
+  long seq;
+  int split;
+  if (!locate(a, item / n_hg, lane, incl0, tot0, seq, split)) return;
+  const int h = (int)(item % n_hg) * kHeadsPerGroup + wv;
+  if (h < a.L.H) decode_item<D, BITS, QLO>(a, seq, split, h, lane, my_ring, ring0);
+}
+
 // Merge of the splits: one wave per (sequence, query head). Lanes read the
 // splits' (m, l) in parallel, then every lane sums its channels over the splits
 // in split order.
@@ -814,8 +882,9 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
 }
 
 template <int D, int BITS, bool QLO>
-hipError_t launch_decode_t(const DecodeArgs& a, dim3 grid, dim3 block, hipStream_t s) {
-  const size_t lds = (size_t)(block.x / 64) * Ring<D, BITS>::WAVE_BYTES;
+hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
+  const dim3 block(64 * kHeadsPerGroup);
+  const size_t lds = (size_t)kHeadsPerGroup * Ring<D, BITS>::WAVE_BYTES;
   static bool attr = false;  // idempotent; set once per instantiation
   if (!attr) {
     if (hipFuncSetAttribute((const void*)decode_kernel<D, BITS, QLO>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -823,24 +892,23 @@ hipError_t launch_decode_t(const DecodeArgs& a, dim3 grid, dim3 block, hipStream
       return hipErrorInvalidValue;
     attr = true;
   }
-  hipLaunchKernelGGL((decode_kernel<D, BITS, QLO>), grid, block, lds, s, a);
+  const long items = a.num_seqs * a.num_splits * ((a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup);
+  hipLaunchKernelGGL((decode_kernel<D, BITS, QLO>), dim3((unsigned)items), block, lds, s, a);
   return hipGetLastError();
 }
 
 template <int D, bool QLO>
-hipError_t launch_decode_d(const DecodeArgs& a, dim3 grid, dim3 block, hipStream_t s) {
-  if (a.tier == 8) return launch_decode_t<D, 8, QLO>(a, grid, block, s);
-  if (a.tier == 2) return launch_decode_t<D, 2, QLO>(a, grid, block, s);
-  return launch_decode_t<D, 4, QLO>(a, grid, block, s);
+hipError_t launch_decode_d(const DecodeArgs& a, hipStream_t s) {
+  if (a.tier == 8) return launch_decode_t<D, 8, QLO>(a, s);
+  if (a.tier == 2) return launch_decode_t<D, 2, QLO>(a, s);
+  return launch_decode_t<D, 4, QLO>(a, s);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
-  const int hpw = a.L.H < kHeadsPerGroup ? a.L.H : kHeadsPerGroup;
-  const dim3 grid((unsigned)a.num_splits, (unsigned)num_seqs, (unsigned)((a.L.H + hpw - 1) / hpw));
-  const dim3 block(64 * hpw);
+  (void)num_seqs;  // a.num_seqs
   const bool qlo = a.q_dtype == ECHOKV_F32;
-  if (a.L.D == 128) return qlo ? launch_decode_d<128, true>(a, grid, block, s) : launch_decode_d<128, false>(a, grid, block, s);
-  if (a.L.D == 64) return qlo ? launch_decode_d<64, true>(a, grid, block, s) : launch_decode_d<64, false>(a, grid, block, s);
+  if (a.L.D == 128) return qlo ? launch_decode_d<128, true>(a, s) : launch_decode_d<128, false>(a, s);
+  if (a.L.D == 64) return qlo ? launch_decode_d<64, true>(a, s) : launch_decode_d<64, false>(a, s);
   return hipErrorInvalidValue;
 }
 

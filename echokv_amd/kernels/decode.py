@@ -16,7 +16,7 @@ import torch
 
 from echokv_amd import _lib
 
-BLOCKS_PER_SPLIT = 8
+BLOCKS_PER_SPLIT = 16
 MAX_SPLITS = 64  # default cap: more, shorter splits keep every CU busy at small batch
 
 
