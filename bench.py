@@ -260,11 +260,29 @@ def main():
     ap.add_argument("--max-splits", type=int, default=64, help="cap on decode splits per sequence")
     ap.add_argument("--reps", type=int, default=50, help="graph replays of the 16 INT4 layers' decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 1 GiB device-to-device 5 times (the reference kernel for FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     print(json.dumps(run(args)), flush=True)
+
+
+def copy_calibration(nbytes: int = 1 << 30, reps: int = 5) -> None:
+    """A plain copy of known size: under ``rocprofv3 --pmc FETCH_SIZE`` (then WRITE_SIZE)
+    it reads nbytes / 1024 KiB per dispatch, which scales the decode kernel's counters."""
+    import torch
+
+    a = torch.ones(nbytes, dtype=torch.uint8, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": nbytes, "reps": reps}), flush=True)
 
 
 if __name__ == "__main__":

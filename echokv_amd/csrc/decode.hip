@@ -806,7 +806,14 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   uint8_t* my_ring = ring_lds + wv * R::WAVE_BYTES;
   const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)my_ring);
   const int n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
-  const long item = blockIdx.x;
+  // The head groups of one split read neighbouring bytes of the same rows, and
+  // rows start 16 bytes into a 128-byte line (the page format's offsets), so
+  // they share lines. Workgroups are dealt to the 8 XCDs round-robin by
+  // dispatch order: put a split's head groups 8 dispatches apart (same XCD,
+  // same L2) so a shared line is fetched from HBM once.
+  const long span = 8L * n_hg;
+  const long r = blockIdx.x % span;
+  const long item = blockIdx.x - r + (r % 8) * n_hg + r / 8;
   const int incl0 = scan_chunk(a, 0, lane);
   const int tot0 = __builtin_amdgcn_readlane(incl0, 63);
   if (a.num_seqs <= 64 && item >= (long)tot0 * n_hg) return;  // past the last non-empty split
@@ -892,7 +899,9 @@ hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
       return hipErrorInvalidValue;
     attr = true;
   }
-  const long items = a.num_seqs * a.num_splits * ((a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup);
+  const long n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  const long span = 8 * n_hg;  // the kernel permutes workgroups within runs of `span`
+  const long items = (a.num_seqs * a.num_splits * n_hg + span - 1) / span * span;
   hipLaunchKernelGGL((decode_kernel<D, BITS, QLO>), dim3((unsigned)items), block, lds, s, a);
   return hipGetLastError();
 }
