@@ -10,8 +10,9 @@
 // Per 16-token tile a wave runs two MFMA contractions with no transposes:
 //   S^T[t, q]  = sum_d codes[t, d] * (q[q, d] * k_scale[d]) + sum_d q[q, d] * k_min[d]
 //                (v_mfma_f32_16x16x32_f16; the K scale is folded into the query,
-//                 the K min into a per-query float32 bias; the block's open K
-//                 group reads the full-precision residual instead)
+//                 the K min term is one more contraction of k_min with q into
+//                 the same accumulator; the block's open K group reads the
+//                 full-precision residual instead)
 //   O^T[d, q] += V[t, d]^T * P^T[t, q]   (v_mfma_f32_16x16x16f16, V dequantized
 //                 to fp16 in registers with its per-token fp16 scale / min)
 // Codes are exact in fp16. The query-side operand (q * k_scale, and the residual
@@ -189,13 +190,14 @@ struct Wave {
   float m_run, l_lane;
 };
 
-// One K group's query-side operand: q * k_scale as fp16 hi / lo MFMA fragments
-// and scale_log2 * sum_d q * k_min (built per tile: a per-tile temporary keeps
-// it out of the registers that live across the tile loop).
+// One K group's operands: q * k_scale as fp16 hi / lo MFMA fragments, and the
+// k_min fragments, contracted with q itself so sum_d q * k_min lands in the same
+// accumulator (k_min is exact in fp16; no cross-lane reduction needed). Built
+// per tile: a per-tile temporary keeps it out of the registers that live across
+// the tile loop.
 template <int D>
 struct QK {
-  h8_t hi[D / 32], lo[D / 32];
-  float bias_s;
+  h8_t hi[D / 32], lo[D / 32], mn[D / 32];
 };
 
 // q * k_scale (hi / lo) fragments and the scaled k_min bias of one K group from
@@ -204,19 +206,13 @@ template <int D, bool QLO>
 __device__ __forceinline__ void build_qk(QK<D>& qk, const Wave<D, QLO>& w, const uint32_t* ks, const uint32_t* km,
                                          float scale_log2) {
   constexpr int CPL = Wave<D, QLO>::CPL;
-  float b0 = 0.f, b1 = 0.f;
   uint32_t hi[CPL / 2], lo[CPL / 2];
 #pragma unroll
   for (int i = 0; i < CPL / 2; ++i) {
     const h2_t q = u2h(w.qn[i]), s = u2h(ks[i]);
     const h2_t ph = q * s;
     h2_t pl = __builtin_elementwise_fma(q, s, -ph);  // exact product minus its rounding, rounded once
-    float& b = (i & 1) ? b1 : b0;
-    b = __builtin_amdgcn_fdot2(q, u2h(km[i]), b, false);
-    if constexpr (QLO) {
-      pl = __builtin_elementwise_fma(u2h(w.ql[i]), s, pl);
-      b = __builtin_amdgcn_fdot2(u2h(w.ql[i]), u2h(km[i]), b, false);
-    }
+    if constexpr (QLO) pl = __builtin_elementwise_fma(u2h(w.ql[i]), s, pl);
     hi[i] = h2u(ph);
     lo[i] = h2u(pl);
   }
@@ -224,8 +220,22 @@ __device__ __forceinline__ void build_qk(QK<D>& qk, const Wave<D, QLO>& w, const
   for (int j = 0; j < Wave<D, QLO>::NQK; ++j) {
     qk.hi[j] = w2h8(hi[4 * j], hi[4 * j + 1], hi[4 * j + 2], hi[4 * j + 3]);
     qk.lo[j] = w2h8(lo[4 * j], lo[4 * j + 1], lo[4 * j + 2], lo[4 * j + 3]);
+    qk.mn[j] = w2h8(km[4 * j], km[4 * j + 1], km[4 * j + 2], km[4 * j + 3]);
   }
-  qk.bias_s = rows_sum(b0 + b1) * scale_log2;
+}
+
+// S^T += k_min q^T: the K min term of every token (rows), from the group's k_min
+// fragments and the query (hi, and lo for float32 queries).
+template <int D, bool QLO>
+__device__ __forceinline__ void add_kmin(const QK<D>& qk, const Wave<D, QLO>& w, f4_t& sh, f4_t& sl) {
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) {
+    sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(qk.mn[j], w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2],
+                                                               w.qn[4 * j + 3]), sh, 0, 0, 0);
+    if constexpr (QLO)
+      sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(qk.mn[j], w2h8(w.ql[4 * j], w.ql[4 * j + 1], w.ql[4 * j + 2],
+                                                                 w.ql[4 * j + 3]), sl, 0, 0, 0);
+  }
 }
 
 // S^T of a tile whose keys are the block's open K group, read from the
@@ -301,7 +311,6 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
 
   // ---- S^T = K Q'^T (+ bias) -------------------------------------------
   f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
-  float bias_s = 0.f;
   if (in_res) {
     s_from_residual<D, QLO>(w, a, rslot, t0, h, lane, sh, sl);
   } else {
@@ -313,7 +322,7 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
       load_bytes<2 * CPL>(pages + blk * L.stride + L.o_km + 2 * e0, km);
       build_qk<D, QLO>(qk, w, ks, km, a.scale_log2);
     }
-    bias_s = qk.bias_s;
+    add_kmin<D, QLO>(qk, w, sh, sl);
     const long rb = row_base(pages, L, blk, t0 + n, BITS);
     constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
     uint32_t kw[KW];
@@ -333,8 +342,7 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
   float x[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float s = sh[i] + sl[i];
-    const float v = __builtin_fmaf(s, a.scale_log2, bias_s);  // bias_s = 0 for residual keys
+    const float v = (sh[i] + sl[i]) * a.scale_log2;
     x[i] = (t0 + 4 * c + i < n_valid) ? v : -__builtin_inff();
   }
 
@@ -557,7 +565,6 @@ __device__ __forceinline__ void compute_tile(Wave<D, QLO>& w, const DecodeArgs& 
   constexpr int CPL = W::CPL, NQK = W::NQK, CPM = W::CPM;
   const int c = lane >> 4;
   f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
-  float bias_s = 0.f;
   if (in_res) {
     s_from_residual<D, QLO>(w, a, rslot, t0, h, lane, sh, sl);
   } else {
@@ -568,7 +575,7 @@ __device__ __forceinline__ void compute_tile(Wave<D, QLO>& w, const DecodeArgs& 
       load_bytes<2 * CPL>(sp + k.s_rd + 2 * D, km);
       build_qk<D, QLO>(qk, w, ks, km, a.scale_log2);
     }
-    bias_s = qk.bias_s;
+    add_kmin<D, QLO>(qk, w, sh, sl);
     constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
     uint32_t kw[KW];
     load_bytes<CPL * BITS / 8>(sp + k.k_rd, kw);
@@ -592,7 +599,7 @@ __device__ __forceinline__ void compute_tile(Wave<D, QLO>& w, const DecodeArgs& 
   h2_t m01 = {vm[0], vm[G]}, m23 = {vm[2 * G], vm[3 * G]};
   float x[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = __builtin_fmaf(sh[i] + sl[i], a.scale_log2, bias_s);
+  for (int i = 0; i < 4; ++i) x[i] = (sh[i] + sl[i]) * a.scale_log2;
   if (n_rel < 16) {
     // The block's last tile: tokens past the sequence get p = 0 and V = 0 (their
     // page bytes are arbitrary and 0 * inf would poison the sum).
