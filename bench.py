@@ -211,7 +211,7 @@ def run(args) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "decode_kernel<128, 4> + merge_kernel (one INT4 layer-step, graph replay over the 16 INT4 layers)",
             "alg_bytes_per_launch": int(per_layer_bytes),
         },
@@ -219,6 +219,22 @@ def run(args) -> dict:
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(stores[int4[0]], q[int4[0]], table, ctx + args.warmup + args.steps - 1)
     return res
+
+
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_cfg2_int4_traffic.md"
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes of one INT4 decode layer-step (decode + merge), from the committed
+    FETCH_SIZE / WRITE_SIZE passes scaled by the copy calibration (the profile's
+    ``traffic_bytes_per_layer_step`` line); None when the profile is absent."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_layer_step:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(store, q, table, lens) -> dict:
