@@ -1,10 +1,9 @@
 // Split-KV paged decode attention over the tiered (INT2/INT4/INT8) pages, gfx950.
 //
 // Work decomposition: a work item is (sequence, split, group of <= 4 KV heads),
-// one 64-wide wave per KV head; a persistent grid of as many workgroups as the
-// device holds at once walks the batch's non-empty items. The heads of a token
-// row sit side by side in a page ([K codes of all heads | V codes of all
-// heads]), so the waves of a workgroup read neighbouring slices of the same
+// one 64-wide wave per KV head, one workgroup per non-empty item. The heads of
+// a token row sit side by side in a page ([K codes of all heads | V codes of
+// all heads]), so the waves of a workgroup read neighbouring slices of the same
 // cache lines together.
 //
 // Per 16-token tile a wave runs two MFMA contractions with no transposes:
@@ -26,8 +25,10 @@
 // online softmax runs per lane with two cross-row max reductions per tile
 // (v_permlane16_swap / v_permlane32_swap). Query columns are the GQA heads of
 // the KV head, padded to 16. Codes become fp16 by placing them under the
-// exponent of 1024 (0x6400) and subtracting 1024 (exact); v_perm_b32 picks the
-// byte of each code pair, the low nibble of a pre-shifted copy gives odd codes.
+// exponent of 1024 (0x6400): V subtracts 1024 before the dequantizing fma, K
+// keeps 1024 + c and removes 1024 * sum(q * k_scale) with one more MFMA
+// contraction; v_perm_b32 picks the byte of each code pair, the low nibble of a
+// pre-shifted copy gives odd codes.
 // The running max is rescaled lazily: only when some column's max grows by more
 // than 2^8 (probabilities stay <= 256, far inside fp16).
 //
@@ -58,69 +59,79 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// (x & mask) holds two codes at bits 0.. and 16..; as fp16 (1024 + c) - 1024, exact.
-__device__ __forceinline__ h2_t code_pair(uint32_t x, uint32_t mask) {
-  const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-  return u2h((x & mask) | 0x64006400u) - k1024;
+// Code unpacking constants, held in registers: GFX9 VOP3 instructions take no
+// literal operand, so with both in registers (one of them scalar) the
+// mask-and-insert-exponent step is one v_and_or_b32 instead of v_and + v_or.
+struct CodeK {
+  uint32_t mask;   // the code bits of each 16-bit half (scalar register)
+  uint32_t magic;  // 0x64006400: the exponent of 1024 in each half (vector register)
+};
+template <int BITS>
+__device__ __forceinline__ CodeK code_consts() {
+  CodeK k{BITS == 4 ? 0x000F000Fu : (BITS == 8 ? 0x00FF00FFu : 0x00030003u), 0x64006400u};
+  asm volatile("" : "+s"(k.mask));
+  asm volatile("" : "+v"(k.magic));
+  return k;
 }
 
-// Eight consecutive channels of a K row, natural order, as an MFMA fragment.
+// (x & mask) holds two codes at bits 0.. and 16..; as the fp16 pair 1024 + c (exact).
+__device__ __forceinline__ uint32_t biased_pair(uint32_t x, const CodeK& k) { return (x & k.mask) | k.magic; }
+// ... and as c itself.
+__device__ __forceinline__ h2_t code_pair(uint32_t x, const CodeK& k) {
+  const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+  return u2h(biased_pair(x, k)) - k1024;
+}
+
+// Eight consecutive channels of a K row, natural order, as an MFMA fragment of
+// 1024 + code (the bias is taken out of the product by unbias()).
 // INT4: one word (8 nibbles); INT8: two words; INT2: bytes 2*hf, 2*hf+1 of one word.
 template <int BITS>
-__device__ __forceinline__ h8_t kfrag(const uint32_t* w, int hf) {
+__device__ __forceinline__ h8_t kfrag(const uint32_t* w, int hf, const CodeK& k) {
   if constexpr (BITS == 4) {
     const uint32_t x = w[0], x4 = x >> 4;
-    return w2h8(h2u(code_pair(perm(x4, x, pair_sel(0, 0)), 0x000F000Fu)),
-                h2u(code_pair(perm(x4, x, pair_sel(1, 1)), 0x000F000Fu)),
-                h2u(code_pair(perm(x4, x, pair_sel(2, 2)), 0x000F000Fu)),
-                h2u(code_pair(perm(x4, x, pair_sel(3, 3)), 0x000F000Fu)));
+    return w2h8(biased_pair(perm(x4, x, pair_sel(0, 0)), k), biased_pair(perm(x4, x, pair_sel(1, 1)), k),
+                biased_pair(perm(x4, x, pair_sel(2, 2)), k), biased_pair(perm(x4, x, pair_sel(3, 3)), k));
   } else if constexpr (BITS == 8) {
-    const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
     const uint32_t m = 0x64646464u;  // perm(m, x, ...) puts 0x64 above each code byte
-    return w2h8(h2u(u2h(perm(m, w[0], 0x04010400u)) - k1024), h2u(u2h(perm(m, w[0], 0x04030402u)) - k1024),
-                h2u(u2h(perm(m, w[1], 0x04010400u)) - k1024), h2u(u2h(perm(m, w[1], 0x04030402u)) - k1024));
+    return w2h8(perm(m, w[0], 0x04010400u), perm(m, w[0], 0x04030402u), perm(m, w[1], 0x04010400u),
+                perm(m, w[1], 0x04030402u));
   } else {
     const uint32_t x = w[0], x2 = x >> 2, x4 = x >> 4, x6 = x >> 6;
     const int b0 = 2 * hf, b1 = 2 * hf + 1;
-    return w2h8(h2u(code_pair(perm(x2, x, pair_sel(b0, b0)), 0x00030003u)),
-                h2u(code_pair(perm(x6, x4, pair_sel(b0, b0)), 0x00030003u)),
-                h2u(code_pair(perm(x2, x, pair_sel(b1, b1)), 0x00030003u)),
-                h2u(code_pair(perm(x6, x4, pair_sel(b1, b1)), 0x00030003u)));
+    return w2h8(biased_pair(perm(x2, x, pair_sel(b0, b0)), k), biased_pair(perm(x6, x4, pair_sel(b0, b0)), k),
+                biased_pair(perm(x2, x, pair_sel(b1, b1)), k), biased_pair(perm(x6, x4, pair_sel(b1, b1)), k));
   }
 }
 
 // Fragment j (channels 8j..8j+7 of the lane's slice) from the lane's K words.
 template <int BITS>
-__device__ __forceinline__ h8_t kfrag_j(const uint32_t* kw, int j) {
-  if constexpr (BITS == 4) return kfrag<4>(kw + j, 0);
-  else if constexpr (BITS == 8) return kfrag<8>(kw + 2 * j, 0);
-  else return kfrag<2>(kw + (j >> 1), j & 1);
+__device__ __forceinline__ h8_t kfrag_j(const uint32_t* kw, int j, const CodeK& k) {
+  if constexpr (BITS == 4) return kfrag<4>(kw + j, 0, k);
+  else if constexpr (BITS == 8) return kfrag<8>(kw + 2 * j, 0, k);
+  else return kfrag<2>(kw + (j >> 1), j & 1, k);
 }
 
 // V^T operand of the lane's channel j for its 4 tokens: v[i] = token i's slice
 // words, x4 / x2.. = pre-shifted copies; dequantized as c * s + m (one rounding).
 template <int BITS, int VW>
 __device__ __forceinline__ h4_t vfrag(int j, const uint32_t (*v)[VW], const uint32_t (*vs)[4], h2_t s01, h2_t s23,
-                                      h2_t m01, h2_t m23) {
-  uint32_t x01, x23, mask;
+                                      h2_t m01, h2_t m23, const CodeK& k) {
+  uint32_t x01, x23;
   if constexpr (BITS == 4) {
     const int by = j >> 1, sh = j & 1;  // odd channels: low nibble of the word >> 4
     x01 = perm(vs[1][sh], vs[0][sh], pair_sel(by, by));
     x23 = perm(vs[3][sh], vs[2][sh], pair_sel(by, by));
-    mask = 0x000F000Fu;
   } else if constexpr (BITS == 8) {
     const int wd = j >> 2, by = j & 3;
     x01 = perm(v[1][wd], v[0][wd], pair_sel(by, by));
     x23 = perm(v[3][wd], v[2][wd], pair_sel(by, by));
-    mask = 0x00FF00FFu;
   } else {
     const int by = j >> 2, sh = j & 3;  // code j at bits 2*sh of byte by
     x01 = perm(vs[1][sh], vs[0][sh], pair_sel(by, by));
     x23 = perm(vs[3][sh], vs[2][sh], pair_sel(by, by));
-    mask = 0x00030003u;
   }
-  const h2_t v01 = __builtin_elementwise_fma(code_pair(x01, mask), s01, m01);
-  const h2_t v23 = __builtin_elementwise_fma(code_pair(x23, mask), s23, m23);
+  const h2_t v01 = __builtin_elementwise_fma(code_pair(x01, k), s01, m01);
+  const h2_t v23 = __builtin_elementwise_fma(code_pair(x23, k), s23, m23);
   return h4_t{v01[0], v01[1], v23[0], v23[1]};
 }
 
@@ -238,6 +249,20 @@ __device__ __forceinline__ void add_kmin(const QK<D>& qk, const Wave<D, QLO>& w,
   }
 }
 
+// S^T -= 1024 * sum_d (q * k_scale)[d]: the code fragments carry 1024 + c, so the
+// bias leaves through one more contraction (the products are exact in fp32 and
+// the sums ~1024x the unbiased ones, so S keeps ~2^-17 relative accuracy).
+template <int D>
+__device__ __forceinline__ void unbias(const QK<D>& qk, f4_t& sh, f4_t& sl) {
+  const h8_t m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f,
+                      (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f};
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) {
+    sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, qk.hi[j], sh, 0, 0, 0);
+    sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, qk.lo[j], sl, 0, 0, 0);
+  }
+}
+
 // S^T of a tile whose keys are the block's open K group, read from the
 // full-precision residual (row = token % KG) and split into fp16 hi + lo
 // (fp16 / bf16 keys are exact in fp16: lo = 0 is skipped). Lane (c, n): token
@@ -332,12 +357,14 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
 #pragma unroll
       for (int i = 0; i < KW; ++i) kw[i] = 0;
     }
+    const CodeK ck = code_consts<BITS>();
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
-      const h8_t kf = kfrag_j<BITS>(kw, j);
+      const h8_t kf = kfrag_j<BITS>(kw, j, ck);
       sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.hi[j], sh, 0, 0, 0);
       sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.lo[j], sl, 0, 0, 0);
     }
+    unbias<D>(qk, sh, sl);
   }
   float x[4];
 #pragma unroll
@@ -373,9 +400,10 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
   vshift<BITS, VW>(vw, vsh);
   const h2_t s01 = {sv[0], sv[1]}, s23 = {sv[2], sv[3]};
   const h2_t m01 = {mv[0], mv[1]}, m23 = {mv[2], mv[3]};
+  const CodeK vk = code_consts<BITS>();
   h4_t va[CPM];
 #pragma unroll
-  for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23);
+  for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23, vk);
   softmax_pv<D, QLO>(w, x, va);
 }
 
@@ -395,11 +423,17 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
 // ---------------------------------------------------------------------------
 #pragma clang diagnostic ignored "-Winline-asm"
 
+// `lds` is wave-uniform; readfirstlane keeps it in a scalar register even where
+// the compiler computed it with vector instructions.
 __device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, %2" ::"v"(off), "s"(lds), "s"(base) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, %2" ::"v"(off), "s"(__builtin_amdgcn_readfirstlane(lds)),
+               "s"(base)
+               : "memory", "m0");
 }
 __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, %2" ::"v"(off), "s"(lds), "s"(base) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, %2" ::"v"(off), "s"(__builtin_amdgcn_readfirstlane(lds)),
+               "s"(base)
+               : "memory", "m0");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -579,12 +613,14 @@ __device__ __forceinline__ void compute_tile(Wave<D, QLO>& w, const DecodeArgs& 
     constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
     uint32_t kw[KW];
     load_bytes<CPL * BITS / 8>(sp + k.k_rd, kw);
+    const CodeK ck = code_consts<BITS>();
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
-      const h8_t kf = kfrag_j<BITS>(kw, j);
+      const h8_t kf = kfrag_j<BITS>(kw, j, ck);
       sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.hi[j], sh, 0, 0, 0);
       sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.lo[j], sl, 0, 0, 0);
     }
+    unbias<D>(qk, sh, sl);
   }
 
   constexpr int VB = CPM * BITS / 8;
@@ -614,9 +650,10 @@ __device__ __forceinline__ void compute_tile(Wave<D, QLO>& w, const DecodeArgs& 
     for (int i = 0; i < 4; ++i) x[i] = t + i < n_rel ? x[i] : -__builtin_inff();
   }
   vshift<BITS, VW>(vw, vsh);
+  const CodeK vk = code_consts<BITS>();
   h4_t va[CPM];
 #pragma unroll
-  for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23);
+  for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23, vk);
   softmax_pv<D, QLO>(w, x, va);
 }
 
@@ -831,9 +868,82 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   if (h < a.L.H) decode_item<D, BITS, QLO>(a, seq, split, h, lane, my_ring, ring0);
 }
 
-// Merge of the splits: one wave per (sequence, query head). Lanes read the
-// splits' (m, l) in parallel, then every lane sums its channels over the splits
-// in split order.
+// Merge of the splits: one wave per (sequence, query head); lane l holds
+// channels [D/64 * l, D/64 * (l + 1)). Up to 64 splits: the (max, sum) pairs
+// and the first 16 splits' partial rows are requested together, so a row costs
+// about one memory round trip; more splits take a slower two-pass loop.
+template <int D>
+__device__ __forceinline__ void merge_row(const MergeArgs& a, long row, long seq, int head, int used, int lane) {
+  constexpr int C = D / 64;
+  const long base = row * a.num_splits;
+  float num[C] = {};
+  float den = 0.f;
+  if (used <= 64) {
+    const float2 ml = lane < used ? ((const float2*)a.ml)[base + lane] : float2{-__builtin_inff(), 0.f};
+    float w = 0.f;
+    for (int g = 0; g < used; g += 16) {
+      float x[16][C];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const long s = g + u < used ? g + u : 0;  // past the last split: split 0, unused
+        const float* src = a.acc + (base + s) * D + C * lane;
+        if constexpr (C == 2) {
+          const float2 v = *(const float2*)src;
+          x[u][0] = v.x;
+          x[u][1] = v.y;
+        } else {
+          x[u][0] = src[0];
+        }
+      }
+      if (g == 0) {
+        float m = ml.x;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        w = lane < used ? __builtin_amdgcn_exp2f(ml.x - m) : 0.f;
+        den = ml.y * w;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        if (g + u < used) {
+          const float ws = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(w), g + u));
+#pragma unroll
+          for (int e = 0; e < C; ++e) num[e] += x[u][e] * ws;
+        }
+      }
+    }
+  } else {
+    float m = -__builtin_inff();
+    for (int s0 = 0; s0 < used; s0 += 64) {
+      const float mi = s0 + lane < used ? a.ml[(base + s0 + lane) * 2] : -__builtin_inff();
+      m = fmaxf(m, mi);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    for (int s0 = 0; s0 < used; s0 += 64) {
+      const bool in = s0 + lane < used;
+      const float wl = in ? __builtin_amdgcn_exp2f(a.ml[(base + s0 + lane) * 2] - m) : 0.f;
+      den += in ? a.ml[(base + s0 + lane) * 2 + 1] * wl : 0.f;
+      const int cnt = used - s0 < 64 ? used - s0 : 64;
+      for (int i = 0; i < cnt; ++i) {
+        const float ws = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(wl), i));
+        const float* src = a.acc + (base + s0 + i) * D + C * lane;
+#pragma unroll
+        for (int e = 0; e < C; ++e) num[e] += src[e] * ws;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+  }
+  const long o_row = a.q_rows ? a.q_rows[seq] : seq;
+  float o[C];
+#pragma unroll
+  for (int e = 0; e < C; ++e) o[e] = num[e] / den;
+  st_n<C>(a.out, a.out_dtype, o_row * a.o_s0 + head * a.o_s1 + C * lane, o);
+}
+
+template <int D>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int lane = threadIdx.x & 63;
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);  // seq * hq + head
@@ -846,53 +956,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int per = (n_blocks + a.num_splits - 1) / a.num_splits;
   const int bps = a.bps > per ? a.bps : per;
   const int used = (n_blocks + bps - 1) / bps;
-  const long base = row * a.num_splits;
-  float m = -__builtin_inff();
-  for (int s0 = 0; s0 < used; s0 += 64) {
-    const float mi = s0 + lane < used ? a.ml[(base + s0 + lane) * 2] : -__builtin_inff();
-    m = fmaxf(m, mi);
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  float den = 0.f;
-  float num[2] = {0.f, 0.f};
-  const int nd = (a.D + 63) / 64;  // channels per lane (D <= 128)
-  for (int s0 = 0; s0 < used; s0 += 64) {
-    const bool in = s0 + lane < used;
-    const float wl = in ? __builtin_amdgcn_exp2f(a.ml[(base + s0 + lane) * 2] - m) : 0.f;
-    den += in ? a.ml[(base + s0 + lane) * 2 + 1] * wl : 0.f;
-    const int cnt = used - s0 < 64 ? used - s0 : 64;
-    int i = 0;
-    for (; i + 8 <= cnt; i += 8) {  // 8 splits' loads in flight per lane
-      const float* src = a.acc + (base + s0 + i) * a.D;
-      for (int e = 0; e < nd; ++e) {
-        const int d = lane + 64 * e;
-        if (d < a.D) {
-          float x[8];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) x[u] = src[u * a.D + d];
-#pragma unroll
-          for (int u = 0; u < 8; ++u)
-            num[e] += x[u] * __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(wl), i + u));
-        }
-      }
-    }
-    for (; i < cnt; ++i) {
-      const float wsp = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(wl), i));
-      const float* src = a.acc + (base + s0 + i) * a.D;
-      for (int e = 0; e < nd; ++e) {
-        const int d = lane + 64 * e;
-        if (d < a.D) num[e] += src[d] * wsp;
-      }
-    }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
-  const long o_row = a.q_rows ? a.q_rows[seq] : seq;
-  for (int e = 0; e < nd; ++e) {
-    const int d = lane + 64 * e;
-    if (d < a.D) st(a.out, a.out_dtype, o_row * a.o_s0 + head * a.o_s1 + d, num[e] / den);
-  }
+  merge_row<D>(a, row, seq, head, used, lane);
 }
 
 template <int D, int BITS, bool QLO>
@@ -931,7 +995,9 @@ hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
 hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s) {
   (void)num_seqs;
   const long wgs = (a.rows + 3) / 4;
-  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)wgs), dim3(256), 0, s, a);
+  if (a.D == 128) hipLaunchKernelGGL(merge_kernel<128>, dim3((unsigned)wgs), dim3(256), 0, s, a);
+  else if (a.D == 64) hipLaunchKernelGGL(merge_kernel<64>, dim3((unsigned)wgs), dim3(256), 0, s, a);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
