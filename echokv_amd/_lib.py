@@ -22,7 +22,8 @@ _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTS = (
     "echokv_error_string", "echokv_write_tokens", "echokv_finalize_k", "echokv_seal_groups", "echokv_gather",
-    "echokv_store_blocks", "echokv_decode", "echokv_prefill", "echokv_dequant_dense", "echokv_canary_kl",
+    "echokv_store_blocks", "echokv_decode", "echokv_prefill", "echokv_prefill_dense", "echokv_prefill_dense_workspace",
+    "echokv_dequant_dense", "echokv_canary_kl",
 )
 
 
@@ -56,6 +57,8 @@ _SIGS = {
     "echokv_decode": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, P, P, P, I64,
                       I64, I32, P],
     "echokv_prefill": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, I32, P, I64, FL, P],
+    "echokv_prefill_dense": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, P, I64, I32, P, I64,
+                             P, I64, FL, P],
     "echokv_dequant_dense": [LP, P, P, P, RP, P, I64, P, I64, P, P, I64, I64, I32, P],
     "echokv_canary_kl": [P, I32, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32, I32, I32, I32, I32, I32, FL, P, P],
 }
@@ -78,6 +81,8 @@ def lib() -> C.CDLL:
             fn = getattr(l, name)
             fn.argtypes = args
             fn.restype = C.c_int
+        l.echokv_prefill_dense_workspace.argtypes = [LP, I64]
+        l.echokv_prefill_dense_workspace.restype = C.c_int64
         _lib = l
     return _lib
 

@@ -218,6 +218,58 @@ int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* 
   return launched(ek::launch_prefill(a, n_tiles, (hipStream_t)stream));
 }
 
+int64_t echokv_prefill_dense_workspace(const echokv_layout* L, int64_t n_packs) {
+  if (!lay_ok(L)) return -ECHOKV_ESHAPE;
+  if (L->head_size != 64 && L->head_size != 128) return -ECHOKV_ESHAPE;
+  if (n_packs < 0) return -ECHOKV_EINVAL;
+  return n_packs * L->num_kv_heads * ek::dense_tile_bytes(L->head_size);
+}
+
+int echokv_prefill_dense(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                         const int64_t* res_group, const echokv_residual* res, const void* query, int64_t q_s0,
+                         int64_t q_s1, int32_t q_dtype, int32_t num_q_heads, void* out, int64_t o_s0, int64_t o_s1,
+                         int32_t out_dtype, const int32_t* packs, int64_t n_packs, const int32_t* qtiles,
+                         int64_t n_qtiles, int32_t tile_m, const int32_t* block_table, int64_t bt_s0, void* workspace,
+                         int64_t workspace_bytes, float softmax_scale, echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (L->head_size != 64 && L->head_size != 128) return ECHOKV_ESHAPE;
+  if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
+  const int gqa = num_q_heads / L->num_kv_heads;
+  if (gqa > 32 * ek::kDenseWaves || tile_m != ek::dense_tile_tokens(gqa)) return ECHOKV_ESHAPE;
+  if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
+  if (n_packs < 0 || n_qtiles < 0 || n_qtiles > INT32_MAX / L->num_kv_heads || !res_ok(res)) return ECHOKV_EINVAL;
+  if (n_qtiles == 0) return ECHOKV_OK;
+  if (workspace_bytes < n_packs * L->num_kv_heads * ek::dense_tile_bytes(L->head_size)) return ECHOKV_EINVAL;
+  if (!pages || !block_res || !res_group || !query || !out || !packs || !qtiles || !block_table ||
+      (n_packs > 0 && !workspace))
+    return ECHOKV_EINVAL;
+  const hipStream_t s = (hipStream_t)stream;
+  uint8_t* ws = (uint8_t*)workspace;
+  if (n_packs > 0) {
+    ek::PackArgs p{to_lay(L), pages, block_res, res_group, to_res(res), packs, block_table, bt_s0, ws};
+    const int rc = launched(ek::launch_prefill_pack(p, n_packs, s));
+    if (rc != ECHOKV_OK) return rc;
+  }
+  ek::FlashArgs f;
+  f.ws = ws;
+  f.q = query;
+  f.q_s0 = q_s0;
+  f.q_s1 = q_s1;
+  f.q_dtype = q_dtype;
+  f.out = out;
+  f.o_s0 = o_s0;
+  f.o_s1 = o_s1;
+  f.out_dtype = out_dtype;
+  f.qtiles = qtiles;
+  f.n_qtiles = (int)n_qtiles;
+  f.H = L->num_kv_heads;
+  f.gqa = gqa;
+  f.D = L->head_size;
+  f.n_packs = n_packs;
+  f.scale_log2 = softmax_scale * 1.4426950408889634f;
+  return launched(ek::launch_prefill_flash(f, s));
+}
+
 int echokv_dequant_dense(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
                          const int64_t* res_group, const echokv_residual* res, const int32_t* work, int64_t n_work,
                          const int32_t* block_table, int64_t bt_s0, void* k_out, void* v_out, int64_t o_s0,

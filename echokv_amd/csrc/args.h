@@ -14,6 +14,13 @@ constexpr int kPrefillRows = 128;    // prefill: query rows (tokens x GQA heads)
 // Query tokens per prefill tile for a GQA group size.
 inline int prefill_tile_tokens(int gqa) { return kPrefillRows / gqa; }
 
+// Long-chunk (two-pass) prefill: keys per workspace tile, waves (32 query rows
+// each) per attention workgroup, and the workspace bytes of one tile and head.
+constexpr int kDenseKeys = 64;
+constexpr int kDenseWaves = 8;
+inline int dense_tile_tokens(int gqa) { return 32 * kDenseWaves / gqa; }
+inline long dense_tile_bytes(int D) { return (long)kDenseKeys * D * 6; }
+
 struct WriteTokArgs {
   Lay L;
   uint8_t* pages;
@@ -149,6 +156,32 @@ struct PrefillArgs {
   float scale_log2;
 };
 
+struct PackArgs {
+  Lay L;
+  const uint8_t* pages;
+  const int64_t* block_res;
+  const int64_t* res_group;
+  Res res;
+  const int32_t* packs;  // [n, 3]: block-table row, first key, ctx
+  const int32_t* bt;
+  long bt_s0;
+  uint8_t* ws;  // [n][H][dense_tile_bytes(D)]
+};
+
+struct FlashArgs {
+  const uint8_t* ws;
+  const void* q;
+  long q_s0, q_s1;
+  int q_dtype;
+  void* out;
+  long o_s0, o_s1;
+  int out_dtype;
+  const int32_t* qtiles;  // [n, 5]: first query row, tokens, first query position, ctx, first workspace tile
+  int n_qtiles, H, gqa, D;
+  long n_packs;  // workspace tiles present: reads stay below this
+  float scale_log2;
+};
+
 hipError_t launch_write_tokens(const WriteTokArgs& a, long n_rows, hipStream_t s);
 hipError_t launch_finalize_k(const FinArgs& a, long rows, hipStream_t s);
 hipError_t launch_seal(const SealArgs& a, long n, hipStream_t s);
@@ -159,5 +192,7 @@ hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s);
 hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s);
 hipError_t launch_canary(const CanaryArgs& a, int num_layers, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs& a, long n_tiles, hipStream_t s);
+hipError_t launch_prefill_pack(const PackArgs& a, long n_packs, hipStream_t s);
+hipError_t launch_prefill_flash(const FlashArgs& a, hipStream_t s);
 
 }  // namespace ek

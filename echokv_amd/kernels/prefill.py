@@ -7,22 +7,32 @@ context (this chunk included, already written) with the bottom-right causal
 limit: query ``i`` of an ``nq``-token chunk over ``ctx`` keys sees keys
 ``<= ctx - nq + i``.
 
-One fused HIP kernel (``echokv_amd/csrc/prefill.hip``) serves every chunk
-length: each workgroup takes a tile of ``128 // GQA`` query tokens of one
-request for one KV head, dequantizes each 32-key tile of the context once
-into LDS (fp16) and runs QK^T and PV on MFMA. ``dequant_dense`` keeps the
-reference's dense-dequantization entry point (``[total_ctx, H, D]`` K/V).
+Two paths, chosen as the reference chooses (``FUSED_MAX_CHUNK``,
+prefill.py:74): when every chunk is at most 64 tokens, one fused HIP kernel
+(``echokv_amd/csrc/prefill.hip``): each workgroup takes a tile of
+``128 // GQA`` query tokens of one request for one KV head, dequantizes each
+32-key tile of the context into LDS (fp16) and runs QK^T and PV on MFMA.
+Longer chunks take the two-pass path (``echokv_amd/csrc/prefill_dense.hip``,
+the reference's dense dequantization + flash attention, prefill.py:133-167):
+every 64-key tile of each context is dequantized once into a workspace, then
+a flash-attention kernel with ``256 // GQA``-token query tiles streams it
+through LDS. ``dequant_dense`` keeps the reference's dense-dequantization
+entry point (``[total_ctx, H, D]`` K/V).
 """
 
 from __future__ import annotations
+
+from typing import NamedTuple
 
 import torch
 
 from echokv_amd import _lib
 from echokv_amd._util import to_device
 
-ROWS = 128  # query rows (tokens x GQA heads) per workgroup
-FUSED_MAX_CHUNK = 1 << 30  # the fused kernel handles every chunk length
+ROWS = 128  # query rows (tokens x GQA heads) per workgroup of the fused kernel
+FUSED_MAX_CHUNK = 64  # the fused kernel only when every chunk is this short
+DENSE_ROWS = 256  # query rows per workgroup of the two-pass path
+DENSE_KEYS = 64  # keys per workspace tile
 
 
 def gqa_pad(gqa: int) -> int:
@@ -48,6 +58,50 @@ def build_tiles(prefill, req_of, gqa: int, device) -> torch.Tensor:
             rows.append((qs + t0, min(bm, nq - t0), pos0 + t0, ctx, r))
     tiles = to_device(torch.tensor(rows, dtype=torch.int32).reshape(-1, 5), device)
     return tiles
+
+
+class DensePlan(NamedTuple):
+    """Device tables of the two-pass path: ``packs [n, 3]`` (block-table row,
+    first key, ctx) per 64-key workspace tile and ``qtiles [n, 5]`` (q_row0,
+    n_tokens, q_pos0, ctx, first workspace tile of the request's context)."""
+
+    packs: torch.Tensor
+    qtiles: torch.Tensor
+    tile_m: int
+
+
+def dense_block_m(gqa: int) -> int:
+    """Query tokens per tile of the two-pass path."""
+    return max(1, DENSE_ROWS // gqa)
+
+
+def build_dense_plan(prefill, req_of, gqa: int, device) -> DensePlan:
+    """Workspace tiles and query tiles for the two-pass path.
+
+    Query tiles are listed per request, heaviest (most keys) first, requests
+    with the most work first, so the longest workgroups start earliest."""
+    bm = dense_block_m(gqa)
+    packs, groups = [], []
+    for (qs, qe, ctx, *_), r in zip(prefill, req_of):
+        nq = qe - qs
+        t0 = len(packs)
+        packs.extend((r, k0, ctx) for k0 in range(0, ctx, DENSE_KEYS))
+        pos0 = ctx - nq
+        tiles = [(qs + s, min(bm, nq - s), pos0 + s, ctx, t0) for s in range(0, nq, bm)]
+        tiles.sort(key=lambda t: -(min(t[3], t[2] + t[1])))
+        groups.append((sum(min(t[3], t[2] + t[1]) * t[1] for t in tiles), tiles))
+    groups.sort(key=lambda g: -g[0])
+    rows = [t for _, tiles in groups for t in tiles]
+    packs_t = to_device(torch.tensor(packs, dtype=torch.int32).reshape(-1, 3), device)
+    qtiles_t = to_device(torch.tensor(rows, dtype=torch.int32).reshape(-1, 5), device)
+    return DensePlan(packs_t, qtiles_t, bm)
+
+
+def dense_workspace_bytes(store, n_packs: int) -> int:
+    n = _lib.lib().echokv_prefill_dense_workspace(_lib.byref(store.abi), n_packs)
+    if n < 0:
+        raise RuntimeError(f"echokv_prefill_dense_workspace: {_lib.lib().echokv_error_string(int(-n)).decode()}")
+    return int(n)
 
 
 def build_dequant_work(prefill, req_of, block_size: int, device) -> torch.Tensor:
@@ -86,12 +140,70 @@ def dequant_dense(store, work: torch.Tensor, total_ctx: int, block_table: torch.
     return k, v
 
 
+def _out_view(output: torch.Tensor, hq: int) -> torch.Tensor:
+    out = output.view(output.shape[0], hq, -1) if output.dim() == 2 else output
+    if out.stride(2) != 1:
+        raise ValueError("output rows must be contiguous along head_dim")
+    return out
+
+
+def use_dense(prefill, head_size: int) -> bool:
+    """The two-pass path serves a batch with any chunk longer than FUSED_MAX_CHUNK."""
+    return head_size in (64, 128) and any(qe - qs > FUSED_MAX_CHUNK for qs, qe, *_ in prefill)
+
+
+def prefill_attention_dense(store, query: torch.Tensor, output: torch.Tensor, prefill, req_of,
+                            block_table: torch.Tensor, softmax_scale: float, plan: DensePlan | None = None) -> None:
+    """Two-pass prefill (echokv_vllm/kernels/prefill.py:133-167): dequantize each
+    context once into a workspace of 64-key tiles, then flash attention over it."""
+    if not prefill:
+        return
+    L = store.layout
+    _lib.require_device(query, output, block_table, store.pages)
+    hq = query.shape[1]
+    gqa = hq // L.num_kv_heads
+    if plan is None:
+        plan = build_dense_plan(prefill, req_of, gqa, query.device)
+    n_q = plan.qtiles.shape[0]
+    if n_q == 0:
+        return
+    if query.stride(2) != 1:
+        query = query.contiguous()
+    out = _out_view(output, hq)
+    block_table = _bt(block_table)
+    n_packs = plan.packs.shape[0]
+    ws_bytes = dense_workspace_bytes(store, n_packs)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=query.device)
+    res = _lib.residual(store.res_k)
+    _lib.call(
+        "echokv_prefill_dense", _lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(store.block_res),
+        _lib.ptr(store.res_group), _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1),
+        _lib.dtype_code(query), hq, _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out),
+        _lib.ptr(plan.packs), n_packs, _lib.ptr(plan.qtiles), n_q, plan.tile_m, _lib.ptr(block_table),
+        block_table.stride(0), _lib.ptr(ws), ws_bytes, float(softmax_scale), _lib.stream(),
+    )
+
+
 def prefill_attention(store, query: torch.Tensor, output: torch.Tensor, prefill, req_of, block_table: torch.Tensor,
                       softmax_scale: float, tiles: torch.Tensor | None = None, gather=None, dense=None) -> None:
     """Write attention for every prefill chunk into ``output [T, Hq, D]``.
 
-    ``gather`` / ``dense`` (the reference's alternative inputs) are accepted and
-    unused: the fused kernel covers every chunk."""
+    A batch with a chunk longer than ``FUSED_MAX_CHUNK`` takes the two-pass
+    path (``dense`` may carry its prebuilt ``DensePlan``); otherwise the fused
+    kernel over ``tiles``. ``gather`` (the reference's PyTorch-path index) is
+    accepted and unused."""
+    if not prefill:
+        return
+    if use_dense(prefill, store.layout.head_size):
+        prefill_attention_dense(store, query, output, prefill, req_of, block_table, softmax_scale,
+                                dense if isinstance(dense, DensePlan) else None)
+    else:
+        prefill_attention_fused(store, query, output, prefill, req_of, block_table, softmax_scale, tiles)
+
+
+def prefill_attention_fused(store, query: torch.Tensor, output: torch.Tensor, prefill, req_of,
+                            block_table: torch.Tensor, softmax_scale: float, tiles: torch.Tensor | None = None) -> None:
+    """The fused kernel (echokv_vllm/kernels/prefill.py:242-327) over ``tiles``."""
     if not prefill:
         return
     L = store.layout
@@ -104,9 +216,7 @@ def prefill_attention(store, query: torch.Tensor, output: torch.Tensor, prefill,
         return
     if query.stride(2) != 1:
         query = query.contiguous()
-    out = output.view(output.shape[0], hq, -1) if output.dim() == 2 else output
-    if out.stride(2) != 1:
-        raise ValueError("output rows must be contiguous along head_dim")
+    out = _out_view(output, hq)
     block_table = _bt(block_table)
     tiles = tiles.to(torch.int32).contiguous()
     res = _lib.residual(store.res_k)

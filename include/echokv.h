@@ -126,6 +126,27 @@ int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* 
                    const int32_t* block_table, int64_t bt_s0, float softmax_scale,
                    echokv_stream_t stream);
 
+/* Long-chunk prefill in two passes (the dense path for chunks longer than the fused
+ * kernel's): each 64-key tile of every context is dequantized once into `workspace`
+ * (packs [n_packs, 3] int32 = (block-table row, first key, ctx); tile i of head h at
+ * byte (i * H + h) * 64 * D * 6: K rows as fp16 hi + lo, V transposed fp16), then
+ * flash attention on MFMA reads it: qtiles [n_qtiles, 5] int32 = (first query row,
+ * tokens <= tile_m = 256 / GQA, first query position, ctx, first workspace tile of
+ * the request's context), bottom-right causal. Workspace reads stay below n_packs tiles.
+ * Replaces echokv_vllm/kernels/prefill.py:133-167 (prefill_attention_dense:
+ * dequant_dense prefill.py:90-115 + flash-attention varlen).
+ * echokv_prefill_dense_workspace: the workspace bytes for n_packs tiles, or minus an
+ * error code. */
+int64_t echokv_prefill_dense_workspace(const echokv_layout* L, int64_t n_packs);
+int echokv_prefill_dense(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                         const int64_t* res_group, const echokv_residual* res,
+                         const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype, int32_t num_q_heads,
+                         void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                         const int32_t* packs, int64_t n_packs, const int32_t* qtiles, int64_t n_qtiles,
+                         int32_t tile_m, const int32_t* block_table, int64_t bt_s0,
+                         void* workspace, int64_t workspace_bytes, float softmax_scale,
+                         echokv_stream_t stream);
+
 /* Dense dequantization of prefill contexts: work [n, 4] int32 = (block-table row,
  * block index, dense row of the block's first token, ctx) -> K, V [*, H, D].
  * Replaces echokv_vllm/kernels/prefill.py:90-115 (dequant_dense), kernel 330-369. */

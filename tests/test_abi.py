@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported(lib):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(_lib.EXPORTS)
-    assert set(_lib._SIGS) == set(names) - {"echokv_error_string"}
+    assert set(_lib._SIGS) == set(names) - {"echokv_error_string", "echokv_prefill_dense_workspace"}
 
 
 def test_error_strings(lib):
@@ -75,3 +75,25 @@ def test_store_entry_points_reject_bad_layouts(lib):
     assert rc == 2
     rc = lib.echokv_store_blocks(C.byref(_layout()), p, p, 1, p, p, 3, None)
     assert rc != 0  # bits must be 2, 4 or 8
+
+
+def _prefill_dense(lib, L, hq=32, tile_m=64, n_packs=4, n_q=2, ws_bytes=None):
+    res = _lib.Residual(C.c_void_p(16), 1, 2, 16 * 8 * 128, 8 * 128, 128)
+    p = C.c_void_p(64)  # never dereferenced: every call below fails its checks first
+    if ws_bytes is None:
+        ws_bytes = lib.echokv_prefill_dense_workspace(C.byref(L), n_packs)
+    return lib.echokv_prefill_dense(C.byref(L), p, p, p, C.byref(res), p, 4096, 128, 1, hq, p, 4096, 128, 1, p,
+                                    n_packs, p, n_q, tile_m, p, 64, p, ws_bytes, 0.088, None)
+
+
+def test_prefill_dense_workspace_size_and_argument_checks(lib):
+    L = _layout()
+    assert lib.echokv_prefill_dense_workspace(C.byref(L), 3) == 3 * 8 * 64 * 128 * 6
+    assert lib.echokv_prefill_dense_workspace(C.byref(_layout(head_size=96)), 3) < 0
+    assert lib.echokv_prefill_dense_workspace(C.byref(L), -1) < 0
+    assert _prefill_dense(lib, _layout(head_size=96)) == 2   # D must be 64 or 128
+    assert _prefill_dense(lib, L, hq=30) == 2                 # heads not a multiple of KV heads
+    assert _prefill_dense(lib, L, tile_m=32) == 2             # GQA 4 tiles hold 64 tokens
+    assert _prefill_dense(lib, L, ws_bytes=1000) != 0         # workspace too small
+    assert _prefill_dense(lib, L, n_packs=-1) != 0
+    assert _prefill_dense(lib, L, n_q=0) == 0                 # nothing to do: no launch

@@ -137,16 +137,21 @@ def test_graph_padding_and_fixed_split_grid(device, case_stores):
 
 # ---- prefill -------------------------------------------------------------------------
 
-def test_cfg1_prefill_matches_reference_output(device):
+PATHS = {"fused": pf.prefill_attention_fused, "dense": pf.prefill_attention_dense}
+
+
+@pytest.mark.parametrize("path", sorted(PATHS))
+def test_cfg1_prefill_matches_reference_output(device, path):
     s = next(x for x in S.all_scripts() if x.name == "cfg1_int4_bs16")
     g = golden(s.name)
     store, *_ = gpu_replay(s, device)
     prefill, req_of, q = S.cfg1_prefill(s)
     table = t(s.meta["table"], device, torch.int32)
     for qdt in (torch.float32, torch.float16, torch.bfloat16):
+        print(f"[prefill cfg1] {path} {qdt}", flush=True)
         qt = t(q, device, qdt)
         out = torch.zeros(q.shape, device=device, dtype=torch.float32)
-        pf.prefill_attention(store, qt, out, prefill, req_of, table, s.d ** -0.5)
+        PATHS[path](store, qt, out, prefill, req_of, table, s.d ** -0.5)
         torch.cuda.synchronize()
         if qdt == torch.float32:
             err = maxdiff(out, g["prefill_out"])
@@ -159,6 +164,31 @@ def test_cfg1_prefill_matches_reference_output(device):
         assert err <= TOL, f"{qdt}: max err {err}"
 
 
+@pytest.mark.parametrize("chunk", [200, 1000])
+def test_cfg1_long_chunk_prefill_matches_oracle(device, chunk):
+    """Long chunks (the two-pass path): each sequence's last ``chunk`` tokens (or
+    all of them) over its whole context, several query and key tiles per request."""
+    s = next(x for x in S.all_scripts() if x.name == "cfg1_int4_bs16")
+    sim = replay(s)
+    store, *_ = gpu_replay(s, device)
+    prefill, req_of, row = [], [], 0
+    for r, n in enumerate(S.CFG1_LENS):
+        nq = min(chunk, n)
+        prefill.append((row, row + nq, n, 0))
+        req_of.append(r)
+        row += nq
+    q = np.random.default_rng(chunk).standard_normal((row, 32, s.d), dtype=np.float32)
+    qt = t(q, device, torch.bfloat16)
+    out = torch.zeros(q.shape, device=device, dtype=torch.float32)
+    print(f"[prefill long] chunk={chunk}", flush=True)
+    pf.prefill_attention(store, qt, out, prefill, req_of, t(s.meta["table"], device, torch.int32), s.d ** -0.5)
+    torch.cuda.synchronize()
+    assert pf.use_dense(prefill, s.d)
+    ref = OA.prefill_attention(sim.ps, qt.float().cpu().numpy(), prefill, req_of, s.meta["table"], s.d ** -0.5)
+    err = maxdiff(out, ref)
+    assert err <= TOL, f"chunk {chunk}: max err {err}"
+
+
 PREFILL_CASES = [  # decode case index, ctx == its lens, chunk lengths
     (0, [1, 40, 64, 65, 200], [1, 40, 1, 65, 77]),
     (3, [200, 70], [17, 70]),
@@ -167,12 +197,13 @@ PREFILL_CASES = [  # decode case index, ctx == its lens, chunk lengths
 ]
 
 
+@pytest.mark.parametrize("path", sorted(PATHS))
 @pytest.mark.parametrize("case", PREFILL_CASES)
 @pytest.mark.parametrize("gqa", [1, 4, 7])
-def test_prefill_matches_oracle(device, case_stores, case, gqa):
+def test_prefill_matches_oracle(device, case_stores, case, gqa, path):
     i, ctxs, chunks = case
     s, sim, store = case_stores[i]
-    print(f"[prefill] {s.name} gqa={gqa}", flush=True)
+    print(f"[prefill] {path} {s.name} gqa={gqa}", flush=True)
     prefill, req_of, row = [], [], 0
     for r, (ctx, nq) in enumerate(zip(ctxs, chunks)):
         prefill.append((row, row + nq, ctx, 0))
@@ -181,21 +212,11 @@ def test_prefill_matches_oracle(device, case_stores, case, gqa):
     q = np.random.default_rng(gqa).standard_normal((row, gqa * s.h, s.d), dtype=np.float32)
     qt = t(q, device, torch.float16)
     out = torch.zeros(row, gqa * s.h, s.d, device=device)
-    pf.prefill_attention(store, qt, out, prefill, req_of, t(s.meta["table"], device, torch.int32), s.d ** -0.5)
+    PATHS[path](store, qt, out, prefill, req_of, t(s.meta["table"], device, torch.int32), s.d ** -0.5)
     torch.cuda.synchronize()
     ref = OA.prefill_attention(sim.ps, qt.float().cpu().numpy(), prefill, req_of, s.meta["table"], s.d ** -0.5)
     err = maxdiff(out, ref)
     assert err <= TOL, f"{s.name} gqa={gqa}: max err {err}"
-
-
-def test_tiles_cover_every_query_row():
-    prefill = [(0, 70, 70, 0), (70, 110, 200, 0), (110, 111, 33, 0)]
-    for gqa in (1, 4, 7):
-        tiles = pf.build_tiles(prefill, [0, 1, 2], gqa, "cpu")
-        covered = sorted(r for q0, n, *_ in tiles.tolist() for r in range(q0, q0 + n))
-        assert covered == list(range(111))
-        assert all(n <= pf.block_m(gqa) for _, n, *_ in tiles.tolist())
-        assert tiles[0].tolist()[2] == 0 and any(x[2] == 160 for x in tiles.tolist())
 
 
 @pytest.mark.parametrize("i", [0, 1, 4])
