@@ -12,7 +12,7 @@
 //
 // Pass 2, flash_kernel: one workgroup (8 waves) per (query tile, KV head). A
 // query tile holds up to 256 / GQA tokens; its rows are (token, GQA head)
-// pairs, 32 per wave. Workspace tiles stream through a two-slot LDS ring by
+// pairs, 32 per wave. Workspace tiles stream through a three-slot LDS ring by
 // LDS DMA (global_load_lds_dwordx4, 6 per wave per tile), the next tile in
 // flight while the current one is consumed. Per wave and tile:
 //   S^T[key, row] = K Q^T    v_mfma_f32_32x32x16_f16 on K hi and K lo (and Q lo
@@ -33,6 +33,8 @@ namespace ek {
 namespace {
 
 typedef float f16v_t __attribute__((ext_vector_type(16)));
+
+constexpr int kDenseRing = 3;  // workspace tiles in the LDS ring
 
 template <int D>
 struct Ws {
@@ -77,6 +79,76 @@ __device__ __forceinline__ float halves_sum(float x) {
 
 // ---- pass 1 ------------------------------------------------------------------
 
+// One thread's CPT channels of one key at BITS: codes by vector loads (CPT * BITS / 8
+// bytes, aligned to their size by the page format), K scale / min rows as fp16x8.
+template <int BITS, int CPT>
+struct Codes {
+  static constexpr int BYTES = CPT * BITS / 8;
+  static constexpr int WORDS = BYTES / 4;
+  uint32_t w[WORDS];
+  __device__ __forceinline__ void load(const uint8_t* p) {
+    if constexpr (BYTES % 16 == 0) {
+#pragma unroll
+      for (int i = 0; i < BYTES / 16; ++i) {
+        const uint4 v = ((const uint4*)p)[i];
+        w[4 * i] = v.x, w[4 * i + 1] = v.y, w[4 * i + 2] = v.z, w[4 * i + 3] = v.w;
+      }
+    } else if constexpr (BYTES == 8) {
+      const uint2 v = *(const uint2*)p;
+      w[0] = v.x, w[1] = v.y;
+    } else {
+      w[0] = *(const uint32_t*)p;
+    }
+  }
+  __device__ __forceinline__ float operator[](int e) const {
+    return (float)((w[(e * BITS) / 32] >> ((e * BITS) % 32)) & ((1u << BITS) - 1u));
+  }
+};
+
+template <int BITS, int D>
+__device__ __forceinline__ void dequant_key(const PackArgs& a, long blk, int off, long rb, bool in_res, long rs,
+                                            int h, int cq, float* kx, float* vx) {
+  constexpr int CPT = D / 4;
+  const Lay& L = a.L;
+  const int c0 = cq * CPT;
+  const long hb = (long)h * (D * BITS / 8) + c0 * BITS / 8;
+  Codes<BITS, CPT> vc;
+  vc.load(a.pages + rb + (long)L.H * D * BITS / 8 + hb);
+  const int G = D / L.VG;
+  const long pg = blk * L.stride;
+  if (L.VG >= CPT) {  // the thread's channels share one (scale, min)
+    const long ve = ((long)off * L.H + h) * G + c0 / L.VG;
+    const float vs = (float)*f16p(a.pages, pg + L.o_vs + 2 * ve);
+    const float vm = (float)*f16p(a.pages, pg + L.o_vm + 2 * ve);
+#pragma unroll
+    for (int e = 0; e < CPT; ++e) vx[e] = vc[e] * vs + vm;
+  } else {
+#pragma unroll
+    for (int e = 0; e < CPT; ++e) {
+      const long ve = ((long)off * L.H + h) * G + (c0 + e) / L.VG;
+      vx[e] = vc[e] * (float)*f16p(a.pages, pg + L.o_vs + 2 * ve) + (float)*f16p(a.pages, pg + L.o_vm + 2 * ve);
+    }
+  }
+  if (in_res) {
+#pragma unroll
+    for (int q4 = 0; q4 < CPT / 4; ++q4)
+      ld4(a.res.ptr, a.res.dtype, rs * a.res.s0 + (long)(off % L.KG) * a.res.s1 + h * a.res.s2 + c0 + 4 * q4,
+          &kx[4 * q4]);
+    return;
+  }
+  Codes<BITS, CPT> kc;
+  kc.load(a.pages + rb + hb);
+  const long se = ((long)(off / L.KG) * L.H + h) * D + c0;
+  const h8_t* ks = (const h8_t*)(a.pages + pg + L.o_ks + 2 * se);
+  const h8_t* km = (const h8_t*)(a.pages + pg + L.o_km + 2 * se);
+#pragma unroll
+  for (int v8 = 0; v8 < CPT / 8; ++v8) {
+    const h8_t s8 = ks[v8], m8 = km[v8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kx[8 * v8 + e] = kc[8 * v8 + e] * (float)s8[e] + (float)m8[e];
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
   using W = Ws<D>;
@@ -100,33 +172,10 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
       const long rb = row_base(a.pages, L, blk, off, bits);
       if (rb >= 0) {
         const long rs = a.block_res[blk];
-        const int grp = off / L.KG;
-        const bool in_res = rs >= 0 && rs < a.res.rows && a.res_group[rs] == grp;
-        const int G = D / L.VG;
-        const long hb = (long)h * (D * bits / 8);
-#pragma unroll
-        for (int q4 = 0; q4 < CPT / 4; ++q4) {
-          const int ch = cq * CPT + 4 * q4;
-          const uint32_t vc = load_codes4(a.pages + rb + (long)L.H * D * bits / 8 + hb + ch * bits / 8, bits);
-          const long ve = ((long)off * L.H + h) * G + ch / L.VG;
-          const float vs = (float)*f16p(a.pages, blk * L.stride + L.o_vs + 2 * ve);
-          const float vm = (float)*f16p(a.pages, blk * L.stride + L.o_vm + 2 * ve);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) vx[4 * q4 + e] = code_at(vc, e, bits) * vs + vm;
-          if (in_res) {
-            ld4(a.res.ptr, a.res.dtype, rs * a.res.s0 + (long)(off % L.KG) * a.res.s1 + h * a.res.s2 + ch,
-                &kx[4 * q4]);
-          } else {
-            const uint32_t kc = load_codes4(a.pages + rb + hb + ch * bits / 8, bits);
-            const long se = ((long)grp * L.H + h) * D + ch;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float ks = (float)*f16p(a.pages, blk * L.stride + L.o_ks + 2 * (se + e));
-              const float km = (float)*f16p(a.pages, blk * L.stride + L.o_km + 2 * (se + e));
-              kx[4 * q4 + e] = code_at(kc, e, bits) * ks + km;
-            }
-          }
-        }
+        const bool in_res = rs >= 0 && rs < a.res.rows && a.res_group[rs] == off / L.KG;
+        if (bits == 8) dequant_key<8, D>(a, blk, off, rb, in_res, rs, h, cq, kx, vx);
+        else if (bits == 4) dequant_key<4, D>(a, blk, off, rb, in_res, rs, h, cq, kx, vx);
+        else dequant_key<2, D>(a, blk, off, rb, in_res, rs, h, cq, kx, vx);
       }
     }
   }
@@ -155,13 +204,16 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
 
 // ---- pass 2 ------------------------------------------------------------------
 
-template <int D, bool QLO>
+template <int D, bool QLO, int NBUF>
 __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
   using W = Ws<D>;
   constexpr int NS = D / 16;   // 16-channel steps of S^T
   constexpr int NDB = D / 32;  // 32-channel blocks of O^T
+  static_assert(NBUF == 2 || NBUF == 3, "two or three ring slots");
   constexpr int NDMA = W::BYTES / 1024 / kDenseWaves;
   static_assert(W::BYTES % (1024 * kDenseWaves) == 0, "tile must split into whole DMA rounds");
+  constexpr int KGROUPS = NS / 2;          // 8-fragment K groups per 64-key tile
+  static_assert(2 * NDB <= 8, "V^T fragments of two steps fit one group");
   constexpr float kInf = __builtin_inff();
   extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
 
@@ -219,11 +271,13 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
   const long tstride = (long)a.H * W::BYTES;
   auto issue = [&](int kt) {
     const uint8_t* g = uniform_ptr(gbase + kt * tstride);
-    const uint32_t m = ring0 + (uint32_t)((kt & 1) * W::BYTES + 1024 * NDMA * wave);
+    const uint32_t m = ring0 + (uint32_t)((kt % NBUF) * W::BYTES + 1024 * NDMA * wave);
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) dma16(g, doff[i], m + 1024 * i);
   };
-  if (n_kt > 0) issue(0);
+#pragma unroll
+  for (int i = 0; i < NBUF - 1; ++i)
+    if (i < n_kt) issue(i);
 
   // Query fragments (B operand of S^T): row r, channels 16 s + 8 hh .. +8.
   h8_t qf[NS], ql[QLO ? NS : 1];
@@ -253,33 +307,61 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
   for (int db = 0; db < NDB; ++db) acc[db] = f16v_t{};
   float m_run = -kInf, lsum = 0.f;
   const float sl2 = a.scale_log2;
+  f16v_t s[2];
+  h8_t fr[2][8];
 
-  for (int kt = 0; kt < n_kt; ++kt) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (kt + 1 < n_kt) issue(kt + 1);
-    const int kbase = kt * kDenseKeys;
-    if (!active || kbase >= kend_w) continue;
-    const uint8_t* buf = ring + (kt & 1) * W::BYTES;
-
-    // S^T = K Q^T over two 32-key blocks.
-    f16v_t s[2];
+  // S^T = K Q^T over two 32-key blocks. K fragments go in groups of 8 (hi and
+  // lo of two 16-channel steps for both blocks): the next group's LDS reads
+  // are in flight while the current group feeds the MFMAs, which alternate
+  // between the two blocks' accumulators (scheduling fences keep that order).
+  auto kload = [&](const uint8_t* buf, int g, h8_t* dst) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int i = 0; i < 4; ++i) {
+      const int st = 2 * g + (i >> 1), kb = i & 1;
       const int k = 32 * kb + j;
       const uint8_t* kr = buf + k * W::KROW;
-      s[kb] = f16v_t{};
-#pragma unroll
-      for (int st = 0; st < NS; ++st) {
-        const int slot = (2 * st + hh) ^ (k & W::KSW);
-        const h8_t khi = *(const h8_t*)(kr + 16 * slot);
-        const h8_t klo = *(const h8_t*)(kr + 2 * D + 16 * slot);
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(khi, qf[st], s[kb], 0, 0, 0);
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(klo, qf[st], s[kb], 0, 0, 0);
-        if constexpr (QLO) s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(khi, ql[st], s[kb], 0, 0, 0);
-      }
+      const int slot = (2 * st + hh) ^ (k & W::KSW);
+      dst[2 * i] = *(const h8_t*)(kr + 16 * slot);
+      dst[2 * i + 1] = *(const h8_t*)(kr + 2 * D + 16 * slot);
     }
-
+  };
+  auto qk = [&](const uint8_t* buf) {
+    s[0] = f16v_t{};
+    s[1] = f16v_t{};
+    kload(buf, 0, fr[0]);
+#pragma unroll
+    for (int g = 0; g < KGROUPS; ++g) {
+      if (g + 1 < KGROUPS) kload(buf, g + 1, fr[(g + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      const h8_t* f = fr[g & 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int st = 2 * g + (i >> 1), kb = i & 1;
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * i], qf[st], s[kb], 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int st = 2 * g + (i >> 1), kb = i & 1;
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * i + 1], qf[st], s[kb], 0, 0, 0);
+        if constexpr (QLO) s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * i], ql[st], s[kb], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // V^T fragments of keys 32 half .. 32 half + 31 (two 16-key steps).
+  auto vload = [&](const uint8_t* buf, int half, h8_t* dst) {
+#pragma unroll
+    for (int i = 0; i < 2 * NDB; ++i) {
+      const int ks = 2 * half + i / NDB, db = i % NDB;
+      const int d = 32 * db + j;
+      const int slot = (2 * ks + hh) ^ ((d >> 1) & 7);
+      dst[i] = *(const h8_t*)(buf + W::K_BYTES + d * W::VROW + 16 * slot);
+    }
+  };
+  // Online softmax of the tile at key kbase: S^T becomes P^T in place (the
+  // first V^T fragments, issued before, are in flight meanwhile).
+  auto softmax = [&](int kbase) {
+    __builtin_amdgcn_sched_barrier(0);
     // Causal / context limit, only where this tile reaches it.
     if (kbase + kDenseKeys > qmin + 1 || kbase + kDenseKeys > kv_end) {
 #pragma unroll
@@ -318,22 +400,48 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
         lsum += p;
       }
     }
-
-    // O^T += V^T P^T, 16 keys per step.
+  };
+  // O^T += V^T P^T, 16 keys per step; keys 32..63's fragments load while
+  // keys 0..31 feed the MFMAs.
+  auto pv = [&](const uint8_t* buf) {
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int kb = ks >> 1, r0 = 8 * (ks & 1);
-      h8_t pb;
+    for (int half = 0; half < 2; ++half) {
+      if (half == 0) vload(buf, 1, fr[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      const h8_t* f = fr[half];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pb[e] = (_Float16)s[kb][r0 + e];
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const int ks = 2 * half + k2;
+        const int kb = ks >> 1, r0 = 8 * (ks & 1);
+        h8_t pb;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const int d = 32 * db + j;
-        const int slot = (2 * ks + hh) ^ ((d >> 1) & 7);
-        const h8_t va = *(const h8_t*)(buf + W::K_BYTES + d * W::VROW + 16 * slot);
-        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, acc[db], 0, 0, 0);
+        for (int e = 0; e < 8; ++e) pb[e] = (_Float16)s[kb][r0 + e];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[k2 * NDB + db], pb, acc[db], 0, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  auto finish = [&](const uint8_t* buf, int kbase) {
+    vload(buf, 0, fr[0]);
+    softmax(kbase);
+    pv(buf);
+  };
+
+  // Tiles kt + 1 .. kt + NBUF - 1 are in flight while tile kt is consumed.
+  for (int kt = 0; kt < n_kt; ++kt) {
+    // Tile kt has landed once at most the DMAs of the tiles after it remain.
+    if (NBUF == 3 && kt + 1 < n_kt) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (kt + NBUF - 1 < n_kt) issue(kt + NBUF - 1);
+    const int kbase = kt * kDenseKeys;
+    if (!active || kbase >= kend_w) continue;
+    const uint8_t* buf = ring + (kt % NBUF) * W::BYTES;
+    qk(buf);
+    finish(buf, kbase);
   }
 
   const float l = halves_sum(lsum);
@@ -364,16 +472,17 @@ hipError_t launch_prefill_pack(const PackArgs& a, long n_packs, hipStream_t s) {
 
 template <int D, bool QLO>
 static hipError_t flash_one(const FlashArgs& a, hipStream_t s) {
-  constexpr int lds = 2 * Ws<D>::BYTES;
+  constexpr int NBUF = kDenseRing;
+  constexpr int lds = NBUF * Ws<D>::BYTES;
   static bool attr = false;
   if (!attr) {
-    const hipError_t e =
-        hipFuncSetAttribute((const void*)flash_kernel<D, QLO>, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    const hipError_t e = hipFuncSetAttribute((const void*)flash_kernel<D, QLO, NBUF>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
     attr = true;
   }
   const long n = (long)a.n_qtiles * a.H;
-  hipLaunchKernelGGL((flash_kernel<D, QLO>), dim3((unsigned)n), dim3(64 * kDenseWaves), lds, s, a);
+  hipLaunchKernelGGL((flash_kernel<D, QLO, NBUF>), dim3((unsigned)n), dim3(64 * kDenseWaves), lds, s, a);
   return hipGetLastError();
 }
 
