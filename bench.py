@@ -17,6 +17,13 @@ and replayed ``--reps`` times between HIP events on the launch stream, so the
 time is GPU work only; ``roofline`` puts it against 8 TB/s. ``ms_per_step`` and
 ``e2e_decode_tok_s`` time the whole 32-layer step (host planning included) over
 the ``--steps`` timed steps.
+
+``prefill`` (one layer): 16 sequences x 4096 tokens written
+and attended in 512-token chunks over an INT4 cache, bf16 activations; per
+chunk the quantize-on-write of its tokens, then chunked-prefill attention over
+the whole context written so far (the two-pass path: workspace pack + flash
+kernel), timed with HIP events; utilisation = 4 D Hq (causal pairs) / time
+against 2.5 PFLOP/s dense fp16.
 """
 
 from __future__ import annotations
@@ -37,6 +44,8 @@ METRIC = "INT4 paged-decode attn HBM GB/s (% of peak); e2e decode tok/s at 8B sh
 HBM_PEAK_GBS = 8000.0
 
 H, HQ, D, BS, KG, VG, MEM, LAYERS, S = 8, 32, 128, 16, 16, 32, 8, 32, 64
+PF_SEQS, PF_CTX, PF_CHUNK = 16, 4096, 512  # config 3
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16
 
 
 def alg_bytes(lens: np.ndarray, bits: int, res_bytes: int = 2) -> int:
@@ -218,7 +227,92 @@ def run(args) -> dict:
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(stores[int4[0]], q[int4[0]], table, ctx + args.warmup + args.steps - 1)
+    if not args.no_prefill:
+        res["prefill"] = run_prefill()
     return res
+
+
+def prefill_flops(ctx: int, chunk: int, seqs: int) -> int:
+    """QK^T + PV flops of one chunk: 4 D Hq per (query, visible key) pair, causal."""
+    pairs = seqs * (chunk * (ctx - chunk) + chunk * (chunk + 1) // 2)
+    return 4 * D * HQ * pairs
+
+
+def run_prefill(reps: int = 3) -> dict:
+    """Config 3 on one layer: every 512-token chunk of 16 x 4096 tokens is written
+    (quantize-on-write into INT4 pages) and attended over its whole context. A
+    first pass over a fresh cache warms every kernel up; the second is timed."""
+    _prefill_pass(1)
+    return _prefill_pass(reps)
+
+
+def _prefill_pass(reps: int) -> dict:
+    import torch
+
+    from echokv_amd.kernels import prefill as pf
+    from echokv_amd.tiered_cache import TieredKVCache, TieredLayout
+    from echokv_amd.write_plan import SharedState, stage_plan
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(3)
+    layout = TieredLayout(H, D, BS, MEM, KG, VG)
+    page = BS * TieredLayout.per_token_bytes(H, D, MEM, KG, VG)
+    nbs = PF_CTX // BS
+    nb = PF_SEQS * nbs + 16
+    table = rng.permutation(nb)[: PF_SEQS * nbs].reshape(PF_SEQS, nbs).astype(np.int64)
+    shared = SharedState(nb, BS, KG, PF_SEQS + 16, kref_window=64, device=dev)
+    pages = torch.zeros(nb, page, dtype=torch.uint8, device=dev)
+    res = torch.zeros(PF_SEQS + 17, KG, H, D, dtype=torch.bfloat16, device=dev)
+    store = TieredKVCache(layout, pages, residual=res, shared=shared)
+    kref = torch.zeros(64, H, D, device=dev)
+    table_d = torch.from_numpy(table).to(dev, torch.int32)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    scale = D ** -0.5
+    t_write = t_attn = 0.0
+    flops = 0
+    for c in range(PF_CTX // PF_CHUNK):
+        pos = np.arange(c * PF_CHUNK, (c + 1) * PF_CHUNK)
+        slots = np.concatenate([table[s][pos // BS] * BS + pos % BS for s in range(PF_SEQS)])
+        plan = shared.planner.plan(slots)
+        opened = store.prepare(plan, 4)
+        shared.commit(plan)
+        meta, extra = stage_plan(plan, dev, None)
+        shared.apply_res_map(*extra[:4])
+        if opened is not None:
+            store.write_headers(torch.from_numpy(opened[0]).to(dev), torch.from_numpy(opened[1]).to(dev))
+        k = torch.randn(slots.size, H, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        v = torch.randn(slots.size, H, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        q = torch.randn(slots.size, HQ, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        out = torch.empty_like(q)
+        ctx = (c + 1) * PF_CHUNK
+        prefill = [(s * PF_CHUNK, (s + 1) * PF_CHUNK, ctx, 0) for s in range(PF_SEQS)]
+        req = list(range(PF_SEQS))
+        plan_d = pf.build_dense_plan(prefill, req, HQ // H, dev)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record()
+        store.apply(meta, k, v, kref)
+        ev[1].record()
+        ev[2].record()
+        for _ in range(reps):
+            pf.prefill_attention(store, q, out, prefill, req, table_d, scale, dense=plan_d)
+        ev[3].record()
+        torch.cuda.synchronize()
+        t_write += ev[0].elapsed_time(ev[1])
+        t_attn += ev[2].elapsed_time(ev[3]) / reps
+        flops += prefill_flops(ctx, PF_CHUNK, PF_SEQS)
+    tflops = flops / (t_attn * 1e-3) / 1e12
+    return {
+        "workload": "cfg3: 16 x 4096 tokens in 512-token chunks over an INT4 cache, Hq 32 / H 8 / D 128, bf16, "
+                    "one layer",
+        "attn_ms_per_layer": round(t_attn, 3),
+        "write_ms_per_layer": round(t_write, 3),
+        "tflop_per_layer": round(flops / 1e12, 4),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+                     "kernel": "pack_kernel<128> + flash_kernel<128, false, 3> per chunk (8 chunks)"},
+    }
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_cfg2_int4_traffic.md"
@@ -276,6 +370,8 @@ def main():
     ap.add_argument("--max-splits", type=int, default=64, help="cap on decode splits per sequence")
     ap.add_argument("--reps", type=int, default=50, help="graph replays of the 16 INT4 layers' decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill measurement")
+    ap.add_argument("--prefill-only", action="store_true", help="only the config-3 prefill measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 1 GiB device-to-device 5 times (the reference kernel for FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -284,6 +380,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.prefill_only:
+        print(json.dumps({"prefill": run_prefill()}), flush=True)
         return
     print(json.dumps(run(args)), flush=True)
 
