@@ -83,7 +83,7 @@ __device__ __forceinline__ h2_t code_pair(uint32_t x, const CodeK& k) {
 }
 
 // Eight consecutive channels of a K row, natural order, as an MFMA fragment of
-// 1024 + code (the bias is taken out of the product by unbias()).
+// 1024 + code (s_block takes the bias back out with one more contraction).
 // INT4: one word (8 nibbles); INT8: two words; INT2: bytes 2*hf, 2*hf+1 of one word.
 template <int BITS>
 __device__ __forceinline__ h8_t kfrag(const uint32_t* w, int hf, const CodeK& k) {
@@ -201,66 +201,40 @@ struct Wave {
   float m_run, l_lane;
 };
 
-// One K group's operands: q * k_scale as fp16 hi / lo MFMA fragments, and the
-// k_min fragments, contracted with q itself so sum_d q * k_min lands in the same
-// accumulator (k_min is exact in fp16; no cross-lane reduction needed). Built
-// per tile: a per-tile temporary keeps it out of the registers that live across
-// the tile loop.
-template <int D>
-struct QK {
-  h8_t hi[D / 32], lo[D / 32], mn[D / 32];
-};
-
-// q * k_scale (hi / lo) fragments and the scaled k_min bias of one K group from
-// the lane's CPL channels of k_scale (ks) and k_min (km), natural order.
-template <int D, bool QLO>
-__device__ __forceinline__ void build_qk(QK<D>& qk, const Wave<D, QLO>& w, const uint32_t* ks, const uint32_t* km,
-                                         float scale_log2) {
-  constexpr int CPL = Wave<D, QLO>::CPL;
-  uint32_t hi[CPL / 2], lo[CPL / 2];
+// S^T of one 16-token tile from its codes, K group by 32-channel block j:
+//   S^T += codes_j . (q * k_scale)_j^T   as fp16 hi / lo pairs (two chains)
+//        - 1024 * sum_d (q * k_scale)_j  (the code fragments carry 1024 + c)
+//        + k_min_j . q_j^T               (and q lo for float32 queries)
+// The products q * s are exact in fp32; hi = fp16(q * s), lo = fp16(fma(q, s,
+// -hi)) keeps S accurate to ~2^-22 relative. Each block's operands are built
+// right before its MFMAs, so only one block's live at a time. ks / km: the
+// lane's k_scale / k_min words of block j (channels 8 at a time, natural order).
+template <int D, bool QLO, int BITS>
+__device__ __forceinline__ void s_block(const Wave<D, QLO>& w, const uint32_t* ks, const uint32_t* km,
+                                        const h8_t& kf, int j, f4_t& sh, f4_t& sl) {
+  uint32_t hi[4], lo[4];
 #pragma unroll
-  for (int i = 0; i < CPL / 2; ++i) {
-    const h2_t q = u2h(w.qn[i]), s = u2h(ks[i]);
-    const h2_t ph = q * s;
-    h2_t pl = __builtin_elementwise_fma(q, s, -ph);  // exact product minus its rounding, rounded once
-    if constexpr (QLO) pl = __builtin_elementwise_fma(u2h(w.ql[i]), s, pl);
+  for (int i = 0; i < 4; ++i) {
+    const h2_t q = u2h(w.qn[4 * j + i]), sc = u2h(ks[i]);
+    const h2_t ph = q * sc;
+    h2_t pl = __builtin_elementwise_fma(q, sc, -ph);  // exact product minus its rounding, rounded once
+    if constexpr (QLO) pl = __builtin_elementwise_fma(u2h(w.ql[4 * j + i]), sc, pl);
     hi[i] = h2u(ph);
     lo[i] = h2u(pl);
   }
-#pragma unroll
-  for (int j = 0; j < Wave<D, QLO>::NQK; ++j) {
-    qk.hi[j] = w2h8(hi[4 * j], hi[4 * j + 1], hi[4 * j + 2], hi[4 * j + 3]);
-    qk.lo[j] = w2h8(lo[4 * j], lo[4 * j + 1], lo[4 * j + 2], lo[4 * j + 3]);
-    qk.mn[j] = w2h8(km[4 * j], km[4 * j + 1], km[4 * j + 2], km[4 * j + 3]);
-  }
-}
-
-// S^T += k_min q^T: the K min term of every token (rows), from the group's k_min
-// fragments and the query (hi, and lo for float32 queries).
-template <int D, bool QLO>
-__device__ __forceinline__ void add_kmin(const QK<D>& qk, const Wave<D, QLO>& w, f4_t& sh, f4_t& sl) {
-#pragma unroll
-  for (int j = 0; j < D / 32; ++j) {
-    sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(qk.mn[j], w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2],
-                                                               w.qn[4 * j + 3]), sh, 0, 0, 0);
-    if constexpr (QLO)
-      sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(qk.mn[j], w2h8(w.ql[4 * j], w.ql[4 * j + 1], w.ql[4 * j + 2],
-                                                                 w.ql[4 * j + 3]), sl, 0, 0, 0);
-  }
-}
-
-// S^T -= 1024 * sum_d (q * k_scale)[d]: the code fragments carry 1024 + c, so the
-// bias leaves through one more contraction (the products are exact in fp32 and
-// the sums ~1024x the unbiased ones, so S keeps ~2^-17 relative accuracy).
-template <int D>
-__device__ __forceinline__ void unbias(const QK<D>& qk, f4_t& sh, f4_t& sl) {
+  const h8_t h8 = w2h8(hi[0], hi[1], hi[2], hi[3]), l8 = w2h8(lo[0], lo[1], lo[2], lo[3]);
   const h8_t m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f,
                       (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f};
-#pragma unroll
-  for (int j = 0; j < D / 32; ++j) {
-    sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, qk.hi[j], sh, 0, 0, 0);
-    sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, qk.lo[j], sl, 0, 0, 0);
-  }
+  const h8_t mn = w2h8(km[0], km[1], km[2], km[3]);
+  sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, h8, sh, 0, 0, 0);
+  sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, l8, sl, 0, 0, 0);
+  sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, h8, sh, 0, 0, 0);
+  sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, l8, sl, 0, 0, 0);
+  sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+      mn, w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2], w.qn[4 * j + 3]), sh, 0, 0, 0);
+  if constexpr (QLO)
+    sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        mn, w2h8(w.ql[4 * j], w.ql[4 * j + 1], w.ql[4 * j + 2], w.ql[4 * j + 3]), sl, 0, 0, 0);
 }
 
 // S^T of a tile whose keys are the block's open K group, read from the
@@ -321,52 +295,82 @@ __device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, cons
 // kernel's (or whose chunk table names a chunk out of range), including its
 // open K group. Rare: only blocks demoted or downgraded under pool pressure.
 // ---------------------------------------------------------------------------
-// One 16-token tile [t0, t0 + 16) of block `blk` (tier BITS); tokens >= n_valid
-// are masked. in_res: the tile is the block's open K group (K from the residual).
-template <int D, bool QLO, int BITS>
-__device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long blk, int t0, int n_valid, long rslot,
-                                     bool in_res, int h, int lane) {
+// NC codes (4, 8, 16 or 32) of `bits` bits at p (little-endian within bytes),
+// one byte each, in out[NC / 4].
+template <int NC>
+__device__ __forceinline__ void load_as_bytes(const uint8_t* p, int bits, uint32_t* out) {
+  if (bits == 8) {
+    load_bytes<NC>(p, out);
+  } else if (bits == 4) {
+    constexpr int NW = NC / 8 > 0 ? NC / 8 : 1;
+    uint32_t x[NW];
+    load_bytes<NC / 2>(p, x);
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      const uint32_t lo = x[i] & 0x0F0F0F0Fu, hi = (x[i] >> 4) & 0x0F0F0F0Fu;  // even / odd codes
+      out[2 * i] = perm(hi, lo, 0x05010400u);                                   // codes 8i .. 8i+3
+      if (2 * i + 1 < NC / 4) out[2 * i + 1] = perm(hi, lo, 0x07030602u);        // codes 8i+4 .. 8i+7
+    }
+  } else {
+    constexpr int NW = NC / 16 > 0 ? NC / 16 : 1;
+    uint32_t x[NW];
+    if constexpr (NC >= 16) load_bytes<NC / 4>(p, x);
+    else if constexpr (NC == 8) x[0] = *(const uint16_t*)p;
+    else x[0] = *p;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      const uint32_t y0 = x[i] & 0x03030303u, y1 = (x[i] >> 2) & 0x03030303u;
+      const uint32_t y2 = (x[i] >> 4) & 0x03030303u, y3 = (x[i] >> 6) & 0x03030303u;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {  // byte b of y_k = code 4b + k
+        if (4 * i + b < NC / 4) {
+          const uint32_t sel = 0x04000400u | (uint32_t)b | ((uint32_t)b << 8) | ((uint32_t)b << 16) | ((uint32_t)b << 24);
+          const uint32_t t01 = perm(y1, y0, sel);  // y0.b, y1.b, y0.b, y1.b
+          const uint32_t t23 = perm(y3, y2, sel);  // y2.b, y3.b, y2.b, y3.b
+          out[4 * i + b] = perm(t23, t01, 0x05040100u);
+        }
+      }
+    }
+  }
+}
+
+// One 16-token tile [t0, t0 + 16) of block `blk` stored at `bits` (any tier):
+// codes are widened to bytes and go through the 8-bit math. tokens >= n_valid
+// are masked; in_res: the tile is the block's open K group (K from the residual).
+template <int D, bool QLO>
+__device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs& a, long blk, int t0, int n_valid,
+                                         long rslot, bool in_res, int h, int lane, int bits, float* x, h4_t* va) {
   using W = Wave<D, QLO>;
   constexpr int CPL = W::CPL, NQK = W::NQK, CPM = W::CPM;
   const Lay& L = a.L;
   const int c = lane >> 4, n = lane & 15;
   const uint8_t* pages = a.pages;
-  const long side = (long)L.H * D * BITS / 8;
-  const long headb = (long)h * (D * BITS / 8);
+  const long side = (long)L.H * D * bits / 8;
+  const long headb = (long)h * (D * bits / 8);
 
   // ---- S^T = K Q'^T (+ bias) -------------------------------------------
   f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
   if (in_res) {
     s_from_residual<D, QLO>(w, a, rslot, t0, h, lane, sh, sl);
   } else {
-    QK<D> qk;
-    {
-      const long e0 = ((long)(t0 / L.KG) * L.H + h) * D + c * CPL;
-      uint32_t ks[CPL / 2], km[CPL / 2];
-      load_bytes<2 * CPL>(pages + blk * L.stride + L.o_ks + 2 * e0, ks);
-      load_bytes<2 * CPL>(pages + blk * L.stride + L.o_km + 2 * e0, km);
-      build_qk<D, QLO>(qk, w, ks, km, a.scale_log2);
-    }
-    add_kmin<D, QLO>(qk, w, sh, sl);
-    const long rb = row_base(pages, L, blk, t0 + n, BITS);
-    constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
-    uint32_t kw[KW];
+    const long e0 = ((long)(t0 / L.KG) * L.H + h) * D + c * CPL;
+    const long rb = row_base(pages, L, blk, t0 + n, bits);
+    uint32_t kw[CPL / 4];
     if (rb >= 0) {
-      load_bytes<CPL * BITS / 8>(pages + rb + headb + (long)c * (CPL * BITS / 8), kw);
+      load_as_bytes<CPL>(pages + rb + headb + (long)c * (CPL * bits / 8), bits, kw);
     } else {
 #pragma unroll
-      for (int i = 0; i < KW; ++i) kw[i] = 0;
+      for (int i = 0; i < CPL / 4; ++i) kw[i] = 0;
     }
-    const CodeK ck = code_consts<BITS>();
+    const CodeK ck = code_consts<8>();
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
-      const h8_t kf = kfrag_j<BITS>(kw, j, ck);
-      sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.hi[j], sh, 0, 0, 0);
-      sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.lo[j], sl, 0, 0, 0);
+      uint32_t ks[4], km[4];
+      load_bytes<16>(pages + blk * L.stride + L.o_ks + 2 * e0 + 16 * j, ks);
+      load_bytes<16>(pages + blk * L.stride + L.o_km + 2 * e0 + 16 * j, km);
+      s_block<D, QLO, 8>(w, ks, km, kfrag_j<8>(kw, j, ck), j, sh, sl);
     }
-    unbias<D>(qk, sh, sl);
   }
-  float x[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float v = (sh[i] + sl[i]) * a.scale_log2;
@@ -374,8 +378,7 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
   }
 
   // ---- V fragments: tokens t0+4c+i, channels n*CPM + j -------------------
-  constexpr int VB = CPM * BITS / 8;  // bytes per token of the lane's V slice
-  constexpr int VW = VB >= 4 ? VB / 4 : 1;
+  constexpr int VW = CPM / 4;  // words per token of the lane's V slice, one byte per code
   uint32_t vw[4][VW], vsh[4][4];
   const int G = D / L.VG;
   const int g = (n * CPM) / L.VG;
@@ -383,10 +386,10 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int tv = t0 + 4 * c + i;
-    const long rb = row_base(pages, L, blk, tv, BITS);
+    const long rb = row_base(pages, L, blk, tv, bits);
     const bool ok = tv < n_valid && rb >= 0;
     if (ok) {
-      load_bytes<VB>(pages + rb + side + headb + (long)n * VB, vw[i]);
+      load_as_bytes<CPM>(pages + rb + side + headb + (long)n * (CPM * bits / 8), bits, vw[i]);
       const long e = ((long)tv * L.H + h) * G + g;
       sv[i] = *f16p(pages, blk * L.stride + L.o_vs + 2 * e);
       mv[i] = *f16p(pages, blk * L.stride + L.o_vm + 2 * e);
@@ -397,29 +400,36 @@ __device__ __forceinline__ void tile(Wave<D, QLO>& w, const DecodeArgs& a, long 
       mv[i] = (_Float16)0.f;
     }
   }
-  vshift<BITS, VW>(vw, vsh);
+  vshift<8, VW>(vw, vsh);
   const h2_t s01 = {sv[0], sv[1]}, s23 = {sv[2], sv[3]};
   const h2_t m01 = {mv[0], mv[1]}, m23 = {mv[2], mv[3]};
-  const CodeK vk = code_consts<BITS>();
-  h4_t va[CPM];
+  const CodeK vk = code_consts<8>();
 #pragma unroll
-  for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23, vk);
-  softmax_pv<D, QLO>(w, x, va);
+  for (int j = 0; j < CPM; ++j) va[j] = vfrag<8, VW>(j, vw, vsh, s01, s23, m01, m23, vk);
 }
 
 // ---------------------------------------------------------------------------
-// Tier-specialised pipelined path. Each wave streams its KV head's tiles of the
-// split through an NBUF-slot ring in LDS, filled by direct global->LDS DMA
-// (global_load_lds_dword{,x4}: lane L's bytes land at slot + size * L), so the
-// bytes in flight per CU are set by the ring size, not by VGPRs. The DMAs are
-// issued from inline asm with a 64-bit scalar base (the layer's pages) and a
-// 32-bit per-lane byte offset; the compiler neither sees them nor inserts waits
-// for them; the wave waits with an explicit s_waitcnt vmcnt(n) for the tile it
-// is about to read (loads retire in order, so waiting for "at most n
-// outstanding" covers every older load). Every tile issues the same number of
-// DMA instructions (a tile the fast path does not take -- the open K group, a
-// block of another tier -- loads 4 dummy bytes from its page header into its
-// slot), so n is a compile-time count.
+// Tier-specialised pipelined path. The 4 waves of a workgroup (the 4 KV heads of
+// a head group) stream the split's tiles through one NBUF-slot ring in LDS,
+// filled by direct global->LDS DMA (global_load_lds_dword{,x4}: lane L's bytes
+// land at M0 + size * L). A token row holds [K codes of all heads | V codes of
+// all heads], so the group's 4 heads are one contiguous 4 * D * b/8-byte
+// segment per side: the tile is loaded as whole segments, jobs of 1 KB dealt
+// round-robin to the 4 waves, and every wave then reads its own head from LDS.
+// (Per-head loads would fetch 64-byte pieces at 1 KB stride: about three times
+// the cache-line requests for the same bytes.) Within a DMA job, lane L takes
+// 16-byte unit (L + row) % U of its row: the rotation spreads any one head's
+// units of the 16 rows over all LDS banks, so the per-head reads are conflict-free.
+// The DMAs are issued from inline asm with a 64-bit scalar base (the layer's
+// pages) and a 32-bit per-lane byte offset; the compiler neither sees them nor
+// inserts waits for them. A wave waits with an explicit s_waitcnt vmcnt(n) for
+// its own part of the tile about to be read (loads retire in order, so "at most
+// n outstanding" covers every older load), then the workgroup meets at a
+// barrier: after it every part has landed and every wave is done with the
+// previous tile, whose slot the next DMAs then reuse. Every tile issues the
+// same number of DMA instructions per wave (a job past the tile's last, or a
+// tile the pipelined path does not take, loads 4 dummy bytes from the page
+// header into the slot's spare word), so n is a compile-time count.
 // ---------------------------------------------------------------------------
 #pragma clang diagnostic ignored "-Winline-asm"
 
@@ -439,19 +449,35 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// Workgroup barrier without a memory fence (a fence would wait for the DMAs in
+// flight); the wave's own LDS reads are complete first.
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <int D, int BITS>
 struct Ring {
-  static constexpr int KB = D * BITS / 8;                 // code bytes per token, one side, one head
-  static constexpr int KCB = 16 * KB;                     // per tile
-  static constexpr int KI = (KCB / 16 + 63) / 64;         // dwordx4 DMAs per side
-  static constexpr int OFF_V = KCB, OFF_S = 2 * KCB;      // K codes | V codes | k_scale, k_min | V stats
-  static constexpr int OFF_VS = 2 * KCB + 4 * D;
-  static constexpr int SLOT = OFF_VS + 16 * 4 * 4;        // V stats for G <= 4 groups
+  static constexpr int KB = D * BITS / 8;        // code bytes per token, one side, one head
+  static constexpr int U = 4 * KB / 16;          // 16-byte units of the group's segment of a row, one side
+  static constexpr int RPI = 64 / U;             // rows per DMA job
+  static constexpr int NK = 16 / RPI;            // DMA jobs per side
+  static constexpr int SIDE = 16 * 4 * KB;       // one side of a tile, 4 heads
+  static constexpr int OFF_V = SIDE;             // K codes | V codes | k_scale, k_min (4 heads) | V scale, V min
+  static constexpr int OFF_KS = 2 * SIDE;
+  static constexpr int OFF_VS = OFF_KS + 2 * 4 * D * 2;
+  static constexpr int OFF_DUMMY = OFF_VS + 2 * 16 * 4 * 4 * 2;  // V stats for G <= 4 groups
+  static constexpr int SLOT = OFF_DUMMY + 16;
+  static constexpr int J = 2 * NK + 3;           // DMA jobs per tile
+  static constexpr int M = (J + 3) / 4;          // DMA instructions per wave per tile
   static constexpr int NBUF = BITS == 8 ? 3 : 4;
-  static constexpr int M = 2 * KI + 2;                    // DMA instructions per tile
-  static constexpr int WAVE_BYTES = NBUF * SLOT;
+  static constexpr int WG_BYTES = NBUF * SLOT;
+  static_assert(U >= 4 && U <= 64, "segment units");
 };
+
+// LDS byte offset (within a slot's side) of 16-byte unit u of token n.
+template <int D, int BITS>
+__device__ __forceinline__ uint32_t unit_pos(int n, int u) {
+  using R = Ring<D, BITS>;
+  return (uint32_t)((n / R::RPI) * 1024 + ((n % R::RPI) * R::U + ((u - n) % R::U + R::U) % R::U) * 16);
+}
 
 // Per-block facts of the split's next <= 64 blocks, one block per lane: byte
 // offsets (from the layer's pages) of the block's page and of its chunks
@@ -504,136 +530,124 @@ __device__ __forceinline__ BlockLane load_block(const DecodeArgs& a, long blk) {
   return b;
 }
 
-// Per-lane constants of the pipelined path (byte offsets; LDS ones from the slot).
+// Per-lane constants of the pipelined path: LDS read offsets within a slot
+// for the wave's head (wv, 0..3 within the group).
 template <int D, int BITS>
 struct LaneConst {
-  // DMA sources
-  uint32_t kv_tl[Ring<D, BITS>::KI];   // token (within the tile) of K/V DMA r
-  uint32_t kv_off[Ring<D, BITS>::KI];  // head + 16-byte piece within the row
-  uint32_t ks_off;                     // k_scale / k_min piece (without the page and group)
-  uint32_t vs_off;                     // V stats piece (without the page and first token)
-  // LDS reads
-  uint32_t k_rd, v_rd, s_rd, vs_rd, vm_rd;
+  uint32_t k_rd[BITS == 8 ? 2 : 1];  // K codes of token n, channels c * D/4 .. (16-byte units; INT2: + 8 * (c & 1))
+  uint32_t v_rd[4];                  // V codes of tokens 4c + i, the lane's CPM channels
+  uint32_t s_rd;                     // k_scale (k_min at + 4 * D * 2)
+  uint32_t vs_rd;                    // V scale of token 4c (V min at vm_off; tokens 4c + i at + i * tok stride)
 };
 
 template <int D, int BITS>
-__device__ __forceinline__ LaneConst<D, BITS> lane_const(const DecodeArgs& a, int h, int lane) {
+__device__ __forceinline__ LaneConst<D, BITS> lane_const(const DecodeArgs& a, int wv, int lane) {
   using R = Ring<D, BITS>;
-  const Lay& L = a.L;
-  constexpr int QPT = R::KB / 16;  // 16-byte pieces per token row (one side, one head)
   constexpr int CPL = D / 4, CPM = D / 16, VB = CPM * BITS / 8;
-  LaneConst<D, BITS> k;
-#pragma unroll
-  for (int r = 0; r < R::KI; ++r) {
-    const int idx = lane + 64 * r;
-    k.kv_tl[r] = idx / QPT;
-    k.kv_off[r] = (uint32_t)(h * R::KB + 16 * (idx % QPT));
-  }
-  k.ks_off = (uint32_t)((lane < D / 8 ? L.o_ks : L.o_km) + 2L * h * D + 16 * (lane % (D / 8)));
-  const int G = D >> a.vg_shift;
-  const int sp = G == 4 ? 1 : 0;  // log2(dwords per token per stat)
-  const int which = lane >> (4 + sp);
-  const int r = lane & ((16 << sp) - 1);
-  k.vs_off = (uint32_t)((which ? L.o_vm : L.o_vs) + 2L * ((r >> sp) * L.H + h) * G + 4 * (r & ((1 << sp) - 1)));
   const int c = lane >> 4, n = lane & 15;
-  k.k_rd = (uint32_t)(n * R::KB + c * (CPL * BITS / 8));
-  k.v_rd = (uint32_t)(R::OFF_V + 4 * c * R::KB + n * VB);
-  k.s_rd = (uint32_t)(R::OFF_S + 2 * c * CPL);
+  LaneConst<D, BITS> k;
+  const int kbyte = wv * R::KB + c * (CPL * BITS / 8);  // within the group's segment
+#pragma unroll
+  for (int e = 0; e < (BITS == 8 ? 2 : 1); ++e) k.k_rd[e] = unit_pos<D, BITS>(n, kbyte / 16 + e) + (kbyte % 16);
+  const int vbyte = wv * R::KB + n * VB;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) k.v_rd[i] = R::OFF_V + unit_pos<D, BITS>(4 * c + i, vbyte / 16) + (vbyte % 16);
+  k.s_rd = (uint32_t)(R::OFF_KS + wv * D * 2 + 2 * c * CPL);
+  const int G = D >> a.vg_shift;
   const int g = (n * CPM) >> a.vg_shift;
-  k.vs_rd = (uint32_t)(R::OFF_VS + 2 * (4 * c * G + g));
-  k.vm_rd = k.vs_rd + 2 * 16 * G;
+  k.vs_rd = (uint32_t)(R::OFF_VS + 4 * c * 8 * G + (wv * G + g) * 2);
   return k;
 }
 
-// DMA one tile (16 tokens from block offset t0) of the wave's head into ring
-// slot `slot`. pg / cb: the block's page and chunk byte offsets.
+// This wave's share (jobs wv, wv + 4, ...) of the DMAs of one tile (16 tokens
+// from block offset t0) of head group hg into ring slot `slot`. pg / cb: the
+// block's page and chunk byte offsets.
 template <int D, int BITS>
-__device__ __forceinline__ void issue_tile(const DecodeArgs& a, const LaneConst<D, BITS>& k, uint32_t slot, bool fast,
-                                           int t0, int lane, uint32_t pg, uint32_t cb1, uint32_t cb2, uint32_t cb3) {
+__device__ __forceinline__ void issue_tile(const DecodeArgs& a, uint32_t slot, bool fast, int t0, int lane, int wv,
+                                           int hg, uint32_t pg, uint32_t cb1, uint32_t cb2, uint32_t cb3) {
   using R = Ring<D, BITS>;
   const Lay& L = a.L;
-  if (!fast) {
-#pragma unroll
-    for (int i = 0; i < R::M; ++i) {
-      if (lane == 0) dma4(a.pages, pg, slot);
-    }
-    return;
-  }
   constexpr int LB = BITS == 8 ? 3 : (BITS == 4 ? 2 : 1);
   const int tpc_shift = a.bs_shift + 1 - LB;  // tokens per chunk = 2 * BS / BITS
   const uint32_t rowb = (uint32_t)(2 * D * BITS / 8) * (uint32_t)L.H;
-  const uint32_t side = rowb / 2;
-  const uint32_t cb0 = pg + (uint32_t)L.o_data;
+  const int h0 = hg * 4;
+  const int G = D >> a.vg_shift;
 #pragma unroll
-  for (int r = 0; r < R::KI; ++r) {
-    const uint32_t t = (uint32_t)t0 + k.kv_tl[r];
-    const uint32_t j = t >> tpc_shift;
-    uint32_t cb = cb0;
-    if constexpr (BITS >= 4) cb = j == 1 ? cb1 : cb;
-    if constexpr (BITS == 8) cb = j == 2 ? cb2 : (j == 3 ? cb3 : cb);
-    const uint32_t off = cb + (t & ((1u << tpc_shift) - 1)) * rowb + k.kv_off[r];
-    if (lane + 64 * r < R::KCB / 16) {
-      dma16(a.pages, off, slot + 1024 * r);
-      dma16(a.pages, off + side, slot + R::OFF_V + 1024 * r);
+  for (int m = 0; m < R::M; ++m) {
+    const int j = wv + 4 * m;  // wave-uniform
+    if (!fast || j >= R::J) {
+      if (lane == 0) dma4(a.pages, pg, slot + R::OFF_DUMMY);
+      continue;
+    }
+    if (j < 2 * R::NK) {  // codes: RPI rows of one side
+      const int side = j >= R::NK;
+      const int jj = side ? j - R::NK : j;
+      const int ri = lane / R::U;
+      const int t = jj * R::RPI + ri;               // token within the tile
+      const int u = (lane % R::U + t) % R::U;      // unit of the segment this lane loads
+      const uint32_t tt = (uint32_t)(t0 + t);
+      const uint32_t ch = tt >> tpc_shift;
+      uint32_t cb = pg + (uint32_t)L.o_data;
+      if constexpr (BITS >= 4) cb = ch == 1 ? cb1 : cb;
+      if constexpr (BITS == 8) cb = ch == 2 ? cb2 : (ch == 3 ? cb3 : cb);
+      const bool head_ok = h0 + (u * 16) / R::KB < L.H;
+      const uint32_t off = cb + (tt & ((1u << tpc_shift) - 1)) * rowb + (side ? rowb / 2 : 0u) +
+                           (uint32_t)(h0 * R::KB + u * 16);
+      dma16(a.pages, head_ok ? off : pg, slot + (side ? R::OFF_V : 0) + 1024 * jj);
+    } else if (j < 2 * R::NK + 2) {  // k_scale, then k_min, of the 4 heads
+      const int km = j - 2 * R::NK;
+      const uint32_t src = pg + (uint32_t)(km ? L.o_km : L.o_ks) +
+                           (uint32_t)((((t0 >> a.kg_shift) * L.H + h0) * D) * 2) + 16 * lane;
+      const bool ok = h0 + (16 * lane) / (2 * D) < L.H;
+      if (lane < D / 2) dma16(a.pages, ok ? src : pg, slot + R::OFF_KS + km * 4 * D * 2);
+    } else {  // V scale then V min: G/2 lanes of 16 bytes per token
+      const int lt = G / 2;
+      const int arr = lane / (16 * lt), t = (lane % (16 * lt)) / lt, piece = lane % lt;
+      const uint32_t src = pg + (uint32_t)(arr ? L.o_vm : L.o_vs) + (uint32_t)(((t0 + t) * L.H + h0) * G * 2 + piece * 16);
+      const bool ok = h0 + (piece * 16) / (2 * G) < L.H;
+      if (lane < 32 * lt) dma16(a.pages, ok ? src : pg, slot + R::OFF_VS);
     }
   }
-  // k_scale / k_min of the tile's K group: D/8 lanes each
-  const uint32_t ks = pg + (uint32_t)((t0 >> a.kg_shift) * L.H * D * 2);
-  if (lane < D / 4) dma16(a.pages, ks + k.ks_off, slot + R::OFF_S);
-  // V scale / min: G halves per token each, moved as G/2 dwords
-  const int G = D >> a.vg_shift;
-  const uint32_t vs = pg + (uint32_t)(t0 * L.H * G * 2);
-  if (lane < (G == 4 ? 64 : 32)) dma4(a.pages, vs + k.vs_off, slot + R::OFF_VS);
 }
 
-// One pipelined tile from LDS slot `sp` (tier BITS, K from codes); n_rel =
-// valid tokens of the tile counted from its first token.
-// in_res: the tile is the block's open K group (K from residual slot rslot;
-// its V, in the page, still comes through the ring).
+// One pipelined tile from LDS slot `sp` (tier BITS, K from codes): its scores
+// (log2 units, masked past n_rel valid tokens) and V fragments.
 template <int D, bool QLO, int BITS>
-__device__ __forceinline__ void compute_tile(Wave<D, QLO>& w, const DecodeArgs& a, const LaneConst<D, BITS>& k,
-                                             const uint8_t* sp, int t0, int n_rel, bool in_res, long rslot, int h,
-                                             int lane) {
+__device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const DecodeArgs& a, const LaneConst<D, BITS>& k,
+                                             const uint8_t* sp, int n_rel, int lane, float* x, h4_t* va) {
   using W = Wave<D, QLO>;
   using R = Ring<D, BITS>;
   constexpr int CPL = W::CPL, NQK = W::NQK, CPM = W::CPM;
   const int c = lane >> 4;
-  f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
-  if (in_res) {
-    s_from_residual<D, QLO>(w, a, rslot, t0, h, lane, sh, sl);
+  constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
+  uint32_t kw[KW];
+  if constexpr (BITS == 8) {
+    load_bytes<16>(sp + k.k_rd[0], kw);
+    load_bytes<16>(sp + k.k_rd[1], kw + 4);
   } else {
-    QK<D> qk;
-    {
-      uint32_t ks[CPL / 2], km[CPL / 2];
-      load_bytes<2 * CPL>(sp + k.s_rd, ks);
-      load_bytes<2 * CPL>(sp + k.s_rd + 2 * D, km);
-      build_qk<D, QLO>(qk, w, ks, km, a.scale_log2);
-    }
-    add_kmin<D, QLO>(qk, w, sh, sl);
-    constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
-    uint32_t kw[KW];
-    load_bytes<CPL * BITS / 8>(sp + k.k_rd, kw);
-    const CodeK ck = code_consts<BITS>();
-#pragma unroll
-    for (int j = 0; j < NQK; ++j) {
-      const h8_t kf = kfrag_j<BITS>(kw, j, ck);
-      sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.hi[j], sh, 0, 0, 0);
-      sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qk.lo[j], sl, 0, 0, 0);
-    }
-    unbias<D>(qk, sh, sl);
+    load_bytes<CPL * BITS / 8>(sp + k.k_rd[0], kw);
   }
-
   constexpr int VB = CPM * BITS / 8;
   constexpr int VW = VB >= 4 ? VB / 4 : 1;
   uint32_t vw[4][VW], vsh[4][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) load_bytes<VB>(sp + k.v_rd + i * R::KB, vw[i]);
+  for (int i = 0; i < 4; ++i) load_bytes<VB>(sp + k.v_rd[i], vw[i]);
   const int G = D >> a.vg_shift;
+  const int tok = 8 * G;  // bytes per token of the group's V scales (4 heads x G)
   const _Float16* vs = (const _Float16*)(sp + k.vs_rd);
-  const _Float16* vm = (const _Float16*)(sp + k.vm_rd);
-  h2_t s01 = {vs[0], vs[G]}, s23 = {vs[2 * G], vs[3 * G]};
-  h2_t m01 = {vm[0], vm[G]}, m23 = {vm[2 * G], vm[3 * G]};
-  float x[4];
+  const _Float16* vm = (const _Float16*)(sp + k.vs_rd + 16 * tok);
+  h2_t s01 = {vs[0], vs[tok / 2]}, s23 = {vs[tok], vs[3 * tok / 2]};
+  h2_t m01 = {vm[0], vm[tok / 2]}, m23 = {vm[tok], vm[3 * tok / 2]};
+
+  f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
+  const CodeK ck = code_consts<BITS>();
+#pragma unroll
+  for (int j = 0; j < NQK; ++j) {
+    uint32_t ks[4], km[4];
+    load_bytes<16>(sp + k.s_rd + 16 * j, ks);
+    load_bytes<16>(sp + k.s_rd + 4 * D * 2 + 16 * j, km);
+    s_block<D, QLO, BITS>(w, ks, km, kfrag_j<BITS>(kw, j, ck), j, sh, sl);
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) x[i] = (sh[i] + sl[i]) * a.scale_log2;
   if (n_rel < 16) {
@@ -651,19 +665,17 @@ __device__ __forceinline__ void compute_tile(Wave<D, QLO>& w, const DecodeArgs& 
   }
   vshift<BITS, VW>(vw, vsh);
   const CodeK vk = code_consts<BITS>();
-  h4_t va[CPM];
 #pragma unroll
   for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23, vk);
-  softmax_pv<D, QLO>(w, x, va);
 }
 
+// Wait for this wave's part of the tile about to be read: `ahead` tiles were
+// issued after it, M DMA instructions each (NB - 2 at most).
 template <int D, int BITS, int NB>
 __device__ __forceinline__ void wait_tile(int ahead) {
-  // `ahead` tiles were issued after the one about to be read.
   constexpr int M = Ring<D, BITS>::M;
-  if (NB >= 4 && ahead >= 3) wait_vmcnt<3 * M>();
-  else if (ahead >= 2) wait_vmcnt<2 * M>();
-  else if (ahead == 1) wait_vmcnt<M>();
+  if (NB >= 4 && ahead >= 2) wait_vmcnt<2 * M>();
+  else if (ahead >= 1) wait_vmcnt<M>();
   else wait_vmcnt<0>();
 }
 
@@ -722,8 +734,8 @@ __device__ __forceinline__ bool locate(const DecodeArgs& a, long si, int lane, i
 
 // One work item: split `split` of sequence `seq` for KV head h (one wave).
 template <int D, int BITS, bool QLO>
-__device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int split, int h, int lane,
-                                            uint8_t* my_ring, uint32_t ring0) {
+__device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int split, int hg, int wv, int lane,
+                                            uint8_t* ring, uint32_t ring0) {
   using W = Wave<D, QLO>;
   using R = Ring<D, BITS>;
   const Lay& L = a.L;
@@ -735,10 +747,12 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
   const long q_row = a.q_rows ? a.q_rows[seq] : seq;
   const long bt_row = a.bt_rows ? a.bt_rows[seq] : seq;
   const int c = lane >> 4, n = lane & 15;
+  const int h = hg * kHeadsPerGroup + wv;
+  const bool live = h < L.H;  // a wave past the last head still loads its share of every tile
 
   W w;
   {
-    const bool qv = n < a.gqa;
+    const bool qv = live && n < a.gqa;
     const long qb = q_row * a.q_s0 + (long)(h * a.gqa + (qv ? n : 0)) * a.q_s1 + c * W::CPL;
     float xq[W::CPL];
     if (qv) {
@@ -763,7 +777,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
   w.m_run = -__builtin_inff();
   w.l_lane = 0.f;
 
-  const LaneConst<D, BITS> kc = lane_const<D, BITS>(a, h, lane);
+  const LaneConst<D, BITS> kc = lane_const<D, BITS>(a, wv, lane);
   const int tpb_shift = a.bs_shift - 4;  // tiles per block = BS / 16
   const bool stats_ok = (D >> a.vg_shift) == 2 || (D >> a.vg_shift) == 4;
   for (int c0 = b_start; c0 < b_end; c0 += 64) {
@@ -772,53 +786,77 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
     const int last_tok = (c0 + nb) * L.BS < seq_len ? (c0 + nb) * L.BS : seq_len;
     const int n_tiles = (last_tok - c0 * L.BS + 15) >> 4;
 
+    // A tile takes the pipelined path when its block is stored at the kernel's
+    // tier with every chunk in range and it is not the block's open K group;
+    // the others (rare: demoted / downgraded blocks, each sequence's open
+    // group) are computed after the chunk's pipelined tiles, from global memory.
+    auto piped = [&](int tt) -> bool {
+      const int b = tt >> tpb_shift;
+      const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
+      const int frg = (int)rl((uint32_t)bl.fast_rg, b);
+      return frg != kNotFast && frg != (t0 >> a.kg_shift) && stats_ok;
+    };
     auto issue = [&](int tt) {
       const int b = tt >> tpb_shift;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
-      const bool fast = (int)rl((uint32_t)bl.fast_rg, b) != kNotFast && stats_ok;
       const uint32_t pg = rl(bl.pg, b);
       const uint32_t cb1 = BITS >= 4 ? rl(bl.cb1, b) : 0u;
       const uint32_t cb2 = BITS == 8 ? rl(bl.cb2, b) : 0u;
       const uint32_t cb3 = BITS == 8 ? rl(bl.cb3, b) : 0u;
       const uint32_t slot = ring0 + (uint32_t)((tt % R::NBUF) * R::SLOT);
-      issue_tile<D, BITS>(a, kc, slot, fast, t0, lane, pg, cb1, cb2, cb3);
+      issue_tile<D, BITS>(a, slot, piped(tt), t0, lane, wv, hg, pg, cb1, cb2, cb3);
     };
 
+    // Tile tt: wait for this wave's part of it, meet the others (every part has
+    // landed; every wave is done with tile tt - 1), refill tt - 1's slot with
+    // tile tt + NBUF - 1, compute tile tt.
+    bool rare = false;
 #pragma unroll 1
     for (int tt = 0; tt < R::NBUF - 1 && tt < n_tiles; ++tt) issue(tt);
 #pragma unroll 1
     for (int tt = 0; tt < n_tiles; ++tt) {
+      const int ahead = (n_tiles - 1 - tt) < (R::NBUF - 2) ? (n_tiles - 1 - tt) : (R::NBUF - 2);
+      wait_tile<D, BITS, R::NBUF>(ahead);
+      wg_barrier();
       if (tt + R::NBUF - 1 < n_tiles) issue(tt + R::NBUF - 1);
-      const int ahead = (n_tiles - 1 - tt) < (R::NBUF - 1) ? (n_tiles - 1 - tt) : (R::NBUF - 1);
       const int b = tt >> tpb_shift;
+      if ((int)rl((uint32_t)bl.blk, b) < 0) continue;
+      if (!piped(tt)) {
+        rare = true;
+        continue;
+      }
+      if (!live) continue;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
-      const long blk = (int)rl((uint32_t)bl.blk, b);
-      if (blk < 0) continue;
-      const int grp = t0 >> a.kg_shift;
-      const int frg = (int)rl((uint32_t)bl.fast_rg, b);
-      const bool fast = frg != kNotFast && stats_ok;
       const int n_valid = seq_len - ((c0 + b) << a.bs_shift);
-      if (fast) {
-        const bool in_res = frg == grp;  // frg = the block's residual group, -1: none
-        const long rslot = in_res ? (int)rl((uint32_t)bl.rslot, b) : -1;
-        wait_tile<D, BITS, R::NBUF>(ahead);
-        compute_tile<D, QLO, BITS>(w, a, kc, my_ring + (tt % R::NBUF) * R::SLOT, t0, n_valid - t0, in_res, rslot, h,
-                                   lane);
-      } else {
+      float x[4];
+      h4_t va[W::CPM];
+      compute_tile<D, QLO, BITS>(w, a, kc, ring + (tt % R::NBUF) * R::SLOT, n_valid - t0, lane, x, va);
+      softmax_pv<D, QLO>(w, x, va);
+    }
+    wait_vmcnt<0>();  // nothing of this chunk may still be landing in the ring
+    wg_barrier();     // every wave is done reading the ring before the next chunk refills it
+    if (rare && live) {
+#pragma unroll 1
+      for (int tt = 0; tt < n_tiles; ++tt) {
+        const int b = tt >> tpb_shift;
+        const long blk = (int)rl((uint32_t)bl.blk, b);
+        if (blk < 0 || piped(tt)) continue;
+        const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
         const int tier = (int)rl((uint32_t)bl.tier, b);
         const int rgrp = (int)rl((uint32_t)bl.rgrp, b);
         const long rslot = (int)rl((uint32_t)bl.rslot, b);
-        const bool in_res = rslot >= 0 && rgrp == grp;
-        if (tier == 4) tile<D, QLO, 4>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
-        else if (tier == 8) tile<D, QLO, 8>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
-        else tile<D, QLO, 2>(w, a, blk, t0, n_valid, rslot, in_res, h, lane);
+        const bool in_res = rslot >= 0 && rgrp == (t0 >> a.kg_shift);
+        const int n_valid = seq_len - ((c0 + b) << a.bs_shift);
+        float x[4];
+        h4_t va[W::CPM];
+        tile_any<D, QLO>(w, a, blk, t0, n_valid, rslot, in_res, h, lane, tier, x, va);
+        softmax_pv<D, QLO>(w, x, va);
       }
     }
-    wait_vmcnt<0>();  // nothing of this chunk may still be landing in the ring
   }
 
   const float l = rows_sum(w.l_lane);
-  if (n < a.gqa) {
+  if (live && n < a.gqa) {
     const long qh = (long)h * a.gqa + n;
     const long row = (seq * a.hq + qh) * a.num_splits + split;
     float* dst = a.acc + row * D;
@@ -843,12 +881,10 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
 // workgroups per CU; INT8's larger ring and the float32-query variant get two.
 template <int D, int BITS, bool QLO>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_kernel(DecodeArgs a) {
-  using R = Ring<D, BITS>;
   extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  uint8_t* my_ring = ring_lds + wv * R::WAVE_BYTES;
-  const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)my_ring);
+  const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)ring_lds);
   const int n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
   // The head groups of one split read neighbouring bytes of the same rows, and
   // rows start 16 bytes into a 128-byte line (the page format's offsets), so
@@ -864,8 +900,7 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   long seq;
   int split;
   if (!locate(a, item / n_hg, lane, incl0, tot0, seq, split)) return;
-  const int h = (int)(item % n_hg) * kHeadsPerGroup + wv;
-  if (h < a.L.H) decode_item<D, BITS, QLO>(a, seq, split, h, lane, my_ring, ring0);
+  decode_item<D, BITS, QLO>(a, seq, split, (int)(item % n_hg), wv, lane, ring_lds, ring0);
 }
 
 // Merge of the splits: one wave per (sequence, query head); lane l holds
@@ -962,7 +997,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
 template <int D, int BITS, bool QLO>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
   const dim3 block(64 * kHeadsPerGroup);
-  const size_t lds = (size_t)kHeadsPerGroup * Ring<D, BITS>::WAVE_BYTES;
+  const size_t lds = (size_t)Ring<D, BITS>::WG_BYTES;
   static bool attr = false;  // idempotent; set once per instantiation
   if (!attr) {
     if (hipFuncSetAttribute((const void*)decode_kernel<D, BITS, QLO>, hipFuncAttributeMaxDynamicSharedMemorySize,
