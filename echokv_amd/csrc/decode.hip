@@ -559,54 +559,109 @@ __device__ __forceinline__ LaneConst<D, BITS> lane_const(const DecodeArgs& a, in
   return k;
 }
 
-// This wave's share (jobs wv, wv + 4, ...) of the DMAs of one tile (16 tokens
-// from block offset t0) of head group hg into ring slot `slot`. pg / cb: the
-// block's page and chunk byte offsets.
+// The DMA jobs of a tile (16 tokens of head group hg) are dealt to the waves:
+// wave wv takes jobs wv, wv + 4, ... Each job's per-lane source offset does
+// not depend on the tile, only on the job, the lane and the head group, so it
+// is computed once per work item (JobLane); a tile adds a wave-uniform base.
+// A lane whose unit belongs to a head past the last (H not a multiple of 4)
+// loads the same unit of the last head instead: the bytes land in the slot of
+// a wave that computes nothing, and every address stays in the layer's pages.
+// Code rows: job jj of a side covers rows jj * RPI .. + RPI - 1 of the tile,
+// which lie in one chunk (RPI <= tokens per chunk for D >= 64).
 template <int D, int BITS>
-__device__ __forceinline__ void issue_tile(const DecodeArgs& a, uint32_t slot, bool fast, int t0, int lane, int wv,
-                                           int hg, uint32_t pg, uint32_t cb1, uint32_t cb2, uint32_t cb3) {
+struct JobLane {
+  uint32_t off[Ring<D, BITS>::M];
+};
+
+template <int D, int BITS>
+__device__ __forceinline__ JobLane<D, BITS> job_lane(const DecodeArgs& a, int wv, int hg, int lane) {
+  using R = Ring<D, BITS>;
+  static_assert(D >= 64, "a code-row job must not straddle two chunks");
+  const Lay& L = a.L;
+  const uint32_t rowb = (uint32_t)(2 * D * BITS / 8) * (uint32_t)L.H;
+  const int h0 = hg * 4, hl = L.H - 1;
+  const int G = D >> a.vg_shift;
+  JobLane<D, BITS> jl;
+#pragma unroll
+  for (int m = 0; m < R::M; ++m) {
+    const int j = wv + 4 * m;  // wave-uniform
+    uint32_t off = 0;
+    if (j < 2 * R::NK) {  // codes: RPI rows of one side
+      const int side = j >= R::NK;
+      const int jj = side ? j - R::NK : j;
+      const int ri = lane / R::U;
+      const int t = jj * R::RPI + ri;           // token within the tile
+      const int u = (lane % R::U + t) % R::U;  // unit of the segment this lane loads
+      const int hu = h0 + (u * 16) / R::KB;
+      const int hh = hu < hl ? hu : hl;
+      off = (uint32_t)ri * rowb + (side ? rowb / 2 : 0u) + (uint32_t)(hh * R::KB + (u * 16) % R::KB);
+    } else if (j < 2 * R::NK + 2) {  // k_scale, then k_min, of the 4 heads
+      const int hu = h0 + (16 * lane) / (2 * D);
+      const int hh = hu < hl ? hu : hl;
+      off = (uint32_t)((j - 2 * R::NK) ? L.o_km : L.o_ks) + (uint32_t)(hh * D * 2 + (16 * lane) % (2 * D));
+    } else if (j < R::J) {  // V scale then V min: G/2 lanes of 16 bytes per token
+      const int lt = G / 2 > 0 ? G / 2 : 1;
+      const int arr = lane / (16 * lt), t = (lane % (16 * lt)) / lt, piece = lane % lt;
+      const int hu = h0 + (piece * 16) / (2 * G);
+      const int hh = hu < hl ? hu : hl;
+      off = (uint32_t)(arr ? L.o_vm : L.o_vs) + (uint32_t)((t * L.H + hh) * G * 2 + (piece * 16) % (2 * G));
+    }
+    jl.off[m] = off;
+  }
+  return jl;
+}
+
+// Wave WV's share of the DMAs of one tile (16 tokens from block offset t0)
+// into ring slot `slot`; the wave's jobs are compile-time, so the per-tile work
+// is a few scalar operations and one vector add per DMA. pg / cb: the block's
+// page and chunk byte offsets; a tile the pipelined path does not take (fast
+// false) issues only dummies.
+template <int D, int BITS, int WV>
+__device__ __forceinline__ void issue_tile_w(const DecodeArgs& a, const JobLane<D, BITS>& jl, uint32_t slot, bool fast,
+                                             int t0, int lane, uint32_t pg, uint32_t cb1, uint32_t cb2, uint32_t cb3) {
   using R = Ring<D, BITS>;
   const Lay& L = a.L;
   constexpr int LB = BITS == 8 ? 3 : (BITS == 4 ? 2 : 1);
   const int tpc_shift = a.bs_shift + 1 - LB;  // tokens per chunk = 2 * BS / BITS
   const uint32_t rowb = (uint32_t)(2 * D * BITS / 8) * (uint32_t)L.H;
-  const int h0 = hg * 4;
   const int G = D >> a.vg_shift;
 #pragma unroll
   for (int m = 0; m < R::M; ++m) {
-    const int j = wv + 4 * m;  // wave-uniform
+    constexpr int j0 = WV;
+    const int j = j0 + 4 * m;  // compile-time after unrolling
     if (!fast || j >= R::J) {
       if (lane == 0) dma4(a.pages, pg, slot + R::OFF_DUMMY);
       continue;
     }
-    if (j < 2 * R::NK) {  // codes: RPI rows of one side
+    if (j < 2 * R::NK) {
       const int side = j >= R::NK;
       const int jj = side ? j - R::NK : j;
-      const int ri = lane / R::U;
-      const int t = jj * R::RPI + ri;               // token within the tile
-      const int u = (lane % R::U + t) % R::U;      // unit of the segment this lane loads
-      const uint32_t tt = (uint32_t)(t0 + t);
-      const uint32_t ch = tt >> tpc_shift;
+      const uint32_t tr = (uint32_t)(t0 + jj * R::RPI);  // the job's first token in the block
+      const uint32_t ch = tr >> tpc_shift;
       uint32_t cb = pg + (uint32_t)L.o_data;
       if constexpr (BITS >= 4) cb = ch == 1 ? cb1 : cb;
       if constexpr (BITS == 8) cb = ch == 2 ? cb2 : (ch == 3 ? cb3 : cb);
-      const bool head_ok = h0 + (u * 16) / R::KB < L.H;
-      const uint32_t off = cb + (tt & ((1u << tpc_shift) - 1)) * rowb + (side ? rowb / 2 : 0u) +
-                           (uint32_t)(h0 * R::KB + u * 16);
-      dma16(a.pages, head_ok ? off : pg, slot + (side ? R::OFF_V : 0) + 1024 * jj);
-    } else if (j < 2 * R::NK + 2) {  // k_scale, then k_min, of the 4 heads
-      const int km = j - 2 * R::NK;
-      const uint32_t src = pg + (uint32_t)(km ? L.o_km : L.o_ks) +
-                           (uint32_t)((((t0 >> a.kg_shift) * L.H + h0) * D) * 2) + 16 * lane;
-      const bool ok = h0 + (16 * lane) / (2 * D) < L.H;
-      if (lane < D / 2) dma16(a.pages, ok ? src : pg, slot + R::OFF_KS + km * 4 * D * 2);
-    } else {  // V scale then V min: G/2 lanes of 16 bytes per token
-      const int lt = G / 2;
-      const int arr = lane / (16 * lt), t = (lane % (16 * lt)) / lt, piece = lane % lt;
-      const uint32_t src = pg + (uint32_t)(arr ? L.o_vm : L.o_vs) + (uint32_t)(((t0 + t) * L.H + h0) * G * 2 + piece * 16);
-      const bool ok = h0 + (piece * 16) / (2 * G) < L.H;
-      if (lane < 32 * lt) dma16(a.pages, ok ? src : pg, slot + R::OFF_VS);
+      const uint32_t base = cb + (tr & ((1u << tpc_shift) - 1)) * rowb;
+      dma16(a.pages, base + jl.off[m], slot + (side ? R::OFF_V : 0) + 1024 * jj);
+    } else if (j < 2 * R::NK + 2) {
+      const uint32_t base = pg + (uint32_t)(((t0 >> a.kg_shift) * L.H) * D * 2);
+      if (lane < D / 2) dma16(a.pages, base + jl.off[m], slot + R::OFF_KS + (j - 2 * R::NK) * 4 * D * 2);
+    } else {
+      const uint32_t base = pg + (uint32_t)(t0 * L.H * G * 2);
+      if (lane < 16 * G) dma16(a.pages, base + jl.off[m], slot + R::OFF_VS);
     }
+  }
+}
+
+template <int D, int BITS>
+__device__ __forceinline__ void issue_tile(const DecodeArgs& a, const JobLane<D, BITS>& jl, uint32_t slot, bool fast,
+                                           int t0, int lane, int wv, uint32_t pg, uint32_t cb1, uint32_t cb2,
+                                           uint32_t cb3) {
+  switch (wv) {
+    case 0: issue_tile_w<D, BITS, 0>(a, jl, slot, fast, t0, lane, pg, cb1, cb2, cb3); break;
+    case 1: issue_tile_w<D, BITS, 1>(a, jl, slot, fast, t0, lane, pg, cb1, cb2, cb3); break;
+    case 2: issue_tile_w<D, BITS, 2>(a, jl, slot, fast, t0, lane, pg, cb1, cb2, cb3); break;
+    default: issue_tile_w<D, BITS, 3>(a, jl, slot, fast, t0, lane, pg, cb1, cb2, cb3); break;
   }
 }
 
@@ -681,17 +736,11 @@ __device__ __forceinline__ void wait_tile(int ahead) {
 
 __device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 
-// Blocks per split of a sequence of `len` tokens and the number of its splits
-// (0 for an empty sequence): max(blocks_per_split, ceil(blocks / num_splits)).
+// Blocks per split of a sequence of n_blocks blocks:
+// max(blocks_per_split, ceil(blocks / num_splits)).
 __device__ __forceinline__ int split_blocks(const DecodeArgs& a, int n_blocks) {
   const int per = (n_blocks + a.num_splits - 1) / a.num_splits;
   return a.bps > per ? a.bps : per;
-}
-__device__ __forceinline__ int used_splits(const DecodeArgs& a, int len) {
-  if (len <= 0) return 0;
-  const int nb = (len + a.L.BS - 1) >> a.bs_shift;
-  const int bps = split_blocks(a, nb);
-  return (nb + bps - 1) / bps;
 }
 
 __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
@@ -703,31 +752,57 @@ __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
   return x;
 }
 
-// Inclusive prefix of the split counts of sequences [s0, s0 + 64), one per lane.
+// Inclusive prefixes over sequences [s0, s0 + 64), one per lane, of the
+// number of splits before the last (bits 7 and up) and of last splits (low 7
+// bits: at most 64).
 __device__ __forceinline__ int scan_chunk(const DecodeArgs& a, long s0, int lane) {
   const long s = s0 + lane;
-  return wave_incl_scan(s < a.num_seqs ? used_splits(a, (int)a.lens[s]) : 0, lane);
+  const int len = s < a.num_seqs ? (int)a.lens[s] : 0;
+  int x = 0;
+  if (len > 0) {
+    const int nb = (len + a.L.BS - 1) >> a.bs_shift;
+    const int bps = split_blocks(a, nb);
+    x = (((nb + bps - 1) / bps - 1) << 7) | 1;
+  }
+  return wave_incl_scan(x, lane);
+}
+__device__ __forceinline__ int scan_total(int incl) {
+  const int t = __builtin_amdgcn_readlane(incl, 63);
+  return (t >> 7) + (t & 127);
 }
 
-// The si-th split (in sequence order) of the batch's non-empty splits; false
-// past the last one. incl0 / tot0: the scan of the first 64 sequences.
-__device__ __forceinline__ bool locate(const DecodeArgs& a, long si, int lane, int incl0, int tot0, long& seq,
-                                       int& split) {
-  long base = 0;
-  int incl = incl0, tot = tot0;
-  for (long s0 = 0; s0 < a.num_seqs; s0 += 64) {
-    if (s0 > 0) {
-      incl = scan_chunk(a, s0, lane);
-      tot = __builtin_amdgcn_readlane(incl, 63);
+// The si-th of the batch's non-empty splits, false past the last one. Order:
+// every sequence's last split (sequence order), then the others (sequence
+// order). A last split is the irregular one -- shorter, and holding the open K
+// group, whose tiles take the slower generic path -- so it starts early and
+// the work items dispatched last, whose run time is the kernel's tail, are
+// the uniform full ones. incl0: scan_chunk of the first 64 sequences.
+__device__ __forceinline__ bool locate(const DecodeArgs& a, long si, int lane, int incl0, long& seq, int& split) {
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int shift = pass == 0 ? 0 : 7, mask = pass == 0 ? 127 : -1;
+    long base = 0;
+    int incl = incl0;
+    for (long s0 = 0; s0 < a.num_seqs; s0 += 64) {
+      if (s0 > 0) incl = scan_chunk(a, s0, lane);
+      const int mine = (incl >> shift) & mask;
+      const int tot = __builtin_amdgcn_readlane(mine, 63);
+      if (si < base + tot) {
+        const int k = __builtin_popcountll(__builtin_amdgcn_ballot_w64(base + mine <= si));
+        const int excl = k == 0 ? 0 : __builtin_amdgcn_readlane(mine, k - 1);
+        seq = s0 + k;
+        if (pass == 1) {
+          split = (int)(si - base - excl);
+        } else {  // the last split: after the sequence's others
+          const int prev_incl = __builtin_amdgcn_readlane(incl, k) >> 7;
+          const int prev_excl = k == 0 ? 0 : __builtin_amdgcn_readlane(incl, k - 1) >> 7;
+          split = prev_incl - prev_excl;
+        }
+        return true;
+      }
+      base += tot;
     }
-    if (si < base + tot) {
-      const int k = __builtin_popcountll(__builtin_amdgcn_ballot_w64(base + incl <= si));
-      const int excl = k == 0 ? 0 : __builtin_amdgcn_readlane(incl, k - 1);
-      seq = s0 + k;
-      split = (int)(si - base - excl);
-      return true;
-    }
-    base += tot;
+    si -= base;
   }
   return false;
 }
@@ -778,6 +853,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
   w.l_lane = 0.f;
 
   const LaneConst<D, BITS> kc = lane_const<D, BITS>(a, wv, lane);
+  const JobLane<D, BITS> jl = job_lane<D, BITS>(a, wv, hg, lane);
   const int tpb_shift = a.bs_shift - 4;  // tiles per block = BS / 16
   const bool stats_ok = (D >> a.vg_shift) == 2 || (D >> a.vg_shift) == 4;
   for (int c0 = b_start; c0 < b_end; c0 += 64) {
@@ -790,11 +866,16 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
     // tier with every chunk in range and it is not the block's open K group;
     // the others (rare: demoted / downgraded blocks, each sequence's open
     // group) are computed after the chunk's pipelined tiles, from global memory.
+    // Per-block bit masks (one bit per lane = block) keep the per-tile test scalar.
+    const uint64_t m_fast = stats_ok ? __builtin_amdgcn_ballot_w64(bl.fast_rg != kNotFast) : 0ull;
+    const uint64_t m_open = __builtin_amdgcn_ballot_w64(bl.fast_rg >= 0);
+    const uint64_t m_blk = __builtin_amdgcn_ballot_w64(bl.blk >= 0);
     auto piped = [&](int tt) -> bool {
       const int b = tt >> tpb_shift;
+      if (!((m_fast >> b) & 1)) return false;
+      if (!((m_open >> b) & 1)) return true;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
-      const int frg = (int)rl((uint32_t)bl.fast_rg, b);
-      return frg != kNotFast && frg != (t0 >> a.kg_shift) && stats_ok;
+      return (int)rl((uint32_t)bl.fast_rg, b) != (t0 >> a.kg_shift);
     };
     auto issue = [&](int tt) {
       const int b = tt >> tpb_shift;
@@ -804,7 +885,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
       const uint32_t cb2 = BITS == 8 ? rl(bl.cb2, b) : 0u;
       const uint32_t cb3 = BITS == 8 ? rl(bl.cb3, b) : 0u;
       const uint32_t slot = ring0 + (uint32_t)((tt % R::NBUF) * R::SLOT);
-      issue_tile<D, BITS>(a, slot, piped(tt), t0, lane, wv, hg, pg, cb1, cb2, cb3);
+      issue_tile<D, BITS>(a, jl, slot, piped(tt), t0, lane, wv, pg, cb1, cb2, cb3);
     };
 
     // Tile tt: wait for this wave's part of it, meet the others (every part has
@@ -820,7 +901,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
       wg_barrier();
       if (tt + R::NBUF - 1 < n_tiles) issue(tt + R::NBUF - 1);
       const int b = tt >> tpb_shift;
-      if ((int)rl((uint32_t)bl.blk, b) < 0) continue;
+      if (!((m_blk >> b) & 1)) continue;
       if (!piped(tt)) {
         rare = true;
         continue;
@@ -883,7 +964,7 @@ template <int D, int BITS, bool QLO>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar job branches
   const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)ring_lds);
   const int n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
   // The head groups of one split read neighbouring bytes of the same rows, and
@@ -895,11 +976,10 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   const long r = blockIdx.x % span;
   const long item = blockIdx.x - r + (r % 8) * n_hg + r / 8;
   const int incl0 = scan_chunk(a, 0, lane);
-  const int tot0 = __builtin_amdgcn_readlane(incl0, 63);
-  if (a.num_seqs <= 64 && item >= (long)tot0 * n_hg) return;  // past the last non-empty split
+  if (a.num_seqs <= 64 && item >= (long)scan_total(incl0) * n_hg) return;  // past the last non-empty split
   long seq;
   int split;
-  if (!locate(a, item / n_hg, lane, incl0, tot0, seq, split)) return;
+  if (!locate(a, item / n_hg, lane, incl0, seq, split)) return;
   decode_item<D, BITS, QLO>(a, seq, split, (int)(item % n_hg), wv, lane, ring_lds, ring0);
 }
 
