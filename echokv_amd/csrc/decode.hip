@@ -74,6 +74,14 @@ __device__ __forceinline__ CodeK code_consts() {
   return k;
 }
 
+// INT4 / INT2 codes as fp16 without a bias: a byte b < 16 read as an OCP E4M3
+// fp8 value is exactly b * 2^-9, so gfx950's fp8 -> fp16 conversion with the
+// scale 2^9 gives the code itself. Two bytes (0-1, or 2-3 with HI) per call.
+template <bool HI>
+__device__ __forceinline__ uint32_t cvt_codes(uint32_t bytes) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(bytes, 512.0f, HI));
+}
+
 // (x & mask) holds two codes at bits 0.. and 16..; as the fp16 pair 1024 + c (exact).
 __device__ __forceinline__ uint32_t biased_pair(uint32_t x, const CodeK& k) { return (x & k.mask) | k.magic; }
 // ... and as c itself.
@@ -82,15 +90,18 @@ __device__ __forceinline__ h2_t code_pair(uint32_t x, const CodeK& k) {
   return u2h(biased_pair(x, k)) - k1024;
 }
 
-// Eight consecutive channels of a K row, natural order, as an MFMA fragment of
-// 1024 + code (s_block takes the bias back out with one more contraction).
-// INT4: one word (8 nibbles); INT8: two words; INT2: bytes 2*hf, 2*hf+1 of one word.
+// Eight consecutive channels of a K row, natural order, as an MFMA fragment.
+// INT4: one word (8 nibbles), the codes themselves (cvt_codes); INT8: two
+// words, INT2: bytes 2*hf, 2*hf+1 of one word, as 1024 + code (s_block takes
+// the bias back out with one more contraction).
 template <int BITS>
 __device__ __forceinline__ h8_t kfrag(const uint32_t* w, int hf, const CodeK& k) {
   if constexpr (BITS == 4) {
-    const uint32_t x = w[0], x4 = x >> 4;
-    return w2h8(biased_pair(perm(x4, x, pair_sel(0, 0)), k), biased_pair(perm(x4, x, pair_sel(1, 1)), k),
-                biased_pair(perm(x4, x, pair_sel(2, 2)), k), biased_pair(perm(x4, x, pair_sel(3, 3)), k));
+    const uint32_t x = w[0];
+    const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;  // even / odd channels, one per byte
+    const uint32_t c03 = perm(hi, lo, 0x05010400u), c47 = perm(hi, lo, 0x07030602u);
+    (void)k;
+    return w2h8(cvt_codes<false>(c03), cvt_codes<true>(c03), cvt_codes<false>(c47), cvt_codes<true>(c47));
   } else if constexpr (BITS == 8) {
     const uint32_t m = 0x64646464u;  // perm(m, x, ...) puts 0x64 above each code byte
     return w2h8(perm(m, w[0], 0x04010400u), perm(m, w[0], 0x04030402u), perm(m, w[1], 0x04010400u),
@@ -135,6 +146,37 @@ __device__ __forceinline__ h4_t vfrag(int j, const uint32_t (*v)[VW], const uint
   return h4_t{v01[0], v01[1], v23[0], v23[1]};
 }
 
+// INT4 V^T operands of all the lane's CPM (4 or 8) channels: each token's word is
+// split into even / odd channels one per byte, a v_perm pairs tokens (0, 1) or
+// (2, 3) for two channels at once, cvt_codes makes the exact fp16 codes and one
+// fma dequantizes (c * s + m, one rounding).
+template <int CPM>
+__device__ __forceinline__ void vfrags4(const uint32_t (*v)[1], h2_t s01, h2_t s23, h2_t m01, h2_t m23, h4_t* va) {
+  static_assert(CPM == 4 || CPM == 8, "INT4 V: the lane's channels of a token fit one word");
+  uint32_t b[4][2];  // [token][even / odd channels]
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    b[i][0] = v[i][0] & 0x0F0F0F0Fu;
+    b[i][1] = (v[i][0] >> 4) & 0x0F0F0F0Fu;
+  }
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+#pragma unroll
+    for (int hb = 0; hb < CPM / 4; ++hb) {  // channel bytes 2hb, 2hb+1 -> channels 4hb+p, 4hb+2+p
+      const uint32_t sel = 0x04000400u | (uint32_t)(2 * hb) | ((uint32_t)(2 * hb) << 8) | ((uint32_t)(2 * hb + 1) << 16) |
+                           ((uint32_t)(2 * hb + 1) << 24);
+      const uint32_t x01 = perm(b[1][p], b[0][p], sel), x23 = perm(b[3][p], b[2][p], sel);
+      const int j0 = 4 * hb + p, j1 = j0 + 2;
+      const h2_t a0 = __builtin_elementwise_fma(u2h(cvt_codes<false>(x01)), s01, m01);
+      const h2_t a1 = __builtin_elementwise_fma(u2h(cvt_codes<false>(x23)), s23, m23);
+      const h2_t c0 = __builtin_elementwise_fma(u2h(cvt_codes<true>(x01)), s01, m01);
+      const h2_t c1 = __builtin_elementwise_fma(u2h(cvt_codes<true>(x23)), s23, m23);
+      va[j0] = h4_t{a0[0], a0[1], a1[0], a1[1]};
+      va[j1] = h4_t{c0[0], c0[1], c1[0], c1[1]};
+    }
+  }
+}
+
 // Shifted copies of the V words that vfrag reads (INT4: >> 0, 4; INT2: >> 0, 2, 4, 6).
 template <int BITS, int VW>
 __device__ __forceinline__ void vshift(const uint32_t (*v)[VW], uint32_t (*vs)[4]) {
@@ -175,12 +217,25 @@ __device__ __forceinline__ void load_bytes(const uint8_t* p, uint32_t* w) {
   }
 }
 
+// max without the NaN-quieting canonicalizations fmaxf adds around values of
+// unknown origin (the scores are never NaN: masked ones are -inf).
+__device__ __forceinline__ float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Cross-row (lanes l, l^16, l^32, l^48) reductions; every lane gets the result.
 __device__ __forceinline__ float rows_max(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  x = vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
   const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+  return vmax(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
 __device__ __forceinline__ float rows_sum(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -203,7 +258,7 @@ struct Wave {
 
 // S^T of one 16-token tile from its codes, K group by 32-channel block j:
 //   S^T += codes_j . (q * k_scale)_j^T   as fp16 hi / lo pairs (two chains)
-//        - 1024 * sum_d (q * k_scale)_j  (the code fragments carry 1024 + c)
+//        - 1024 * sum_d (q * k_scale)_j  (INT8 / INT2 fragments carry 1024 + c)
 //        + k_min_j . q_j^T               (and q lo for float32 queries)
 // The products q * s are exact in fp32; hi = fp16(q * s), lo = fp16(fma(q, s,
 // -hi)) keeps S accurate to ~2^-22 relative. Each block's operands are built
@@ -228,8 +283,12 @@ __device__ __forceinline__ void s_block(const Wave<D, QLO>& w, const uint32_t* k
   const h8_t mn = w2h8(km[0], km[1], km[2], km[3]);
   sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, h8, sh, 0, 0, 0);
   sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, l8, sl, 0, 0, 0);
-  sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, h8, sh, 0, 0, 0);
-  sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, l8, sl, 0, 0, 0);
+  if constexpr (BITS != 4) {  // INT4 fragments carry the codes themselves
+    sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, h8, sh, 0, 0, 0);
+    sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, l8, sl, 0, 0, 0);
+  } else {
+    (void)m1024;
+  }
   sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(
       mn, w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2], w.qn[4 * j + 3]), sh, 0, 0, 0);
   if constexpr (QLO)
@@ -271,8 +330,8 @@ __device__ __forceinline__ void s_from_residual(const Wave<D, QLO>& w, const Dec
 // Online-softmax update with the tile's scores x (log2 units, masked), then O^T += V^T P^T.
 template <int D, bool QLO>
 __device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, const h4_t* va) {
-  const float mt = rows_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
-  const float m_new = fmaxf(w.m_run, mt);
+  const float mt = rows_max(vmax(vmax3(x[0], x[1], x[2]), x[3]));
+  const float m_new = vmax(w.m_run, mt);
   if (__builtin_amdgcn_ballot_w64(m_new > w.m_run + kLazyRescale)) {
     const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);  // m_run = -inf at the start: 0
     w.l_lane *= alpha;
@@ -537,7 +596,7 @@ struct LaneConst {
   uint32_t k_rd[BITS == 8 ? 2 : 1];  // K codes of token n, channels c * D/4 .. (16-byte units; INT2: + 8 * (c & 1))
   uint32_t v_rd[4];                  // V codes of tokens 4c + i, the lane's CPM channels
   uint32_t s_rd;                     // k_scale (k_min at + 4 * D * 2)
-  uint32_t vs_rd;                    // V scale of token 4c (V min at vm_off; tokens 4c + i at + i * tok stride)
+  uint32_t vs_rd;                    // V scale of token 4c (32-byte rows: token 4c + i at + 32 i, V min at + 512)
 };
 
 template <int D, int BITS>
@@ -555,7 +614,7 @@ __device__ __forceinline__ LaneConst<D, BITS> lane_const(const DecodeArgs& a, in
   k.s_rd = (uint32_t)(R::OFF_KS + wv * D * 2 + 2 * c * CPL);
   const int G = D >> a.vg_shift;
   const int g = (n * CPM) >> a.vg_shift;
-  k.vs_rd = (uint32_t)(R::OFF_VS + 4 * c * 8 * G + (wv * G + g) * 2);
+  k.vs_rd = (uint32_t)(R::OFF_VS + 4 * c * 32 + (wv * G + g) * 2);  // 32 bytes per token
   return k;
 }
 
@@ -599,9 +658,9 @@ __device__ __forceinline__ JobLane<D, BITS> job_lane(const DecodeArgs& a, int wv
       const int hu = h0 + (16 * lane) / (2 * D);
       const int hh = hu < hl ? hu : hl;
       off = (uint32_t)((j - 2 * R::NK) ? L.o_km : L.o_ks) + (uint32_t)(hh * D * 2 + (16 * lane) % (2 * D));
-    } else if (j < R::J) {  // V scale then V min: G/2 lanes of 16 bytes per token
-      const int lt = G / 2 > 0 ? G / 2 : 1;
-      const int arr = lane / (16 * lt), t = (lane % (16 * lt)) / lt, piece = lane % lt;
+    } else if (j < R::J) {  // V scale then V min: 2 lanes of 16 bytes per token (32-byte rows in LDS)
+      const int arr = lane / 32, t = (lane % 32) / 2;
+      const int piece = G == 4 ? lane % 2 : 0;  // G == 2: 16 bytes per token, the odd lane repeats it
       const int hu = h0 + (piece * 16) / (2 * G);
       const int hh = hu < hl ? hu : hl;
       off = (uint32_t)(arr ? L.o_vm : L.o_vs) + (uint32_t)((t * L.H + hh) * G * 2 + (piece * 16) % (2 * G));
@@ -648,7 +707,7 @@ __device__ __forceinline__ void issue_tile_w(const DecodeArgs& a, const JobLane<
       if (lane < D / 2) dma16(a.pages, base + jl.off[m], slot + R::OFF_KS + (j - 2 * R::NK) * 4 * D * 2);
     } else {
       const uint32_t base = pg + (uint32_t)(t0 * L.H * G * 2);
-      if (lane < 16 * G) dma16(a.pages, base + jl.off[m], slot + R::OFF_VS);
+      dma16(a.pages, base + jl.off[m], slot + R::OFF_VS);
     }
   }
 }
@@ -687,21 +746,26 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
   uint32_t vw[4][VW], vsh[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) load_bytes<VB>(sp + k.v_rd[i], vw[i]);
-  const int G = D >> a.vg_shift;
-  const int tok = 8 * G;  // bytes per token of the group's V scales (4 heads x G)
+  // V scale / min of the lane's 4 tokens: 32-byte rows per token, scales then mins.
   const _Float16* vs = (const _Float16*)(sp + k.vs_rd);
-  const _Float16* vm = (const _Float16*)(sp + k.vs_rd + 16 * tok);
-  h2_t s01 = {vs[0], vs[tok / 2]}, s23 = {vs[tok], vs[3 * tok / 2]};
-  h2_t m01 = {vm[0], vm[tok / 2]}, m23 = {vm[tok], vm[3 * tok / 2]};
+  h2_t s01 = {vs[0], vs[16]}, s23 = {vs[32], vs[48]};
+  h2_t m01 = {vs[256], vs[272]}, m23 = {vs[288], vs[304]};
 
   f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
   const CodeK ck = code_consts<BITS>();
+  // k_scale / k_min words one 32-channel block ahead of their use, so each
+  // block's LDS reads are in flight under the previous block's MFMAs.
+  uint32_t ks[2][4], km[2][4];
+  load_bytes<16>(sp + k.s_rd, ks[0]);
+  load_bytes<16>(sp + k.s_rd + 4 * D * 2, km[0]);
 #pragma unroll
   for (int j = 0; j < NQK; ++j) {
-    uint32_t ks[4], km[4];
-    load_bytes<16>(sp + k.s_rd + 16 * j, ks);
-    load_bytes<16>(sp + k.s_rd + 4 * D * 2 + 16 * j, km);
-    s_block<D, QLO, BITS>(w, ks, km, kfrag_j<BITS>(kw, j, ck), j, sh, sl);
+    if (j + 1 < NQK) {
+      load_bytes<16>(sp + k.s_rd + 16 * (j + 1), ks[(j + 1) & 1]);
+      load_bytes<16>(sp + k.s_rd + 4 * D * 2 + 16 * (j + 1), km[(j + 1) & 1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the next block's reads above this block's math
+    s_block<D, QLO, BITS>(w, ks[j & 1], km[j & 1], kfrag_j<BITS>(kw, j, ck), j, sh, sl);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) x[i] = (sh[i] + sl[i]) * a.scale_log2;
@@ -718,10 +782,15 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = t + i < n_rel ? x[i] : -__builtin_inff();
   }
-  vshift<BITS, VW>(vw, vsh);
-  const CodeK vk = code_consts<BITS>();
+  if constexpr (BITS == 4) {
+    (void)vsh;
+    vfrags4<CPM>(vw, s01, s23, m01, m23, va);
+  } else {
+    vshift<BITS, VW>(vw, vsh);
+    const CodeK vk = code_consts<BITS>();
 #pragma unroll
-  for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23, vk);
+    for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23, vk);
+  }
 }
 
 // Wait for this wave's part of the tile about to be read: `ahead` tiles were
