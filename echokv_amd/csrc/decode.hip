@@ -146,34 +146,29 @@ __device__ __forceinline__ h4_t vfrag(int j, const uint32_t (*v)[VW], const uint
   return h4_t{v01[0], v01[1], v23[0], v23[1]};
 }
 
-// INT4 V^T operands of all the lane's CPM (4 or 8) channels: each token's word is
-// split into even / odd channels one per byte, a v_perm pairs tokens (0, 1) or
-// (2, 3) for two channels at once, cvt_codes makes the exact fp16 codes and one
-// fma dequantizes (c * s + m, one rounding).
+// INT4 V^T operands of all the lane's CPM (4 or 8) channels: a v_perm pairs the
+// bytes of tokens (0, 1) or (2, 3) holding four channels, the nibbles split into
+// even / odd channels one per byte, cvt_codes makes the exact fp16 codes and
+// one fma dequantizes (c * s + m, one rounding).
 template <int CPM>
 __device__ __forceinline__ void vfrags4(const uint32_t (*v)[1], h2_t s01, h2_t s23, h2_t m01, h2_t m23, h4_t* va) {
   static_assert(CPM == 4 || CPM == 8, "INT4 V: the lane's channels of a token fit one word");
-  uint32_t b[4][2];  // [token][even / odd channels]
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    b[i][0] = v[i][0] & 0x0F0F0F0Fu;
-    b[i][1] = (v[i][0] >> 4) & 0x0F0F0F0Fu;
-  }
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-#pragma unroll
-    for (int hb = 0; hb < CPM / 4; ++hb) {  // channel bytes 2hb, 2hb+1 -> channels 4hb+p, 4hb+2+p
-      const uint32_t sel = 0x04000400u | (uint32_t)(2 * hb) | ((uint32_t)(2 * hb) << 8) | ((uint32_t)(2 * hb + 1) << 16) |
-                           ((uint32_t)(2 * hb + 1) << 24);
-      const uint32_t x01 = perm(b[1][p], b[0][p], sel), x23 = perm(b[3][p], b[2][p], sel);
-      const int j0 = 4 * hb + p, j1 = j0 + 2;
-      const h2_t a0 = __builtin_elementwise_fma(u2h(cvt_codes<false>(x01)), s01, m01);
-      const h2_t a1 = __builtin_elementwise_fma(u2h(cvt_codes<false>(x23)), s23, m23);
-      const h2_t c0 = __builtin_elementwise_fma(u2h(cvt_codes<true>(x01)), s01, m01);
-      const h2_t c1 = __builtin_elementwise_fma(u2h(cvt_codes<true>(x23)), s23, m23);
-      va[j0] = h4_t{a0[0], a0[1], a1[0], a1[1]};
-      va[j1] = h4_t{c0[0], c0[1], c1[0], c1[1]};
-    }
+  for (int hb = 0; hb < CPM / 4; ++hb) {  // bytes 2hb, 2hb+1 of each token: channels 4hb .. 4hb+3
+    const uint32_t sel = (uint32_t)(2 * hb) | ((uint32_t)(4 + 2 * hb) << 8) | ((uint32_t)(2 * hb + 1) << 16) |
+                         ((uint32_t)(4 + 2 * hb + 1) << 24);
+    const uint32_t x01 = perm(v[1][0], v[0][0], sel), x23 = perm(v[3][0], v[2][0], sel);
+    const uint32_t e01 = x01 & 0x0F0F0F0Fu, o01 = (x01 >> 4) & 0x0F0F0F0Fu;  // even / odd channels
+    const uint32_t e23 = x23 & 0x0F0F0F0Fu, o23 = (x23 >> 4) & 0x0F0F0F0Fu;
+    auto frag = [&](uint32_t c01, uint32_t c23) {
+      const h2_t a0 = __builtin_elementwise_fma(u2h(c01), s01, m01);
+      const h2_t a1 = __builtin_elementwise_fma(u2h(c23), s23, m23);
+      return h4_t{a0[0], a0[1], a1[0], a1[1]};
+    };
+    va[4 * hb] = frag(cvt_codes<false>(e01), cvt_codes<false>(e23));
+    va[4 * hb + 1] = frag(cvt_codes<false>(o01), cvt_codes<false>(o23));
+    va[4 * hb + 2] = frag(cvt_codes<true>(e01), cvt_codes<true>(e23));
+    va[4 * hb + 3] = frag(cvt_codes<true>(o01), cvt_codes<true>(o23));
   }
 }
 
@@ -253,7 +248,8 @@ struct Wave {
   uint32_t qn[CPL / 2];               // fp16 query pairs (hi), natural channel order
   uint32_t ql[QLO ? CPL / 2 : 1];     // fp16 query pairs (lo = q - hi)
   f4_t acc[CPM];                      // O^T fragments
-  float m_run, l_lane;
+  float m_run, l_lane;                // running max (scaled log2 units), this lane's sum
+  float scale;                        // |softmax scale| * log2(e), > 0 (a negative scale negates the query)
 };
 
 // S^T of one 16-token tile from its codes, K group by 32-channel block j:
@@ -327,10 +323,11 @@ __device__ __forceinline__ void s_from_residual(const Wave<D, QLO>& w, const Dec
   }
 }
 
-// Online-softmax update with the tile's scores x (log2 units, masked), then O^T += V^T P^T.
+// Online-softmax update with the tile's unscaled scores x (masked: -inf), then
+// O^T += V^T P^T. p = exp2(scale * x - m): the scale rides in the fma.
 template <int D, bool QLO>
 __device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, const h4_t* va) {
-  const float mt = rows_max(vmax(vmax3(x[0], x[1], x[2]), x[3]));
+  const float mt = rows_max(vmax(vmax3(x[0], x[1], x[2]), x[3])) * w.scale;
   const float m_new = vmax(w.m_run, mt);
   if (__builtin_amdgcn_ballot_w64(m_new > w.m_run + kLazyRescale)) {
     const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);  // m_run = -inf at the start: 0
@@ -341,7 +338,7 @@ __device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, cons
   }
   float p[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(x[i] - w.m_run);
+  for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], w.scale, -w.m_run));
   w.l_lane += (p[0] + p[1]) + (p[2] + p[3]);
   const h4_t pb = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
 #pragma unroll
@@ -432,7 +429,7 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float v = (sh[i] + sl[i]) * a.scale_log2;
+    const float v = sh[i] + sl[i];
     x[i] = (t0 + 4 * c + i < n_valid) ? v : -__builtin_inff();
   }
 
@@ -768,7 +765,7 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
     s_block<D, QLO, BITS>(w, ks[j & 1], km[j & 1], kfrag_j<BITS>(kw, j, ck), j, sh, sl);
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = (sh[i] + sl[i]) * a.scale_log2;
+  for (int i = 0; i < 4; ++i) x[i] = sh[i] + sl[i];
   if (n_rel < 16) {
     // The block's last tile: tokens past the sequence get p = 0 and V = 0 (their
     // page bytes are arbitrary and 0 * inf would poison the sum).
@@ -899,6 +896,12 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
     const bool qv = live && n < a.gqa;
     const long qb = q_row * a.q_s0 + (long)(h * a.gqa + (qv ? n : 0)) * a.q_s1 + c * W::CPL;
     float xq[W::CPL];
+    // Scores are scaled inside the exponent (exp2(s * x - m)); the max is taken
+    // on unscaled scores, which needs the scale positive: a negative one flips
+    // the query's sign (exact), a zero one becomes 2^-100 (every weight equal,
+    // as at zero, and masked scores stay -inf).
+    const float q_sign = a.scale_log2 < 0.f ? -1.f : 1.f;
+    w.scale = fmaxf(fabsf(a.scale_log2), 7.8886090522101181e-31f);
     if (qv) {
       ld_n<W::CPL>(a.q, a.q_dtype, qb, xq);
     } else {
@@ -907,7 +910,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
     }
 #pragma unroll
     for (int i = 0; i < W::CPL / 2; ++i) {
-      const float x0 = xq[2 * i], x1 = xq[2 * i + 1];
+      const float x0 = q_sign * xq[2 * i], x1 = q_sign * xq[2 * i + 1];
       const h2_t hi = {(_Float16)x0, (_Float16)x1};
       w.qn[i] = h2u(hi);
       if constexpr (QLO) {

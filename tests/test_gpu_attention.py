@@ -66,6 +66,26 @@ def test_decode_matches_oracle(device, case_stores, i, bps, qdt):
         assert err <= TOL, f"{s.name} gqa={gqa} bps={bps}: max err {err}"
 
 
+@pytest.mark.parametrize("scale", [-0.088, 0.0, 0.9])
+def test_decode_softmax_scale_sign_and_zero(device, case_stores, scale):
+    """The kernels take the max on unscaled scores and scale inside the
+    exponent; a negative scale (query sign flipped) and a zero one (every
+    weight equal) must still match the oracle's softmax(scale * q.k)."""
+    for i in range(len(S.DECODE_CASES)):
+        s, sim, store = case_stores[i]
+        print(f"[decode] {s.name} scale={scale}", flush=True)
+        table = t(s.meta["table"], device, torch.int32)
+        lens = t(s.meta["lens"], device)
+        rng = np.random.default_rng(7)
+        q = rng.standard_normal((len(s.meta["lens"]), 4 * s.h, s.d), dtype=np.float32)
+        qt = t(q, device, torch.float16)
+        ref = OA.decode_attention(sim.ps, qt.float().cpu().numpy(), s.meta["table"], s.meta["lens"], scale)
+        got = dec.decode_attention(store, qt, table, lens, scale, blocks_per_split=2)
+        torch.cuda.synchronize()
+        err = maxdiff(got, ref)
+        assert err <= TOL, f"{s.name} scale={scale}: max err {err}"
+
+
 def test_decode_is_batch_invariant(device, case_stores):
     s, sim, store = case_stores[0]
     table = t(s.meta["table"], device, torch.int32)
