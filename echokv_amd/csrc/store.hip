@@ -93,23 +93,27 @@ __global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) 
 // stats over the n tokens, then codes for each token at offset off0 + p.
 // ---------------------------------------------------------------------------
 template <typename Fetch>
-__device__ void quantize_k_group(const Lay& L, uint8_t* pages, long blk, int grp, int off0, int n, int bits, int h,
+__device__ __forceinline__ void quantize_k_group(const Lay& L, uint8_t* pages, long blk, int grp, int off0, int n, int bits, int h,
                                  int c, Fetch fetch) {
-  // Tokens are fetched eight at a time so their loads are in flight together.
+  // The group's tokens are held in registers 32 at a time: all their loads
+  // (and the page header's) are in flight together, and a group of up to 32
+  // tokens is read once -- the per-step groups (K group 16 or 32) cost two
+  // or three dependent memory round trips instead of one per 8 tokens per pass.
+  constexpr int kChunk = 32;
   const Hdr hd = load_hdr(pages, L, blk);
+  float x[kChunk][4];
   float mn[4], mx[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     mn[e] = __builtin_inff();
     mx[e] = -__builtin_inff();
   }
-  for (int p0 = 0; p0 < n; p0 += 8) {
-    float x[8][4];
+  for (int p0 = 0; p0 < n; p0 += kChunk) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kChunk; ++u)
       if (p0 + u < n) fetch(p0 + u, x[u]);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kChunk; ++u) {
       if (p0 + u < n) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -128,13 +132,14 @@ __device__ void quantize_k_group(const Lay& L, uint8_t* pages, long blk, int grp
     *f16p(pages, blk * L.stride + L.o_ks + 2 * (se + e)) = s16;
     *f16p(pages, blk * L.stride + L.o_km + 2 * (se + e)) = m16;
   }
-  for (int p0 = 0; p0 < n; p0 += 8) {
-    float x[8][4];
+  for (int p0 = 0; p0 < n; p0 += kChunk) {
+    if (n > kChunk) {  // a group over 32 tokens: the registers hold its last chunk
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (p0 + u < n) fetch(p0 + u, x[u]);
+      for (int u = 0; u < kChunk; ++u)
+        if (p0 + u < n) fetch(p0 + u, x[u]);
+    }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kChunk; ++u) {
       if (p0 + u >= n) continue;
       const long rb = row_base_h(L, blk, hd, off0 + p0 + u, bits);
       if (rb < 0) continue;
@@ -150,6 +155,84 @@ __device__ void quantize_k_group(const Lay& L, uint8_t* pages, long blk, int grp
 // finalize_k (echokv_vllm/kernels/write.py:205-230, 340-396)
 // ---------------------------------------------------------------------------
 
+// The common case -- key and residual of one dtype, a group of at most 32
+// tokens -- as straight-line code: every token's 4 values are loaded without
+// a branch (the source is a select between this step's key row and the
+// residual row; tokens past the group repeat its last one, which leaves the
+// min / max unchanged), all loads in flight together; the block's chunk bases
+// are computed once and rows are walked without divisions.
+template <typename T>
+__device__ __forceinline__ void finalize_group(const FinArgs a, const int64_t* row, long blk, int grp, long rs, int h,
+                                               int c) {
+  constexpr int kMax = 32;
+  const Lay& L = a.L;
+  const int n = L.KG;
+  const Hdr hd = load_hdr(a.pages, L, blk);
+  const T* key = (const T*)a.key;
+  const T* res = (const T*)a.res.ptr;
+  float x[kMax][4];
+#pragma unroll
+  for (int u = 0; u < kMax; ++u) {
+    const int p = u < n ? u : n - 1;
+    const long r = row[3 + p];
+    const T* src = r >= 0 ? key + r * a.k_s0 + h * a.k_s1 + 4 * c
+                          : res + rs * a.res.s0 + (long)p * a.res.s1 + h * a.res.s2 + 4 * c;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[u][e] = (float)src[e];
+  }
+  float mn[4], mx[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    mn[e] = x[0][e];
+    mx[e] = x[0][e];
+#pragma unroll
+    for (int u = 1; u < kMax; ++u) {
+      mn[e] = fminf(mn[e], x[u][e]);
+      mx[e] = fmaxf(mx[e], x[u][e]);
+    }
+  }
+  const int bits = tier_of(hd.tag);
+  float s[4], m[4];
+  const long se = ((long)grp * L.H + h) * L.D + 4 * c;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    _Float16 s16, m16;
+    group_stats(mn[e], mx[e], bits, s16, m16, s[e], m[e]);
+    *f16p(a.pages, blk * L.stride + L.o_ks + 2 * (se + e)) = s16;
+    *f16p(a.pages, blk * L.stride + L.o_km + 2 * (se + e)) = m16;
+  }
+  // Chunk j of the block: its own page's data for j = 0, pool chunk id[j - 1]
+  // otherwise (-1: out of range, nothing stored there).
+  long cb[4];
+  cb[0] = blk * L.stride + L.o_data;
+#pragma unroll
+  for (int j = 1; j < 4; ++j) {
+    const int id = hd.id[j - 1];
+    const uint32_t page = (uint32_t)id / (uint32_t)L.KC, slot = (uint32_t)id % (uint32_t)L.KC;
+    cb[j] = (id < 0 || (long)page >= L.nb) ? -1L : (long)page * L.stride + L.o_data + (long)slot * L.cb;
+  }
+  const int tpc = 2 * L.BS / bits;  // tokens per chunk
+  const long rowb = 2L * L.H * L.D * bits / 8;
+  const long within = (long)h * (L.D * bits / 8) + c * (bits / 2);
+  int j = (grp * L.KG) / tpc, w = (grp * L.KG) % tpc;
+#pragma unroll
+  for (int u = 0; u < kMax; ++u) {
+    if (u < n) {
+      const long base = j == 0 ? cb[0] : (j == 1 ? cb[1] : (j == 2 ? cb[2] : cb[3]));
+      if (base >= 0) {
+        uint32_t q[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = quant_code(x[u][e], m[e], s[e], bits);
+        store_codes4(a.pages + base + w * rowb + within, pack4(q, bits), bits);
+      }
+      if (++w == tpc) {
+        w = 0;
+        ++j;
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void finalize_k_kernel(FinArgs a) {
   const Lay& L = a.L;
   const long f = blockIdx.x;
@@ -159,16 +242,23 @@ __global__ __launch_bounds__(kThreads) void finalize_k_kernel(FinArgs a) {
   const int grp = (int)row[1];
   const long rs = row[2] < 0 ? 0 : row[2];
   if (blk < 0 || blk >= L.nb || grp < 0 || grp >= L.BS / L.KG || rs >= a.res.rows) return;
-  const int bits = tier_of(a.pages[blk * L.stride]);
   const int quads = L.D / 4;
+  const bool same = a.kv_dtype == a.res.dtype && L.KG <= 32;
   for (int i = threadIdx.x; i < L.H * quads; i += kThreads) {
     const int h = i / quads, c = i % quads;
-    auto fetch = [&](int p, float x[4]) {
-      const long r = row[3 + p];
-      if (r >= 0) ld4(a.key, a.kv_dtype, r * a.k_s0 + h * a.k_s1 + 4 * c, x);
-      else ld4(a.res.ptr, a.res.dtype, rs * a.res.s0 + (long)p * a.res.s1 + h * a.res.s2 + 4 * c, x);
-    };
-    quantize_k_group(L, a.pages, blk, grp, grp * L.KG, L.KG, bits, h, c, fetch);
+    if (same && a.kv_dtype == ECHOKV_F16) {
+      finalize_group<_Float16>(a, row, blk, grp, rs, h, c);
+    } else if (same && a.kv_dtype == ECHOKV_F32) {
+      finalize_group<float>(a, row, blk, grp, rs, h, c);
+    } else {
+      const int bits = tier_of(a.pages[blk * L.stride]);
+      auto fetch = [&](int p, float x[4]) {
+        const long r = row[3 + p];
+        if (r >= 0) ld4(a.key, a.kv_dtype, r * a.k_s0 + h * a.k_s1 + 4 * c, x);
+        else ld4(a.res.ptr, a.res.dtype, rs * a.res.s0 + (long)p * a.res.s1 + h * a.res.s2 + 4 * c, x);
+      };
+      quantize_k_group(L, a.pages, blk, grp, grp * L.KG, L.KG, bits, h, c, fetch);
+    }
   }
 }
 
