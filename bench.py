@@ -48,7 +48,7 @@ PF_SEQS, PF_CTX, PF_CHUNK = 16, 4096, 512  # config 3
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16
 
 
-def alg_bytes(lens: np.ndarray, bits: int, res_bytes: int = 2) -> int:
+def alg_bytes(lens: np.ndarray, bits: int, res_bytes: int = 2, hq: int = HQ) -> int:
     """Decode bytes of one layer-step: what the attention math must read / write."""
     g = D // VG
     sealed_grp = lens // KG
@@ -57,7 +57,7 @@ def alg_bytes(lens: np.ndarray, bits: int, res_bytes: int = 2) -> int:
     per_sealed = 2 * H * D * bits // 8 + H * g * 4
     per_open = H * D * bits // 8 + H * g * 4 + H * D * res_bytes
     kv = sealed_tok * per_sealed + sealed_grp * H * D * 4 + open_tok * per_open
-    return int(kv.sum()) + 2 * S * HQ * D * 2
+    return int(kv.sum()) + 2 * len(lens) * hq * D * 2
 
 
 def build_state(dev, steps_total: int, seed: int = 1):
@@ -331,6 +331,136 @@ def measured_traffic() -> int | None:
     return None
 
 
+C4_LAYERS, C4_S, C4_CTX, C4_HQ = 80, 16, 32768, 64  # config 4
+
+
+def run_cfg4(reps: int = 5) -> dict:
+    """Config 4: Llama-3.1-70B-shaped long-context decode on one GPU, no tensor
+    parallelism -- 80 layers (seeded permutation of 20 INT8 / 40 INT4 / 20 INT2),
+    Hq 64 / H 8 / D 128 (GQA 8), page block 16, K group 16, V group 32, mem_bits 8
+    pages (about 102 GB), 16 sequences of 32768 tokens. Every layer's context is
+    written through the quantize-on-write path (one synthetic K/V set, fp16
+    ~N(0,1), 1% of K channels x10, reused by every layer), then each tier's layers'
+    decode (decode + merge) is captured as one HIP graph and replayed ``reps`` times
+    between HIP events; the canary fires once over the 80 layers (8 query rows,
+    the 64-key K_ref window, tiers 2 / 4 / 8), as on every 64th step."""
+    import torch
+
+    from echokv_amd.canary import canary_kl
+    from echokv_amd.kernels.decode import decode_attention
+    from echokv_amd.tiered_cache import TieredKVCache, TieredLayout
+    from echokv_amd.write_plan import SharedState, stage_plan
+
+    dev = torch.device("cuda:0")
+    t_setup = time.time()
+    rng = np.random.default_rng(3)
+    tiers = rng.permutation(np.array([8] * 20 + [4] * 40 + [2] * 20))
+    layout = TieredLayout(H, D, BS, MEM, KG, VG)
+    page = BS * TieredLayout.per_token_bytes(H, D, MEM, KG, VG)
+    ctx = np.full(C4_S, C4_CTX, np.int64)
+    nbs = -(-ctx // BS)
+    nb = int(nbs.sum()) + 16
+    perm = rng.permutation(nb)
+    table = np.zeros((C4_S, int(nbs.max())), np.int64)
+    o = 0
+    for i, n in enumerate(nbs):
+        table[i, :n] = perm[o : o + n]
+        o += n
+    shared = SharedState(nb, BS, KG, C4_S + 16, kref_window=64, device=dev)
+    pre = np.concatenate([table[i][np.arange(n) // BS] * BS + np.arange(n) % BS for i, n in enumerate(ctx)])
+    plan = shared.planner.plan(pre)
+    print(f"[bench cfg4] planned {pre.size} slots, {time.time() - t_setup:.1f}s", file=sys.stderr, flush=True)
+    stores, krefs = [], []
+    for _ in range(C4_LAYERS):
+        pages = torch.empty(nb, page, dtype=torch.uint8, device=dev)
+        res = torch.zeros(C4_S + 17, KG, H, D, dtype=torch.float16, device=dev)
+        stores.append(TieredKVCache(layout, pages, residual=res, shared=shared))
+        krefs.append(torch.zeros(64, H, D, device=dev))
+    opened = [st.prepare(plan, int(t)) for st, t in zip(stores, tiers)]
+    shared.commit(plan)
+    meta, extra = stage_plan(plan, dev, None)
+    shared.apply_res_map(*extra[:4])
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    k = torch.randn(pre.size, H, D, device=dev, dtype=torch.float16, generator=gen)
+    v = torch.randn(pre.size, H, D, device=dev, dtype=torch.float16, generator=gen)
+    out_ch = torch.randperm(H * D, generator=gen, device=dev)[: round(0.01 * H * D)]
+    k.view(pre.size, H * D)[:, out_ch] *= 10
+    for li, (st, op, kr) in enumerate(zip(stores, opened, krefs)):
+        if op is not None:
+            st.write_headers(torch.from_numpy(op[0]).to(dev), torch.from_numpy(op[1]).to(dev))
+        st.apply(meta, k, v, kr)
+        if li % 20 == 19:
+            torch.cuda.synchronize()
+            print(f"[bench cfg4] {li + 1} layers written, {time.time() - t_setup:.1f}s", file=sys.stderr, flush=True)
+    del k, v
+    torch.cuda.synchronize()
+    setup_s = time.time() - t_setup
+    print(f"[bench cfg4] state ready: {nb} blocks/layer, {nb * page * C4_LAYERS / 2**30:.1f} GiB pages, "
+          f"{setup_s:.1f}s", file=sys.stderr, flush=True)
+
+    table_d = torch.from_numpy(table).to(dev, torch.int32)
+    lens_d = torch.from_numpy(ctx).to(dev)
+    q = [torch.randn(C4_S, C4_HQ, D, device=dev, dtype=torch.float16, generator=gen) for _ in range(C4_LAYERS)]
+    out = [torch.empty(C4_S, C4_HQ, D, device=dev, dtype=torch.float16) for _ in range(C4_LAYERS)]
+    num_splits = max(1, min(-(-table.shape[1] // 16), 64))
+    ws = (torch.empty(C4_S, C4_HQ, num_splits, D, device=dev), torch.empty(C4_S, C4_HQ, num_splits, 2, device=dev))
+    scale = D ** -0.5
+    per_tier = {}
+    total_us = 0.0
+    for bits in (8, 4, 2):
+        layers = [li for li in range(C4_LAYERS) if tiers[li] == bits]
+
+        def run_tier():
+            for li in layers:
+                decode_attention(stores[li], q[li], table_d, lens_d, scale, blocks_per_split=16, out=out[li],
+                                 num_splits=num_splits, workspace=ws, tier=bits)
+
+        run_tier()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run_tier()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
+        b = alg_bytes(ctx, bits, hq=C4_HQ)
+        per_tier[f"int{bits}"] = {"layers": len(layers), "us_per_layer": round(us, 1), "alg_bytes_per_layer": b,
+                                  "GBs": round(b / us / 1e3, 1), "frac_of_8TBs": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        total_us += us * len(layers)
+    # Canary: one fire over the 80 layers (the backend's every-64th-step probe).
+    cq = torch.randn(C4_LAYERS, 8, C4_HQ, D, device=dev, dtype=torch.float16, generator=gen)
+    kref = torch.randn(C4_LAYERS, 64, H, D, device=dev, generator=gen)
+    canary_kl(cq, kref, (2, 4, 8), KG, scale)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        canary_kl(cq, kref, (2, 4, 8), KG, scale)
+    e1.record()
+    torch.cuda.synchronize()
+    canary_us = e0.elapsed_time(e1) * 1e3 / reps
+    step_bytes = sum(alg_bytes(ctx, int(t), hq=C4_HQ) for t in tiers)
+    return {
+        "workload": "cfg4: Llama-3.1-70B-shaped decode, 80 layers (20 INT8 / 40 INT4 / 20 INT2), batch 16 x 32768 "
+                    "tokens, Hq 64 / H 8 / D 128, page block 16, K group 16, V group 32, mem_bits 8 pages",
+        "pages_GiB": round(nb * page * C4_LAYERS / 2**30, 1),
+        "decode_ms_per_step": round(total_us / 1e3, 3),
+        "decode_alg_GB_per_step": round(step_bytes / 1e9, 2),
+        "decode_GBs_per_step": round(step_bytes / total_us / 1e3, 1),
+        "per_tier": per_tier,
+        "canary_us_per_fire_80_layers": round(canary_us, 1),
+        "setup_s": round(setup_s, 1),
+        "data": "synthetic: fp16 K/V ~N(0,1), 1% K channels x10 (one set for all layers), random block tables",
+    }
+
+
 def cpu_baseline(store, q, table, lens) -> dict:
     """The numpy oracle's decode (vectorized gather + float64 SDPA) on the host: one INT4
     layer-step over a bounded sample of the batch's sequences."""
@@ -372,6 +502,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill measurement")
     ap.add_argument("--prefill-only", action="store_true", help="only the config-3 prefill measurement")
+    ap.add_argument("--config4", action="store_true",
+                    help="only config 4 (70B shape, 80 layers, about 102 GB of pages): decode per tier and the canary")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 1 GiB device-to-device 5 times (the reference kernel for FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -383,6 +515,9 @@ def main():
         return
     if args.prefill_only:
         print(json.dumps({"prefill": run_prefill()}), flush=True)
+        return
+    if args.config4:
+        print(json.dumps({"cfg4": run_cfg4()}), flush=True)
         return
     print(json.dumps(run(args)), flush=True)
 
