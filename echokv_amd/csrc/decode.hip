@@ -91,9 +91,9 @@ __device__ __forceinline__ h2_t code_pair(uint32_t x, const CodeK& k) {
 }
 
 // Eight consecutive channels of a K row, natural order, as an MFMA fragment.
-// INT4: one word (8 nibbles), the codes themselves (cvt_codes); INT8: two
-// words, INT2: bytes 2*hf, 2*hf+1 of one word, as 1024 + code (s_block takes
-// the bias back out with one more contraction).
+// INT4: one word (8 nibbles); INT2: bytes 2*hf, 2*hf+1 of one word -- both as
+// the codes themselves (cvt_codes); INT8: two words, as 1024 + code (s_block
+// takes the bias back out with one more contraction).
 template <int BITS>
 __device__ __forceinline__ h8_t kfrag(const uint32_t* w, int hf, const CodeK& k) {
   if constexpr (BITS == 4) {
@@ -107,10 +107,17 @@ __device__ __forceinline__ h8_t kfrag(const uint32_t* w, int hf, const CodeK& k)
     return w2h8(perm(m, w[0], 0x04010400u), perm(m, w[0], 0x04030402u), perm(m, w[1], 0x04010400u),
                 perm(m, w[1], 0x04030402u));
   } else {
-    const uint32_t x = w[0], x2 = x >> 2, x4 = x >> 4, x6 = x >> 6;
-    const int b0 = 2 * hf, b1 = 2 * hf + 1;
-    return w2h8(biased_pair(perm(x2, x, pair_sel(b0, b0)), k), biased_pair(perm(x6, x4, pair_sel(b0, b0)), k),
-                biased_pair(perm(x2, x, pair_sel(b1, b1)), k), biased_pair(perm(x6, x4, pair_sel(b1, b1)), k));
+    // y_k: code k of every byte (byte b holds channels 4b .. 4b+3); a v_perm
+    // puts channels (k, k+1) of byte 2hf next to each other, (4+k, 5+k) of
+    // byte 2hf+1 above them.
+    const uint32_t x = w[0];
+    const uint32_t y0 = x & 0x03030303u, y1 = (x >> 2) & 0x03030303u;
+    const uint32_t y2 = (x >> 4) & 0x03030303u, y3 = (x >> 6) & 0x03030303u;
+    const uint32_t b0 = 2 * hf, b1 = 2 * hf + 1;
+    const uint32_t sel = b0 | ((4 + b0) << 8) | (b1 << 16) | ((4 + b1) << 24);
+    const uint32_t p01 = perm(y1, y0, sel), p23 = perm(y3, y2, sel);
+    (void)k;
+    return w2h8(cvt_codes<false>(p01), cvt_codes<false>(p23), cvt_codes<true>(p01), cvt_codes<true>(p23));
   }
 }
 
@@ -169,6 +176,28 @@ __device__ __forceinline__ void vfrags4(const uint32_t (*v)[1], h2_t s01, h2_t s
     va[4 * hb + 1] = frag(cvt_codes<false>(o01), cvt_codes<false>(o23));
     va[4 * hb + 2] = frag(cvt_codes<true>(e01), cvt_codes<true>(e23));
     va[4 * hb + 3] = frag(cvt_codes<true>(o01), cvt_codes<true>(o23));
+  }
+}
+
+// INT2 V^T operands of the lane's CPM (4 or 8) channels: a v_perm interleaves
+// the code bytes of tokens (0, 1) / (2, 3) (byte b holds channels 4b .. 4b+3),
+// so each shift-and-mask leaves channel k of both tokens in bytes 0-1 and
+// channel 4+k in bytes 2-3, as cvt_codes takes them.
+template <int CPM>
+__device__ __forceinline__ void vfrags2(const uint32_t (*v)[1], h2_t s01, h2_t s23, h2_t m01, h2_t m23, h4_t* va) {
+  static_assert(CPM == 4 || CPM == 8, "INT2 V: the lane's channels of a token fit one word");
+  const uint32_t sel = 0x05010400u;  // t0.b0, t1.b0, t0.b1, t1.b1
+  const uint32_t x01 = perm(v[1][0], v[0][0], sel), x23 = perm(v[3][0], v[2][0], sel);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t c01 = (x01 >> (2 * k)) & 0x03030303u, c23 = (x23 >> (2 * k)) & 0x03030303u;
+    auto frag = [&](uint32_t a01, uint32_t a23) {
+      const h2_t a0 = __builtin_elementwise_fma(u2h(a01), s01, m01);
+      const h2_t a1 = __builtin_elementwise_fma(u2h(a23), s23, m23);
+      return h4_t{a0[0], a0[1], a1[0], a1[1]};
+    };
+    va[k] = frag(cvt_codes<false>(c01), cvt_codes<false>(c23));
+    if constexpr (CPM == 8) va[4 + k] = frag(cvt_codes<true>(c01), cvt_codes<true>(c23));
   }
 }
 
@@ -254,7 +283,7 @@ struct Wave {
 
 // S^T of one 16-token tile from its codes, K group by 32-channel block j:
 //   S^T += codes_j . (q * k_scale)_j^T   as fp16 hi / lo pairs (two chains)
-//        - 1024 * sum_d (q * k_scale)_j  (INT8 / INT2 fragments carry 1024 + c)
+//        - 1024 * sum_d (q * k_scale)_j  (INT8 fragments carry 1024 + c)
 //        + k_min_j . q_j^T               (and q lo for float32 queries)
 // The products q * s are exact in fp32; hi = fp16(q * s), lo = fp16(fma(q, s,
 // -hi)) keeps S accurate to ~2^-22 relative. Each block's operands are built
@@ -279,7 +308,7 @@ __device__ __forceinline__ void s_block(const Wave<D, QLO>& w, const uint32_t* k
   const h8_t mn = w2h8(km[0], km[1], km[2], km[3]);
   sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, h8, sh, 0, 0, 0);
   sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, l8, sl, 0, 0, 0);
-  if constexpr (BITS != 4) {  // INT4 fragments carry the codes themselves
+  if constexpr (BITS == 8) {  // INT4 / INT2 fragments carry the codes themselves
     sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, h8, sh, 0, 0, 0);
     sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, l8, sl, 0, 0, 0);
   } else {
@@ -782,6 +811,9 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
   if constexpr (BITS == 4) {
     (void)vsh;
     vfrags4<CPM>(vw, s01, s23, m01, m23, va);
+  } else if constexpr (BITS == 2) {
+    (void)vsh;
+    vfrags2<CPM>(vw, s01, s23, m01, m23, va);
   } else {
     vshift<BITS, VW>(vw, vsh);
     const CodeK vk = code_consts<BITS>();
