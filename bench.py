@@ -16,7 +16,9 @@ own pages, at the lengths the timed steps reached) captured as one HIP graph
 and replayed ``--reps`` times between HIP events on the launch stream, so the
 time is GPU work only; ``roofline`` puts it against 8 TB/s. ``ms_per_step`` and
 ``e2e_decode_tok_s`` time the whole 32-layer step (host planning included) over
-the ``--steps`` timed steps.
+the ``--steps`` timed steps, each replayed as one HIP graph (the plan staged into
+fixed device buffers); ``e2e_eager_*`` times the same steps launched one kernel at
+a time.
 
 ``prefill`` (one layer): 16 sequences x 4096 tokens written
 and attended in 512-token chunks over an INT4 cache, bf16 activations; per
@@ -111,12 +113,13 @@ def build_state(dev, steps_total: int, seed: int = 1):
 def run(args) -> dict:
     import torch
 
+    from echokv_amd._util import to_device
     from echokv_amd.kernels.decode import decode_attention
     from echokv_amd.write_plan import stage_plan
 
     dev = torch.device("cuda:0")
     t_setup = time.time()
-    st = build_state(dev, args.warmup + args.steps)
+    st = build_state(dev, args.warmup + 2 * args.steps + 2)
     ctx, tiers, table = st["ctx"], st["tiers"], st["table"]
     shared, stores, krefs = st["shared"], st["stores"], st["krefs"]
     print(f"[bench] state ready: {st['nb']} blocks/layer, {st['nb'] * st['page'] * LAYERS / 2**30:.1f} GiB pages, "
@@ -143,22 +146,74 @@ def run(args) -> dict:
         lens = pos + 1
         meta, extra = stage_plan(plan, dev, None)
         shared.apply_res_map(*extra[:4])
-        lens_d = torch.from_numpy(lens).to(dev)
+        lens_d = to_device(torch.from_numpy(lens), dev)  # pinned, non-blocking: the host keeps planning
         for li, s in enumerate(stores):
             if opened[li] is not None:
-                s.write_headers(torch.from_numpy(opened[li][0]).to(dev), torch.from_numpy(opened[li][1]).to(dev))
+                s.write_headers(to_device(torch.from_numpy(opened[li][0]), dev), to_device(torch.from_numpy(opened[li][1]), dev))
             s.apply(meta, kn[li], vn[li], krefs[li])
             decode_attention(s, q[li], table_d, lens_d, scale, blocks_per_split=args.bps, out=out[li],
                              num_splits=num_splits, workspace=ws, tier=int(tiers[li]))
         return lens
 
-    # End to end: the host plans every step; all 32 layers write and attend.
+    # End to end, eager: the host plans every step; all 32 layers write and attend.
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.warmup, args.warmup + args.steps):
         lens = step(i)
+    torch.cuda.synchronize()
+    wall_eager = time.perf_counter() - t0
+
+    # End to end, graph-replayed (as a serving engine runs decode): the host plans
+    # each step and copies the plan into fixed device buffers (rows = the batch,
+    # finalize over a full grid masked by the device count); one HIP graph then
+    # runs every layer's finalize, write, decode and merge.
+    from echokv_amd.write_plan import WriteMeta
+    tok_buf = torch.full((4, S), -1, dtype=torch.int64, device=dev)
+    fin_buf = torch.zeros(S, 3 + KG, dtype=torch.int64, device=dev)
+    cnt_buf = torch.zeros(1, dtype=torch.int64, device=dev)
+    lens_buf = torch.zeros(S, dtype=torch.int64, device=dev)
+    gmeta = WriteMeta(tok=tok_buf, fin=fin_buf, fin_count=cnt_buf, n_rows=S, n_fin=S)
+
+    def all_layers():
+        for li, s in enumerate(stores):
+            s.apply(gmeta, kn[li], vn[li], krefs[li], capturing=True)
+            decode_attention(s, q[li], table_d, lens_buf, scale, blocks_per_split=args.bps, out=out[li],
+                             num_splits=num_splits, workspace=ws, tier=int(tiers[li]))
+
+    all_layers()  # warm-up with nothing staged: no row written, every length 0
+    torch.cuda.synchronize()
+    step_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(step_graph):
+        all_layers()
+
+    def gstep(i):
+        pos = ctx - 1 + i
+        slots = table[np.arange(S), pos // BS] * BS + pos % BS
+        plan = shared.planner.plan(slots)
+        opened = [s.prepare(plan, int(t)) for s, t in zip(stores, tiers)]
+        shared.commit(plan)
+        meta, extra = stage_plan(plan, dev, None)
+        shared.apply_res_map(*extra[:4])
+        for li, s in enumerate(stores):
+            if opened[li] is not None:
+                s.write_headers(to_device(torch.from_numpy(opened[li][0]), dev), to_device(torch.from_numpy(opened[li][1]), dev))
+        tok_buf.copy_(meta.tok)
+        if meta.n_fin:
+            fin_buf[: meta.n_fin].copy_(meta.fin)
+        cnt_buf.copy_(meta.fin_count)
+        lens_buf.copy_(to_device(torch.from_numpy(pos + 1), dev))
+        step_graph.replay()
+        return pos + 1
+
+    g0 = args.warmup + args.steps
+    for i in range(g0, g0 + 2):
+        gstep(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(g0 + 2, g0 + 2 + args.steps):
+        lens = gstep(i)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
@@ -213,6 +268,8 @@ def run(args) -> dict:
             "parallelism": "single GPU",
         },
         "e2e_decode_tok_s": round(S * args.steps / wall, 1),
+        "e2e_eager_ms_per_step": round(wall_eager * 1e3 / args.steps, 3),
+        "e2e_eager_tok_s": round(S * args.steps / wall_eager, 1),
         "int4_decode_us_per_layer": round(avg_ms * 1e3, 2),
         "roofline": {
             "bound": "hbm",

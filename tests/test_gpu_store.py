@@ -95,6 +95,58 @@ def test_padded_full_grid_step_matches_plain_write(device):
     np.testing.assert_array_equal(kr.cpu().numpy(), golden("step_path")["kref"])
 
 
+def test_graph_replayed_step_matches_plain_write(device):
+    """The write step captured once as a HIP graph over fixed buffers (rows padded
+    to a fixed count, plan staged into the buffers before each replay, full-grid
+    finalize masked by the device count) stores the plain writes' bytes."""
+    from echokv_amd.write_plan import WriteMeta, stage_plan
+
+    s = _script("step_path")
+    plain, *_ = gpu_replay(s, device)
+    st, *_ = gpu_store(s, device)
+    steps = list(S.script_inputs(s))
+    rows = max(sl.size for sl, *_ in steps) + 3
+    tok = torch.full((4, rows), -1, dtype=torch.int64, device=device)
+    fin = torch.zeros(rows, 3 + s.kg, dtype=torch.int64, device=device)
+    cnt = torch.zeros(1, dtype=torch.int64, device=device)
+    kb = torch.zeros(rows, s.h, s.d, device=device)
+    vb = torch.zeros(rows, s.h, s.d, device=device)
+    kr = torch.zeros(s.kref_window, s.h, s.d, device=device)
+    gmeta = WriteMeta(tok=tok, fin=fin, fin_count=cnt, n_rows=rows, n_fin=rows)
+    st.apply(gmeta, kb, vb, kref=kr, capturing=True)  # warm-up: every row is padding, no group completes
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st.apply(gmeta, kb, vb, kref=kr, capturing=True)
+    gen = torch.Generator().manual_seed(1)
+    for i, (slots, bits, k, v) in enumerate(steps):
+        print(f"[store] graph replay step {i}", flush=True)
+        n = slots.size
+        padded = torch.cat([torch.from_numpy(slots), torch.full((rows - n,), -1, dtype=torch.int64)])
+        plan = st.planner.plan(padded)
+        opened = st.prepare(plan, bits)
+        st.shared.commit(plan)
+        meta, extra = stage_plan(plan, device, opened)
+        st.shared.apply_res_map(*extra[:4])
+        if opened is not None:
+            st.write_headers(extra[4], extra[5])
+        tok.copy_(meta.tok)
+        if meta.n_fin:
+            fin[: meta.n_fin].copy_(meta.fin)
+        cnt.copy_(meta.fin_count)
+        kb[:n].copy_(torch.from_numpy(k))
+        vb[:n].copy_(torch.from_numpy(v))
+        kb[n:].copy_(torch.randn(rows - n, s.h, s.d, generator=gen) * 1e3)
+        vb[n:].copy_(torch.randn(rows - n, s.h, s.d, generator=gen) * 1e3)
+        graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(plain.pages, st.pages)
+    assert torch.equal(plain.block_res, st.block_res)
+    live = plain.block_res[plain.block_res >= 0]
+    assert live.numel() and torch.equal(plain.res_k[live], st.res_k[live])
+    np.testing.assert_array_equal(kr.cpu().numpy(), golden("step_path")["kref"])
+
+
 def test_decode_cases_store_oracle_bytes(device):
     """The decode-case stores (bf16-free, mixed tiers, pool pressure) written on the
     GPU equal the CPU oracle replay byte for byte."""
