@@ -24,9 +24,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 __global__ __launch_bounds__(256) void canary_kernel(CanaryArgs a) {
-  __shared__ float kv[1 + kCanaryMaxTiers][kCanaryMaxKeys][kCanaryMaxD];
-  __shared__ float qrow[kCanaryMaxD];
-  __shared__ float lref[kCanaryMaxKeys];
+  // Key rows padded by one float: lane j reads row j, and unpadded rows of
+  // kCanaryMaxD floats would put every lane's read in the same LDS bank.
+  __shared__ float kv[1 + kCanaryMaxTiers][kCanaryMaxKeys][kCanaryMaxD + 1];
+  __shared__ float lref[2][kCanaryMaxKeys];  // double-buffered by query row: one barrier per row
   const int layer = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int w = (a.window / a.kg) * a.kg;
@@ -60,16 +61,24 @@ __global__ __launch_bounds__(256) void canary_kernel(CanaryArgs a) {
         kv[1 + t][gi * a.kg + p][dd] = (float)quant_code(x, m, s, bits) * s + m;
       }
     }
+    __syncthreads();  // the round trips are staged
+    int buf = 0;
     for (int qh = h * rep; qh < (h + 1) * rep; ++qh) {
-      for (int r = 0; r < a.nq; ++r) {
-        __syncthreads();
-        for (int dd = tid; dd < a.d; dd += 256)
-          qrow[dd] = ld(a.q, a.q_dtype, layer * a.q_sl + (long)r * a.q_s0 + (long)qh * a.q_s1 + dd);
-        __syncthreads();
+      for (int r = 0; r < a.nq; ++r, buf ^= 1) {
+        // The query row is the same for every lane: read 16 channels at a time
+        // with wave-uniform (scalar) loads, no LDS staging or barrier.
+        const long qb = layer * a.q_sl + (long)r * a.q_s0 + (long)qh * a.q_s1;
         float logit = -__builtin_inff();
         if (wave <= a.nbits && lane < w) {
           float acc = 0.f;
-          for (int dd = 0; dd < a.d; ++dd) acc += qrow[dd] * kv[wave][lane][dd];
+          int d0 = 0;
+          for (; d0 + 16 <= a.d; d0 += 16) {
+            float qv[16];
+            ld_n<16>(a.q, a.q_dtype, qb + d0, qv);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc += qv[e] * kv[wave][lane][d0 + e];
+          }
+          for (; d0 < a.d; ++d0) acc += ld(a.q, a.q_dtype, qb + d0) * kv[wave][lane][d0];  // head size not a multiple of 16
           logit = acc * a.scale;
         }
         float lsm = 0.f;
@@ -78,11 +87,11 @@ __global__ __launch_bounds__(256) void canary_kernel(CanaryArgs a) {
           const float e = lane < w ? expf(logit - mx) : 0.f;
           const float lse = mx + logf(wave_sum(e));
           lsm = logit - lse;
-          if (wave == 0 && lane < w) lref[lane] = lsm;
+          if (wave == 0 && lane < w) lref[buf][lane] = lsm;
         }
         __syncthreads();
         if (wave >= 1 && wave <= a.nbits) {
-          const float term = lane < w ? expf(lsm) * (lsm - lref[lane]) : 0.f;
+          const float term = lane < w ? expf(lsm) * (lsm - lref[buf][lane]) : 0.f;
           const float s = wave_sum(term);
           kl += s;
         }

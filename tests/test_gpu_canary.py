@@ -38,3 +38,14 @@ def test_canary_batched_equals_per_layer_and_monotone(device):
     assert (d[:, 0] > d[:, 1]).all() and (d[:, 1] > d[:, 2]).all() and (d >= 0).all()
     low = canary_kl(qd.bfloat16(), kd, (2, 4, 8), 32, 64 ** -0.5)
     assert low.dtype == torch.float32 and low.shape == (3, 3)
+
+
+@pytest.mark.parametrize("d", [72, 40])
+def test_canary_head_size_not_multiple_of_16(device, d):
+    """Query rows are read 16 channels at a time; the remaining channels of a
+    head size that is not a multiple of 16 take the per-element tail."""
+    rng = np.random.default_rng(d)
+    q = rng.standard_normal((2, 4, 8, d)).astype(np.float32)     # [layers, nq, Hq, D]
+    kref = rng.standard_normal((2, 48, 2, d)).astype(np.float32)  # [layers, W, H, D]
+    got = canary_kl(torch.from_numpy(q).to(device), torch.from_numpy(kref).to(device), (2, 4, 8), 16, d ** -0.5)
+    _close(got, OC.canary_kl(q, kref, (2, 4, 8), 16, d ** -0.5))
