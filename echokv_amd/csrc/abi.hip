@@ -122,15 +122,23 @@ int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* b
   return launched(ek::launch_store_blocks(a, n, (hipStream_t)stream));
 }
 
-int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,
-                  const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
-                  int32_t num_q_heads, const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
-                  const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs, float softmax_scale,
-                  int32_t num_splits, int32_t blocks_per_split, int32_t tier, float* acc, float* ml, void* out,
-                  int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// echokv_decode and echokv_decode_static: the checks, then decode + merge with
+// the given workspaces, or (static_scratch) with the library's static scratch.
+int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,
+               const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
+               int32_t num_q_heads, const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
+               const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs, float softmax_scale,
+               int32_t num_splits, int32_t blocks_per_split, int32_t tier, float* acc, float* ml, bool static_scratch,
+               void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;
   if (L->head_size != 64 && L->head_size != 128) return ECHOKV_ESHAPE;
-  if ((L->head_size / 16) % 1 || L->v_group % (L->head_size / 16)) return ECHOKV_ESHAPE;
+  if (L->v_group % (L->head_size / 16)) return ECHOKV_ESHAPE;
+  // A 16-token tile must lie in one K group (one k_scale / k_min row per tile).
+  if (L->k_group < 16) return ECHOKV_ESHAPE;
   if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
   const int gqa = num_q_heads / L->num_kv_heads;
   if (gqa > 16) return ECHOKV_ESHAPE;
@@ -138,8 +146,8 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
   if (num_seqs < 0 || num_splits <= 0 || blocks_per_split <= 0 || !res_ok(res)) return ECHOKV_EINVAL;
   if (tier != 2 && tier != 4 && tier != 8) return ECHOKV_EINVAL;
   if (num_seqs == 0) return ECHOKV_OK;
-  if (!pages || !block_res || !res_group || !query || !block_table || !seq_lens || !acc || !ml || !out)
-    return ECHOKV_EINVAL;
+  if (!pages || !block_res || !res_group || !query || !block_table || !seq_lens || !out) return ECHOKV_EINVAL;
+  if (!static_scratch && (!acc || !ml)) return ECHOKV_EINVAL;
   ek::DecodeArgs a;
   a.L = to_lay(L);
   a.pages = pages;
@@ -170,8 +178,6 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
   // ceil(2^32 / KC) is exact for chunk ids < 2^24 (fractions of id / KC are multiples of 1 / KC >= 1/4).
   a.kc_mul = L->chunks_per_page == 1 ? 0u : (uint32_t)((0x100000000ull + L->chunks_per_page - 1) / L->chunks_per_page);
   if (L->num_blocks * L->chunks_per_page >= (1LL << 24)) return ECHOKV_ESHAPE;
-  // The kernel addresses the layer's pages with 32-bit byte offsets.
-  if (L->num_blocks * L->page_stride > 0xFFFFFFFFLL) return ECHOKV_ESHAPE;
   a.acc = acc;
   a.ml = ml;
   hipError_t e = ek::launch_decode(a, num_seqs, (hipStream_t)stream);
@@ -179,6 +185,21 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
   ek::MergeArgs m{acc, ml, seq_lens, q_rows, out, o_s0, o_s1, out_dtype, num_q_heads, L->head_size,
                   L->block_size, num_splits, blocks_per_split, num_seqs * num_q_heads};
   return launched(ek::launch_merge(m, num_seqs, (hipStream_t)stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,
+                  const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
+                  int32_t num_q_heads, const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
+                  const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs, float softmax_scale,
+                  int32_t num_splits, int32_t blocks_per_split, int32_t tier, float* acc, float* ml, void* out,
+                  int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
+  return decode_run(L, pages, block_res, res_group, res, query, q_s0, q_s1, q_dtype, num_q_heads, q_rows,
+                    block_table, bt_s0, bt_rows, seq_lens, num_seqs, softmax_scale, num_splits, blocks_per_split,
+                    tier, acc, ml, false, out, o_s0, o_s1, out_dtype, stream);
 }
 
 int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,

@@ -1,6 +1,8 @@
 // Kernel argument structs (passed by value) and launchers of libechokv.
 #pragma once
 
+#include <atomic>
+
 #include "common.h"
 
 namespace ek {
@@ -181,6 +183,20 @@ struct FlashArgs {
   long n_packs;  // workspace tiles present: reads stay below this
   float scale_log2;
 };
+
+// Raise `kernel`'s dynamic-LDS limit to `bytes` on the current device, once per
+// device. The flag only skips a repeated call: hipFuncSetAttribute is idempotent,
+// so two threads that race on a fresh device both make it and both succeed.
+template <int kMaxDevices = 64>
+inline hipError_t ensure_lds_limit(const void* kernel, int bytes, std::atomic<uint64_t>* done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return hipErrorInvalidDevice;
+  const uint64_t bit = 1ull << (dev % kMaxDevices);
+  if (done->load(std::memory_order_acquire) & bit) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done->fetch_or(bit, std::memory_order_release);
+  return e;
+}
 
 hipError_t launch_write_tokens(const WriteTokArgs& a, long n_rows, hipStream_t s);
 hipError_t launch_finalize_k(const FinArgs& a, long rows, hipStream_t s);

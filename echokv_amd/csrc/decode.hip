@@ -505,9 +505,10 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
 // the cache-line requests for the same bytes.) Within a DMA job, lane L takes
 // 16-byte unit (L + row) % U of its row: the rotation spreads any one head's
 // units of the 16 rows over all LDS banks, so the per-head reads are conflict-free.
-// The DMAs are issued from inline asm with a 64-bit scalar base (the layer's
-// pages) and a 32-bit per-lane byte offset; the compiler neither sees them nor
-// inserts waits for them. A wave waits with an explicit s_waitcnt vmcnt(n) for
+// The DMAs are issued from inline asm with a 64-bit scalar base (the address
+// of the chunk or page being read: pages may span far more than 4 GiB, as in a
+// layer view of a pool interleaved across layers) and a 32-bit per-lane byte
+// offset within it; the compiler neither sees them nor inserts waits for them. A wave waits with an explicit s_waitcnt vmcnt(n) for
 // its own part of the tile about to be read (loads retire in order, so "at most
 // n outstanding" covers every older load), then the workgroup meets at a
 // barrier: after it every part has landed and every wave is done with the
@@ -564,11 +565,11 @@ __device__ __forceinline__ uint32_t unit_pos(int n, int u) {
   return (uint32_t)((n / R::RPI) * 1024 + ((n % R::RPI) * R::U + ((u - n) % R::U + R::U) % R::U) * 16);
 }
 
-// Per-block facts of the split's next <= 64 blocks, one block per lane: byte
-// offsets (from the layer's pages) of the block's page and of its chunks
+// Per-block facts of the split's next <= 64 blocks, one block per lane: 64-bit
+// byte offsets (from the layer's pages) of the block's page and of its chunks
 // (chunk 0 is in the block's own page), tier and residual mapping.
 struct BlockLane {
-  uint32_t pg, cb1, cb2, cb3;
+  uint64_t pg, cb1, cb2, cb3;
   int blk;    // -1: not a valid block id
   int tier;
   // kNotFast unless the block is stored at the kernel's tier with every chunk it
@@ -586,13 +587,13 @@ __device__ __forceinline__ BlockLane load_block(const DecodeArgs& a, long blk) {
   const Lay& L = a.L;
   BlockLane b{0, 0, 0, 0, -1, 2, kNotFast, -1, -1};
   if (blk < 0 || blk >= L.nb) return b;
-  const uint32_t pg = (uint32_t)blk * (uint32_t)L.stride;  // the pages span < 4 GiB (checked on the host)
+  const uint64_t pg = (uint64_t)blk * (uint64_t)L.stride;
   const uint4 hd = *(const uint4*)(a.pages + pg);
   b.blk = (int)blk;
   b.pg = pg;
   b.tier = tier_of(hd.x & 0xffu);
   const uint32_t ids[3] = {hd.y, hd.z, hd.w};
-  uint32_t cbs[3];
+  uint64_t cbs[3];
   bool ok = true;
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
@@ -600,7 +601,8 @@ __device__ __forceinline__ BlockLane load_block(const DecodeArgs& a, long blk) {
     const uint32_t page = a.kc_mul ? __umulhi(id, a.kc_mul) : id;
     const uint32_t slot = id - page * (uint32_t)L.KC;
     const bool in = (int)id >= 0 && (long)page < L.nb;
-    cbs[j] = in ? page * (uint32_t)L.stride + (uint32_t)L.o_data + slot * (uint32_t)L.cb : pg + (uint32_t)L.o_data;
+    cbs[j] = in ? (uint64_t)page * (uint64_t)L.stride + (uint64_t)L.o_data + (uint64_t)slot * (uint64_t)L.cb
+                : pg + (uint64_t)L.o_data;
     if (j < (BITS == 8 ? 3 : (BITS == 4 ? 1 : 0))) ok = ok && in;
   }
   b.cb1 = cbs[0];
@@ -617,9 +619,14 @@ __device__ __forceinline__ BlockLane load_block(const DecodeArgs& a, long blk) {
 
 // Per-lane constants of the pipelined path: LDS read offsets within a slot
 // for the wave's head (wv, 0..3 within the group).
+// 16-byte LDS units of one lane's K slice (D/4 channels of one token): INT8 D/64,
+// the narrower tiers fit one unit.
+template <int D, int BITS>
+constexpr int k_units() { return BITS == 8 ? D / 64 : 1; }
+
 template <int D, int BITS>
 struct LaneConst {
-  uint32_t k_rd[BITS == 8 ? 2 : 1];  // K codes of token n, channels c * D/4 .. (16-byte units; INT2: + 8 * (c & 1))
+  uint32_t k_rd[k_units<D, BITS>()];  // K codes of token n, channels c * D/4 .. (one offset per 16-byte unit)
   uint32_t v_rd[4];                  // V codes of tokens 4c + i, the lane's CPM channels
   uint32_t s_rd;                     // k_scale (k_min at + 4 * D * 2)
   uint32_t vs_rd;                    // V scale of token 4c (32-byte rows: token 4c + i at + 32 i, V min at + 512)
@@ -633,7 +640,7 @@ __device__ __forceinline__ LaneConst<D, BITS> lane_const(const DecodeArgs& a, in
   LaneConst<D, BITS> k;
   const int kbyte = wv * R::KB + c * (CPL * BITS / 8);  // within the group's segment
 #pragma unroll
-  for (int e = 0; e < (BITS == 8 ? 2 : 1); ++e) k.k_rd[e] = unit_pos<D, BITS>(n, kbyte / 16 + e) + (kbyte % 16);
+  for (int e = 0; e < k_units<D, BITS>(); ++e) k.k_rd[e] = unit_pos<D, BITS>(n, kbyte / 16 + e) + (kbyte % 16);
   const int vbyte = wv * R::KB + n * VB;
 #pragma unroll
   for (int i = 0; i < 4; ++i) k.v_rd[i] = R::OFF_V + unit_pos<D, BITS>(4 * c + i, vbyte / 16) + (vbyte % 16);
@@ -698,12 +705,13 @@ __device__ __forceinline__ JobLane<D, BITS> job_lane(const DecodeArgs& a, int wv
 
 // Wave WV's share of the DMAs of one tile (16 tokens from block offset t0)
 // into ring slot `slot`; the wave's jobs are compile-time, so the per-tile work
-// is a few scalar operations and one vector add per DMA. pg / cb: the block's
-// page and chunk byte offsets; a tile the pipelined path does not take (fast
-// false) issues only dummies.
+// is a few scalar operations per DMA (its 64-bit base) and no vector ones: the
+// per-lane offsets are the item's. pg / cb: the block's page and chunk byte
+// offsets (wave-uniform); a tile the pipelined path does not take (fast false)
+// issues only dummies.
 template <int D, int BITS, int WV>
 __device__ __forceinline__ void issue_tile_w(const DecodeArgs& a, const JobLane<D, BITS>& jl, uint32_t slot, bool fast,
-                                             int t0, int lane, uint32_t pg, uint32_t cb1, uint32_t cb2, uint32_t cb3) {
+                                             int t0, int lane, uint64_t pg, uint64_t cb1, uint64_t cb2, uint64_t cb3) {
   using R = Ring<D, BITS>;
   const Lay& L = a.L;
   constexpr int LB = BITS == 8 ? 3 : (BITS == 4 ? 2 : 1);
@@ -715,7 +723,7 @@ __device__ __forceinline__ void issue_tile_w(const DecodeArgs& a, const JobLane<
     constexpr int j0 = WV;
     const int j = j0 + 4 * m;  // compile-time after unrolling
     if (!fast || j >= R::J) {
-      if (lane == 0) dma4(a.pages, pg, slot + R::OFF_DUMMY);
+      if (lane == 0) dma4(a.pages + pg, 0u, slot + R::OFF_DUMMY);
       continue;
     }
     if (j < 2 * R::NK) {
@@ -723,25 +731,25 @@ __device__ __forceinline__ void issue_tile_w(const DecodeArgs& a, const JobLane<
       const int jj = side ? j - R::NK : j;
       const uint32_t tr = (uint32_t)(t0 + jj * R::RPI);  // the job's first token in the block
       const uint32_t ch = tr >> tpc_shift;
-      uint32_t cb = pg + (uint32_t)L.o_data;
+      uint64_t cb = pg + (uint64_t)L.o_data;
       if constexpr (BITS >= 4) cb = ch == 1 ? cb1 : cb;
       if constexpr (BITS == 8) cb = ch == 2 ? cb2 : (ch == 3 ? cb3 : cb);
-      const uint32_t base = cb + (tr & ((1u << tpc_shift) - 1)) * rowb;
-      dma16(a.pages, base + jl.off[m], slot + (side ? R::OFF_V : 0) + 1024 * jj);
+      const uint64_t base = cb + (uint64_t)((tr & ((1u << tpc_shift) - 1)) * rowb);
+      dma16(a.pages + base, jl.off[m], slot + (side ? R::OFF_V : 0) + 1024 * jj);
     } else if (j < 2 * R::NK + 2) {
-      const uint32_t base = pg + (uint32_t)(((t0 >> a.kg_shift) * L.H) * D * 2);
-      if (lane < D / 2) dma16(a.pages, base + jl.off[m], slot + R::OFF_KS + (j - 2 * R::NK) * 4 * D * 2);
+      const uint64_t base = pg + (uint64_t)(((t0 >> a.kg_shift) * L.H) * D * 2);
+      if (lane < D / 2) dma16(a.pages + base, jl.off[m], slot + R::OFF_KS + (j - 2 * R::NK) * 4 * D * 2);
     } else {
-      const uint32_t base = pg + (uint32_t)(t0 * L.H * G * 2);
-      dma16(a.pages, base + jl.off[m], slot + R::OFF_VS);
+      const uint64_t base = pg + (uint64_t)(t0 * L.H * G * 2);
+      dma16(a.pages + base, jl.off[m], slot + R::OFF_VS);
     }
   }
 }
 
 template <int D, int BITS>
 __device__ __forceinline__ void issue_tile(const DecodeArgs& a, const JobLane<D, BITS>& jl, uint32_t slot, bool fast,
-                                           int t0, int lane, int wv, uint32_t pg, uint32_t cb1, uint32_t cb2,
-                                           uint32_t cb3) {
+                                           int t0, int lane, int wv, uint64_t pg, uint64_t cb1, uint64_t cb2,
+                                           uint64_t cb3) {
   switch (wv) {
     case 0: issue_tile_w<D, BITS, 0>(a, jl, slot, fast, t0, lane, pg, cb1, cb2, cb3); break;
     case 1: issue_tile_w<D, BITS, 1>(a, jl, slot, fast, t0, lane, pg, cb1, cb2, cb3); break;
@@ -761,9 +769,10 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
   const int c = lane >> 4;
   constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
   uint32_t kw[KW];
+  static_assert(BITS != 8 || KW == 4 * k_units<D, BITS>(), "INT8 K slice: whole 16-byte units");
   if constexpr (BITS == 8) {
-    load_bytes<16>(sp + k.k_rd[0], kw);
-    load_bytes<16>(sp + k.k_rd[1], kw + 4);
+#pragma unroll
+    for (int e = 0; e < k_units<D, BITS>(); ++e) load_bytes<16>(sp + k.k_rd[e], kw + 4 * e);
   } else {
     load_bytes<CPL * BITS / 8>(sp + k.k_rd[0], kw);
   }
@@ -833,6 +842,9 @@ __device__ __forceinline__ void wait_tile(int ahead) {
 }
 
 __device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+__device__ __forceinline__ uint64_t rl64(uint64_t v, int lane) {
+  return (uint64_t)rl((uint32_t)v, lane) | ((uint64_t)rl((uint32_t)(v >> 32), lane) << 32);
+}
 
 // Blocks per split of a sequence of n_blocks blocks:
 // max(blocks_per_split, ceil(blocks / num_splits)).
@@ -984,10 +996,10 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
     auto issue = [&](int tt) {
       const int b = tt >> tpb_shift;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
-      const uint32_t pg = rl(bl.pg, b);
-      const uint32_t cb1 = BITS >= 4 ? rl(bl.cb1, b) : 0u;
-      const uint32_t cb2 = BITS == 8 ? rl(bl.cb2, b) : 0u;
-      const uint32_t cb3 = BITS == 8 ? rl(bl.cb3, b) : 0u;
+      const uint64_t pg = rl64(bl.pg, b);
+      const uint64_t cb1 = BITS >= 4 ? rl64(bl.cb1, b) : 0u;
+      const uint64_t cb2 = BITS == 8 ? rl64(bl.cb2, b) : 0u;
+      const uint64_t cb3 = BITS == 8 ? rl64(bl.cb3, b) : 0u;
       const uint32_t slot = ring0 + (uint32_t)((tt % R::NBUF) * R::SLOT);
       issue_tile<D, BITS>(a, jl, slot, piped(tt), t0, lane, wv, pg, cb1, cb2, cb3);
     };
@@ -1182,13 +1194,9 @@ template <int D, int BITS, bool QLO>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
   const dim3 block(64 * kHeadsPerGroup);
   const size_t lds = (size_t)Ring<D, BITS>::WG_BYTES;
-  static bool attr = false;  // idempotent; set once per instantiation
-  if (!attr) {
-    if (hipFuncSetAttribute((const void*)decode_kernel<D, BITS, QLO>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
-      return hipErrorInvalidValue;
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr_done{0};  // devices whose limit is raised, one bit each
+  if (ensure_lds_limit((const void*)decode_kernel<D, BITS, QLO>, (int)lds, &attr_done) != hipSuccess)
+    return hipErrorInvalidValue;
   const long n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
   const long span = 8 * n_hg;  // the kernel permutes workgroups within runs of `span`
   const long items = (a.num_seqs * a.num_splits * n_hg + span - 1) / span * span;

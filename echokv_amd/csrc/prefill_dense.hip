@@ -474,13 +474,9 @@ template <int D, bool QLO>
 static hipError_t flash_one(const FlashArgs& a, hipStream_t s) {
   constexpr int NBUF = kDenseRing;
   constexpr int lds = NBUF * Ws<D>::BYTES;
-  static bool attr = false;
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute((const void*)flash_kernel<D, QLO, NBUF>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr_done{0};  // devices whose limit is raised, one bit each
+  const hipError_t e = ensure_lds_limit((const void*)flash_kernel<D, QLO, NBUF>, lds, &attr_done);
+  if (e != hipSuccess) return e;
   const long n = (long)a.n_qtiles * a.H;
   hipLaunchKernelGGL((flash_kernel<D, QLO, NBUF>), dim3((unsigned)n), dim3(64 * kDenseWaves), lds, s, a);
   return hipGetLastError();

@@ -12,7 +12,7 @@ namespace ek {
 
 
 // ---------------------------------------------------------------------------
-// write_tokens (echokv_vllm/kernels/write.py:170-202, 280-338)
+// write_tokens (echokv_vllm/kernels/write.py:29-36, 172-229)
 // ---------------------------------------------------------------------------
 
 __global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) {
@@ -152,7 +152,7 @@ __device__ __forceinline__ void quantize_k_group(const Lay& L, uint8_t* pages, l
 }
 
 // ---------------------------------------------------------------------------
-// finalize_k (echokv_vllm/kernels/write.py:205-230, 340-396)
+// finalize_k (echokv_vllm/kernels/write.py:39-50, 232-287)
 // ---------------------------------------------------------------------------
 
 // The common case -- key and residual of one dtype, a group of at most 32

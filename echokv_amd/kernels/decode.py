@@ -61,6 +61,8 @@ def decode_attention(
     Blocks of other tiers are read correctly either way.
     """
     L = store.layout
+    if L.k_group < 16:
+        raise ValueError(f"decode reads one K group per 16-token tile: k_group must be >= 16, got {L.k_group}")
     dev = query.device
     _lib.require_device(query, block_table, seq_lens, store.pages)
     s = seq_lens.shape[0]
@@ -88,12 +90,10 @@ def decode_attention(
     if tier is None:
         tier = store.pool.majority_tier()
     res = _lib.residual(store.res_k)
-    _lib.call(
-        "echokv_decode", _lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(store.block_res),
-        _lib.ptr(store.res_group), _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1),
-        _lib.dtype_code(query), hq, _lib.ptr(q_rows), _lib.ptr(block_table), block_table.stride(0),
-        _lib.ptr(bt_rows), _lib.ptr(lens), s, float(softmax_scale), int(num_splits), int(blocks_per_split),
-        int(tier), _lib.ptr(acc), _lib.ptr(ml), _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out),
-        _lib.stream(),
-    )
+    head = (_lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(store.block_res), _lib.ptr(store.res_group),
+            _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1), _lib.dtype_code(query), hq,
+            _lib.ptr(q_rows), _lib.ptr(block_table), block_table.stride(0), _lib.ptr(bt_rows), _lib.ptr(lens), s,
+            float(softmax_scale), int(num_splits), int(blocks_per_split), int(tier))
+    tail = (_lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out), _lib.stream())
+    _lib.call("echokv_decode", *head, _lib.ptr(acc), _lib.ptr(ml), *tail)
     return out

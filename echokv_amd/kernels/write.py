@@ -56,11 +56,12 @@ def finalize_k(store, key: torch.Tensor, meta, full_grid: bool = False) -> None:
     n = meta.n_rows if full_grid else meta.n_fin
     if n == 0 or meta.fin.shape[0] == 0:  # no rows staged: the device count is 0 too
         return
+    fin = meta.fin
+    width = 3 + store.layout.k_group
+    if fin.dtype != torch.int64 or fin.shape[-1] != width or fin.stride(1) != 1 or fin.stride(0) != width:
+        raise ValueError(f"meta.fin must be int64 [n, {width}] with contiguous rows (row stride {width})")
     _lib.require_device(key, store.pages)
     key = _kv(key)
-    fin = meta.fin
-    if fin.numel() and fin.stride(1) != 1:
-        raise ValueError("meta.fin must have contiguous rows")
     # A full grid only reads rows below the device count (<= fin's rows).
     res = _lib.residual(store.res_k)
     _lib.call(

@@ -6,7 +6,9 @@
  * argument. The library never allocates, frees, synchronizes or reads device
  * memory from the host; every buffer is caller-owned, so calls can be captured
  * in a HIP graph. Pointers are device pointers unless noted; strides are in
- * elements. Functions are reentrant (no mutable global state).
+ * elements. Functions are reentrant: the only process state is a per-device bit
+ * recording that a kernel's dynamic-LDS limit was raised (set atomically, by an
+ * idempotent call).
  *
  * Each entry point names the reference interface it replaces
  * (paths relative to the zimo0110/echokv tree).
@@ -58,7 +60,7 @@ const char* echokv_error_string(int code);
  * K to the residual / under sealed stats / to the K_ref ring.
  * tok: [4, tok_s0] int64 = (slot, residual slot, sealed, kref row) per row.
  * Replaces echokv_vllm/kernels/write.py:29-36 (write_tokens) and its kernel
- * write.py:280-338 (_write_tokens_kernel). kref may be NULL. */
+ * write.py:172-229 (_write_tokens_kernel). kref may be NULL. */
 int echokv_write_tokens(const echokv_layout* L, uint8_t* pages,
                         const void* key, int64_t k_s0, int64_t k_s1,
                         const void* value, int64_t v_s0, int64_t v_s1, int32_t kv_dtype,
@@ -69,7 +71,7 @@ int echokv_write_tokens(const echokv_layout* L, uint8_t* pages,
 /* Per-channel quantization of each completed K group.
  * fin: [>= grid_rows, 3 + k_group] int64 = (block, group, residual slot, token row per
  * position or -1 = residual); rows >= *fin_count are skipped (graph full grid).
- * Replaces echokv_vllm/kernels/write.py:39-50 (finalize_k), kernel write.py:340-396. */
+ * Replaces echokv_vllm/kernels/write.py:39-50 (finalize_k), kernel write.py:232-287. */
 int echokv_finalize_k(const echokv_layout* L, uint8_t* pages,
                       const void* key, int64_t k_s0, int64_t k_s1, int32_t kv_dtype,
                       const int64_t* fin, const int64_t* fin_count, int64_t grid_rows,

@@ -10,7 +10,7 @@ Modules (each function cites the reference file:line it restates):
 * ``quant``     -- storage numerics (``echokv_vllm/quant.py``)
 * ``store``     -- page layout, addressing, write / finalize / seal / demote
                    device effects, and ``gather`` (``echokv_vllm/tiered_cache.py``,
-                   ``echokv_vllm/kernels/write.py:170-230``)
+                   ``echokv_vllm/kernels/write.py:61-121``)
 * ``attention`` -- decode and chunked-prefill attention over ``gather``
                    (``echokv_vllm/kernels/decode.py:95-129``,
                    ``echokv_vllm/kernels/prefill.py:210-236``)

@@ -32,21 +32,48 @@ def decode_attention(store, query, block_table, seq_lens, scale, vectorized=Fals
     store's vectorized gather (same values)."""
     out = np.zeros(query.shape, np.float64)
     for i, n in enumerate(np.asarray(seq_lens).tolist()):
-        if vectorized:
+        if vectorized:  # one matrix product per head; a single query sees every key
             pos = np.arange(n)
             k, v = store.gather_vec(np.asarray(block_table[i], np.int64)[pos // store.L.bs], pos % store.L.bs)
+            out[i] = attend_causal(query[i][None], k, v, scale)[0]
         else:
             k, v = store.gather_seq(block_table[i], n)
-        out[i] = attend(query[i], k, v, scale)
+            out[i] = attend(query[i], k, v, scale)
     return out
 
 
-def prefill_attention(store, query, prefill, req_of, block_table, scale):
-    """prefill.py:210-236: ``prefill`` = [(q_start, q_end, ctx, _)], ``req_of`` = block-table rows."""
+def prefill_attention(store, query, prefill, req_of, block_table, scale, vectorized=False):
+    """prefill.py:210-236: ``prefill`` = [(q_start, q_end, ctx, _)], ``req_of`` = block-table rows.
+    ``vectorized`` reads the cache with the vectorized gather and computes each
+    (request, query head) as float64 matrix products (same values as the loop)."""
     out = np.zeros(query.shape, np.float64)
     for (qs, qe, ctx, _), r in zip(prefill, req_of):
-        k, v = store.gather_seq(block_table[r], ctx)
         nq = qe - qs
-        for i in range(nq):
-            out[qs + i] = attend(query[qs + i], k, v, scale, limit=ctx - nq + i + 1)
+        if not vectorized:
+            k, v = store.gather_seq(block_table[r], ctx)
+            for i in range(nq):
+                out[qs + i] = attend(query[qs + i], k, v, scale, limit=ctx - nq + i + 1)
+            continue
+        pos = np.arange(ctx)
+        k, v = store.gather_vec(np.asarray(block_table[r], np.int64)[pos // store.L.bs], pos % store.L.bs)
+        out[qs:qe] = attend_causal(query[qs:qe], k, v, scale)
+    return out
+
+
+def attend_causal(q, k, v, scale):
+    """``q [nq, Hq, D]`` over ``k, v [n, H, D]`` with the bottom-right causal limit
+    (query i sees keys < n - nq + i + 1), float64, one matrix product per head."""
+    nq, hq, _ = q.shape
+    n, h = k.shape[0], k.shape[1]
+    rep = hq // h
+    keep = np.arange(n)[None, :] <= (n - nq + np.arange(nq))[:, None]
+    out = np.empty(q.shape, np.float64)
+    for hh in range(hq):
+        kh = k[:, hh // rep].astype(np.float64)
+        s = (q[:, hh].astype(np.float64) @ kh.T) * scale
+        s = np.where(keep, s, -np.inf)
+        s -= s.max(axis=1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=1, keepdims=True)
+        out[:, hh] = p @ v[:, hh // rep].astype(np.float64)
     return out

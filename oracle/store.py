@@ -4,9 +4,9 @@ Restates the device-side effects of the reference store on raw page bytes:
 
 * layout and addressing: ``echokv_vllm/tiered_cache.py:99-147`` (offsets),
   ``tiered_cache.py:350-375`` (chunk / row / byte of a token, pack into a side);
-* token writes: ``echokv_vllm/kernels/write.py:170-202`` (V per token, K to the
+* token writes: ``echokv_vllm/kernels/write.py:61-95`` (V per token, K to the
   residual or under sealed stats, K_ref ring);
-* K-group finalize: ``write.py:205-230``;
+* K-group finalize: ``write.py:96-121``;
 * seal of an evicted residual group: ``tiered_cache.py:379-394``;
 * LRU demotion requantization to INT2: ``tiered_cache.py:322-340``;
 * ``gather`` (the read oracle): ``tiered_cache.py:451-478``.
@@ -88,6 +88,18 @@ class PageStore:
         self.block_res = np.full(num_blocks, -1, np.int64)
         self.res_group = np.zeros(residual_slots + 1, np.int64)
 
+    @classmethod
+    def over(cls, L: Layout, pages, res_k, block_res, res_group):
+        """A store over existing arrays (e.g. a device store's bytes copied to the host)."""
+        ps = cls.__new__(cls)
+        ps.L, ps.n = L, pages.shape[0]
+        ps.page_bytes = pages.shape[1]
+        ps.pages = pages
+        ps.res_k = res_k
+        ps.block_res = np.asarray(block_res, np.int64)
+        ps.res_group = np.asarray(res_group, np.int64)
+        return ps
+
     # -- typed views ------------------------------------------------------
     def _f16(self, blk, start, count):
         return self.pages[blk, start : start + 2 * count].view(np.float16)
@@ -114,7 +126,7 @@ class PageStore:
         m = self._f16(blk, o["k_min"] + grp * n * 2, n).reshape(L.h, L.d)
         return s, m
 
-    # -- addressing (tiered_cache.py:350-375; write.py:250-262) -------------
+    # -- addressing (tiered_cache.py:350-375; write.py:142-153) -------------
     def locate(self, blk: int, off: int, bits: int):
         """(page, byte offset inside the page) of token ``off``'s K+V row at ``bits``."""
         L = self.L
@@ -154,7 +166,7 @@ class PageStore:
         self.res_group[np.asarray(slots, np.int64)] = groups
 
     def write_tokens(self, key, value, tok, kref=None):
-        """write.py:170-202 (and the Triton kernel write.py:280-338): ``tok [4, n]``."""
+        """write.py:61-95 (and the Triton kernel write.py:172-229): ``tok [4, n]``."""
         L = self.L
         for t in range(tok.shape[1]):
             slot = int(tok[0, t])
@@ -178,7 +190,7 @@ class PageStore:
                 kref[int(tok[3, t])] = kx.astype(kref.dtype)
 
     def finalize_k(self, key, fin):
-        """write.py:205-230 (Triton write.py:340-396): one row per completed K group."""
+        """write.py:96-121 (Triton write.py:232-287): one row per completed K group."""
         L = self.L
         for row in np.asarray(fin, np.int64):
             blk, grp, rs = int(row[0]), int(row[1]), int(row[2])
@@ -269,10 +281,39 @@ class PageStore:
         pos = np.arange(n)
         return self.gather(np.asarray(table_row, np.int64)[pos // self.L.bs], pos % self.L.bs)
 
+    def raw_vec(self, blk, off, bits):
+        """Stored codes and stats of tokens (blk, off) whose blocks are all at ``bits``,
+        vectorized: K codes, V codes ``[n, H, D]`` u8; V scale / min ``[n, H, G]`` and
+        K scale / min of each token's K group ``[n, H, D]`` fp16 (tiered_cache.py:350-375)."""
+        L, o = self.L, self.L.offsets
+        b = np.asarray(blk, np.int64).reshape(-1)
+        t = np.asarray(off, np.int64).reshape(-1)
+        n = b.size
+        tpc = L.tokens_per_chunk(bits)
+        j = t // tpc
+        ids = self.pages[b, 4:16].copy().view(np.int32)[np.arange(n), np.maximum(j - 1, 0)].astype(np.int64)
+        page = np.where(j > 0, ids // L.kc, b)
+        cslot = np.where(j > 0, ids % L.kc, 0)
+        sb = L.side_bytes(bits)
+        base = o["data"] + cslot * L.chunk_bytes + (t % tpc) * 2 * sb
+        cols = np.arange(sb)
+        kc = Q.unpack(self.pages[page[:, None], base[:, None] + cols].reshape(n, L.h, -1), bits)
+        vc = Q.unpack(self.pages[page[:, None], base[:, None] + sb + cols].reshape(n, L.h, -1), bits)
+        ng, nk = L.h * L.g, L.h * L.d
+        def f16(start, count):
+            return self.pages[b[:, None], start[:, None] + np.arange(2 * count)].copy().view(np.float16)
+        vs = f16(o["v_scale"] + t * ng * 2, ng).reshape(n, L.h, L.g)
+        vm = f16(o["v_min"] + t * ng * 2, ng).reshape(n, L.h, L.g)
+        g = t // L.kg
+        ks = f16(o["k_scale"] + g * nk * 2, nk).reshape(n, L.h, L.d)
+        km = f16(o["k_min"] + g * nk * 2, nk).reshape(n, L.h, L.d)
+        return kc, vc, vs, vm, ks, km
+
     def gather_vec(self, blk, off):
         """``gather`` vectorized over tokens (numpy fancy indexing per tier); the same
-        values, used where the per-token loop is too slow (the CPU baseline)."""
-        L, o = self.L, self.L.offsets
+        values, used where the per-token loop is too slow (the CPU baseline, tests at
+        the benchmark configurations)."""
+        L = self.L
         blk = np.asarray(blk, np.int64).reshape(-1)
         off = np.asarray(off, np.int64).reshape(-1)
         n = blk.size
@@ -285,28 +326,9 @@ class PageStore:
             m = np.flatnonzero(tags == bits)
             if not m.size:
                 continue
-            b, t = blk[m], off[m]
-            tpc = L.tokens_per_chunk(bits)
-            j = t // tpc
-            ids = self.pages[b, 4:16].copy().view(np.int32)[np.arange(m.size), np.maximum(j - 1, 0)].astype(np.int64)
-            page = np.where(j > 0, ids // L.kc, b)
-            cslot = np.where(j > 0, ids % L.kc, 0)
-            sb = L.side_bytes(bits)
-            base = o["data"] + cslot * L.chunk_bytes + (t % tpc) * 2 * sb
-            cols = np.arange(sb)
-            kraw = self.pages[page[:, None], base[:, None] + cols]
-            vraw = self.pages[page[:, None], base[:, None] + sb + cols]
-            kc = Q.unpack(kraw.reshape(m.size, L.h, -1), bits)
-            vc = Q.unpack(vraw.reshape(m.size, L.h, -1), bits)
-            ng = L.h * L.g
-            vs = self.pages[b[:, None], o["v_scale"] + (t * ng * 2)[:, None] + np.arange(2 * ng)].copy().view(np.float16)
-            vm = self.pages[b[:, None], o["v_min"] + (t * ng * 2)[:, None] + np.arange(2 * ng)].copy().view(np.float16)
-            v_out[m] = Q.dequantize(vc, vs.reshape(m.size, L.h, L.g), vm.reshape(m.size, L.h, L.g), L.vg)
-            nk = L.h * L.d
-            g = t // L.kg
-            ks = self.pages[b[:, None], o["k_scale"] + (g * nk * 2)[:, None] + np.arange(2 * nk)].copy().view(np.float16)
-            km = self.pages[b[:, None], o["k_min"] + (g * nk * 2)[:, None] + np.arange(2 * nk)].copy().view(np.float16)
-            k_out[m] = Q.dequantize_with(kc, ks.reshape(m.size, L.h, L.d), km.reshape(m.size, L.h, L.d))
+            kc, vc, vs, vm, ks, km = self.raw_vec(blk[m], off[m], bits)
+            v_out[m] = Q.dequantize(vc, vs, vm, L.vg)
+            k_out[m] = Q.dequantize_with(kc, ks, km)
         r = np.flatnonzero(in_res & np.isin(tags, Q.SUPPORTED_BITS))
         if r.size:
             k_out[r] = self.res_k[slot[r], off[r] % L.kg].astype(np.float32)

@@ -60,6 +60,7 @@ def test_decode_rejects_bad_arguments_before_launching(lib):
     assert _decode(lib, _layout(head_size=96)) == 2          # D must be 64 or 128
     assert _decode(lib, _layout(block_size=24)) == 2         # block not a multiple of 16
     assert _decode(lib, _layout(block_size=48, k_group=16)) == 2  # decode needs a power-of-2 block
+    assert _decode(lib, _layout(k_group=8)) == 2             # a 16-token tile spans two K groups
     assert _decode(lib, _layout(), tier=3) != 0
     assert _decode(lib, _layout(), splits=0) != 0
     assert _decode(lib, _layout(), seqs=-1) != 0
@@ -97,3 +98,26 @@ def test_prefill_dense_workspace_size_and_argument_checks(lib):
     assert _prefill_dense(lib, L, ws_bytes=1000) != 0         # workspace too small
     assert _prefill_dense(lib, L, n_packs=-1) != 0
     assert _prefill_dense(lib, L, n_q=0) == 0                 # nothing to do: no launch
+
+
+def test_python_guards_refuse_before_any_device_work():
+    """decode refuses K groups shorter than its 16-token tile; finalize_k refuses a
+    fin table whose rows are not packed at 3 + k_group int64 (the kernel's stride)."""
+    from types import SimpleNamespace
+
+    import torch
+
+    from echokv_amd.kernels.decode import decode_attention
+    from echokv_amd.kernels.write import finalize_k
+    from echokv_amd.write_plan import WriteMeta
+
+    store = SimpleNamespace(layout=TieredLayout(8, 128, 16, 8, 8, 32))
+    q = torch.zeros(1, 32, 128)
+    with pytest.raises(ValueError, match="k_group must be >= 16"):
+        decode_attention(store, q, torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.long), 0.1)
+    store = SimpleNamespace(layout=TieredLayout(8, 128, 16, 8, 16, 32))
+    wide = torch.zeros(2, 40, dtype=torch.long)
+    meta = WriteMeta(tok=torch.zeros(4, 1, dtype=torch.long), fin=wide[:, :19], fin_count=torch.ones(1, dtype=torch.long),
+                     n_rows=1, n_fin=1)
+    with pytest.raises(ValueError, match="row stride 19"):
+        finalize_k(store, torch.zeros(1, 8, 128), meta)

@@ -1,0 +1,325 @@
+"""GPU parity at the benchmark configurations' own shapes, and on the kernel
+paths small cases never reach (tests/echokv_vllm/test_decode_kernel.py:69-75
+runs the 8B shape the same way).
+
+Each store is written through the product's own write path (planner + HIP
+write kernels); the oracle then reads the device's page bytes (copied to the
+host) and computes attention in float64. Every test prints its worst error
+against the 2e-3 budget, so the margin is visible in the log.
+
+* cfg2: one full layer per tier -- 64 sequences, contexts U[512, 8192] (seed 1),
+  H 8 / D 128 / block 16 / K group 16 / V group 32, fp16 K/V with 1% of K
+  channels x10, the context then one decode-step write -- decoded with fp16 and
+  bf16 queries and through the generic (other-tier) path.
+* cfg3: 2 sequences x 4096 tokens written in 512-token chunks, INT4, bf16
+  K/V/Q and residual: every stored code and statistic byte-exact against the
+  vectorized quantization, and chunked-prefill attention of the first and last
+  chunks (two-pass path) plus a short tail chunk (fused path).
+* cfg4 shape: GQA 8 (Hq 64), one 32k-token sequence: default splits, a split of
+  more than 64 blocks (the chunk loop), more than 64 splits (the two-pass merge);
+  the canary at Hq 64.
+* more than 64 sequences (the chunked work-item scan), V groups of 16 and 64,
+  head size 64, and a layer view whose pages span more than 4 GiB (64-bit page
+  addressing, as in a layer view of a pool interleaved across layers).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from echokv_amd.canary import canary_kl
+from echokv_amd.kernels import decode as dec
+from echokv_amd.kernels import prefill as pf
+from echokv_amd.tiered_cache import TieredKVCache, TieredLayout
+from gpu_util import maxdiff
+from oracle import attention as OA
+from oracle import canary as OC
+from oracle import quant as Q
+from oracle import store as OS
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def oracle_view(store) -> OS.PageStore:
+    """The oracle over a copy of a device store's bytes and residual state."""
+    L = store.layout
+    OL = OS.Layout(L.num_kv_heads, L.head_size, L.block_size, L.mem_bits, L.k_group, L.v_group)
+    return OS.PageStore.over(OL, store.pages.cpu().numpy(), store.res_k.float().cpu().numpy(),
+                             store.block_res.cpu().numpy(), store.res_group.cpu().numpy())
+
+
+def block_table(rng, lens, bs, spare=16):
+    """Each sequence's blocks drawn from a seeded permutation of the pages."""
+    nbs = -(-(np.asarray(lens) + 1) // bs)
+    nb = int(nbs.sum()) + spare
+    perm = rng.permutation(nb)
+    table = np.zeros((len(lens), int(nbs.max())), np.int64)
+    o = 0
+    for i, n in enumerate(nbs.tolist()):
+        table[i, :n] = perm[o : o + n]
+        o += n
+    return table, nb
+
+
+def slots_of(table, lens, pos_fn, bs):
+    return np.concatenate([table[i][p // bs] * bs + p % bs for i, p in ((i, pos_fn(i, n)) for i, n in enumerate(lens))])
+
+
+def build_layer(device, lens, bits, *, h=8, d=128, bs=16, kg=16, vg=32, mem_bits=8, dtype=torch.float16, seed=1,
+                outliers=0.01, pages=None, table=None):
+    """A layer store written through the product path: each sequence's first
+    len - 1 tokens in one step, then its last token in a second (decode) step."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, np.int64)
+    if table is None:
+        table, nb = block_table(rng, lens, bs)
+    layout = TieredLayout(h, d, bs, mem_bits, kg, vg)
+    if pages is None:
+        page = bs * TieredLayout.per_token_bytes(h, d, mem_bits, kg, vg)
+        pages = torch.zeros(nb, page, dtype=torch.uint8, device=device)
+    store = TieredKVCache(layout, pages, residual_slots=len(lens) + 16, residual_dtype=dtype)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    out_ch = torch.randperm(h * d, generator=gen, device=device)[: round(outliers * h * d)]
+
+    def kv(n):
+        k = torch.randn(n, h, d, generator=gen, device=device)
+        k.view(n, h * d)[:, out_ch] *= 10
+        v = torch.randn(n, h, d, generator=gen, device=device)
+        return k.to(dtype), v.to(dtype)
+
+    pre = slots_of(table, lens, lambda i, n: np.arange(n - 1), bs)
+    if pre.size:
+        k, v = kv(pre.size)
+        store.write(k, v, torch.from_numpy(pre).to(device), bits)
+    last = slots_of(table, lens, lambda i, n: np.array([n - 1]), bs)
+    k, v = kv(last.size)
+    store.write(k, v, torch.from_numpy(last).to(device), bits)
+    torch.cuda.synchronize()
+    return store, table
+
+
+def check(label, got, ref, tol=TOL):
+    err = maxdiff(got, ref)
+    print(f"[{label}] max err {err:.3e} (budget {tol:g})", flush=True)
+    assert err <= tol, f"{label}: max err {err}"
+    return err
+
+
+# ---- cfg2 -----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bits", [8, 4, 2])
+def test_cfg2_full_layer_decode_matches_oracle(device, bits):
+    rng = np.random.default_rng(1)
+    lens = rng.integers(512, 8193, 64)
+    print(f"[cfg2] int{bits}: writing {int(lens.sum())} tokens", flush=True)
+    store, table = build_layer(device, lens, bits, seed=1)
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    lens_d = torch.from_numpy(lens).to(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(11)
+    q = torch.randn(64, 32, 128, device=device, generator=gen).half()
+    scale = 128 ** -0.5
+    for qt, name in ((q, "fp16 q"), (q.bfloat16(), "bf16 q")):
+        ref = OA.decode_attention(ps, qt.float().cpu().numpy(), table, lens, scale, vectorized=True)
+        got = dec.decode_attention(store, qt, table_d, lens_d, scale, tier=bits)
+        check(f"cfg2 int{bits} {name}", got, ref)
+        if name == "fp16 q":  # every tile through the generic path (the layer's tier set elsewhere)
+            other = 4 if bits != 4 else 8
+            got = dec.decode_attention(store, qt, table_d, lens_d, scale, tier=other)
+            check(f"cfg2 int{bits} as tier {other}", got, ref)
+
+
+# ---- cfg3 -----------------------------------------------------------------------------
+
+def test_cfg3_chunked_prefill_bf16_writes_and_attention(device):
+    h, d, bs, kg, vg, hq, seqs, ctx, chunk = 8, 128, 16, 16, 32, 32, 2, 4096, 512
+    rng = np.random.default_rng(2)
+    nbs = ctx // bs
+    nb = seqs * nbs + 16
+    table = rng.permutation(nb)[: seqs * nbs].reshape(seqs, nbs).astype(np.int64)
+    layout = TieredLayout(h, d, bs, 8, kg, vg)
+    page = bs * TieredLayout.per_token_bytes(h, d, 8, kg, vg)
+    store = TieredKVCache(layout, torch.zeros(nb, page, dtype=torch.uint8, device=device), residual_slots=seqs + 16,
+                          residual_dtype=torch.bfloat16)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(2)
+    K = torch.randn(seqs, ctx, h, d, device=device, generator=gen).bfloat16()
+    V = torch.randn(seqs, ctx, h, d, device=device, generator=gen).bfloat16()
+    Qr = torch.randn(seqs, ctx, hq, d, device=device, generator=gen).bfloat16()
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    scale = d ** -0.5
+    for c in range(ctx // chunk):
+        pos = np.arange(c * chunk, (c + 1) * chunk)
+        slots = np.concatenate([table[s][pos // bs] * bs + pos % bs for s in range(seqs)])
+        sl = slice(c * chunk, (c + 1) * chunk)
+        store.write(K[:, sl].reshape(-1, h, d), V[:, sl].reshape(-1, h, d), torch.from_numpy(slots).to(device), 4)
+        if c not in (0, ctx // chunk - 1):
+            continue
+        q = Qr[:, sl].reshape(-1, hq, d)
+        n_ctx = (c + 1) * chunk
+        prefill = [(s * chunk, (s + 1) * chunk, n_ctx, 0) for s in range(seqs)]
+        assert pf.use_dense(prefill, d)
+        out = torch.zeros(seqs * chunk, hq, d, device=device)
+        pf.prefill_attention(store, q, out, prefill, [0, 1], table_d, scale)
+        torch.cuda.synchronize()
+        ps = oracle_view(store)
+        ref = OA.prefill_attention(ps, q.float().cpu().numpy(), prefill, [0, 1], table, scale, vectorized=True)
+        check(f"cfg3 chunk {c} (two-pass)", out, ref)
+    # The fused path on the last 48 queries of each sequence over the full context.
+    tail = 48
+    q = Qr[:, ctx - tail :].reshape(-1, hq, d)
+    prefill = [(s * tail, (s + 1) * tail, ctx, 0) for s in range(seqs)]
+    out = torch.zeros(seqs * tail, hq, d, device=device)
+    pf.prefill_attention(store, q, out, prefill, [0, 1], table_d, scale)
+    torch.cuda.synchronize()
+    ref = OA.prefill_attention(ps, q.float().cpu().numpy(), prefill, [0, 1], table, scale, vectorized=True)
+    check("cfg3 tail (fused)", out, ref)
+
+    # Every stored code and statistic, byte-exact (quant.py:26-75 on the bf16 inputs).
+    pos = np.arange(ctx)
+    blk = np.concatenate([table[s][pos // bs] for s in range(seqs)])
+    off = np.concatenate([pos % bs] * seqs)
+    assert (ps.pages[blk, 0] == 4).all()
+    kc, vc, vs, vm, ks, km = ps.raw_vec(blk, off, 4)
+    kf = K.float().cpu().numpy().reshape(-1, h, d)
+    vf = V.float().cpu().numpy().reshape(-1, h, d)
+    ecodes, escale, emin = Q.quantize(vf, 4, vg)
+    np.testing.assert_array_equal(vc, ecodes)
+    np.testing.assert_array_equal(vs.view(np.uint16), escale.view(np.uint16))
+    np.testing.assert_array_equal(vm.view(np.uint16), emin.view(np.uint16))
+    kgrp = kf.reshape(-1, kg, h, d)
+    gsc, gmn = Q.stats_along(kgrp, 4, axis=1)
+    kcodes = Q.quantize_with(kgrp, gsc[:, None], gmn[:, None], 4).reshape(-1, h, d)
+    np.testing.assert_array_equal(kc, kcodes)
+    np.testing.assert_array_equal(ks.view(np.uint16), np.repeat(gsc, kg, axis=0).view(np.uint16))
+    np.testing.assert_array_equal(km.view(np.uint16), np.repeat(gmn, kg, axis=0).view(np.uint16))
+    print(f"[cfg3] {blk.size} tokens: codes and stats byte-exact", flush=True)
+
+
+# ---- cfg4 shape -----------------------------------------------------------------------
+
+def test_cfg4_gqa8_long_context_split_paths(device):
+    lens = np.array([32768])
+    store, table = build_layer(device, lens, 4, seed=3)
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    lens_d = torch.from_numpy(lens).to(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(33)
+    q = torch.randn(1, 64, 128, device=device, generator=gen).half()
+    scale = 128 ** -0.5
+    ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, scale, vectorized=True)
+    nblk = -(-32768 // 16)
+    for label, kw in (("default splits", {}),
+                      ("4 splits of 513 blocks", {"num_splits": 4}),
+                      ("187 splits of 11 blocks", {"num_splits": 200, "blocks_per_split": 1})):
+        got = dec.decode_attention(store, q, table_d, lens_d, scale, tier=4, **kw)
+        check(f"cfg4 {label}", got, ref)
+    assert -(-nblk // 4) > 64 and -(-nblk // -(-nblk // 200)) > 64
+
+
+def test_canary_at_hq64(device):
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((2, 8, 64, 128)).astype(np.float32)
+    kref = (rng.standard_normal((2, 64, 8, 128)) * 2).astype(np.float32)
+    got = canary_kl(torch.from_numpy(q).to(device).half(), torch.from_numpy(kref).to(device), (2, 4, 8), 16,
+                    128 ** -0.5)
+    ref = OC.canary_kl(q.astype(np.float16).astype(np.float32), kref, (2, 4, 8), 16, 128 ** -0.5)
+    err = float(np.abs(got.cpu().numpy() / ref - 1).max())
+    print(f"[canary hq64] max rel err {err:.3e}", flush=True)
+    np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=2e-3, atol=2e-6)
+
+
+# ---- paths small cases miss -----------------------------------------------------------
+
+def test_more_than_64_sequences_with_padding_rows(device):
+    rng = np.random.default_rng(5)
+    lens = rng.integers(1, 400, 150)
+    lens[[0, 1, 2, 70, 149]] = [1, 16, 17, 2, 1]
+    store, table = build_layer(device, lens, 4, seed=5, outliers=0.0)
+    ps = oracle_view(store)
+    run = lens.copy()
+    run[[3, 100]] = 0  # graph padding rows: left untouched
+    gen = torch.Generator(device=device)
+    gen.manual_seed(55)
+    q = torch.randn(150, 32, 128, device=device, generator=gen).half()
+    out = torch.full((150, 32, 128), 7.0, device=device)
+    dec.decode_attention(store, q, torch.from_numpy(table).to(device, torch.int32), torch.from_numpy(run).to(device),
+                         128 ** -0.5, out=out)
+    live = np.flatnonzero(run > 0)
+    ref = OA.decode_attention(ps, q[live].float().cpu().numpy(), table[live], lens[live], 128 ** -0.5,
+                              vectorized=True)
+    check("150 sequences", out[live], ref)
+    assert (out[[3, 100]] == 7.0).all()
+
+
+@pytest.mark.parametrize("d,vg", [(128, 16), (128, 64), (64, 32), (64, 16)])
+@pytest.mark.parametrize("bits", [8, 4, 2])
+def test_v_group_and_head_size_variants(device, d, vg, bits):
+    lens = np.array([1, 17, 300, 64, 1000])
+    store, table = build_layer(device, lens, bits, h=4, d=d, vg=vg, seed=6, outliers=0.02)
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(66)
+    q = torch.randn(5, 16, d, device=device, generator=gen).half()
+    got = dec.decode_attention(store, q, table_d, torch.from_numpy(lens).to(device), d ** -0.5)
+    ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, d ** -0.5, vectorized=True)
+    check(f"decode D{d} VG{vg} int{bits}", got, ref)
+    for path, chunk in (("dense", 100), ("fused", 30)):
+        prefill, row = [], 0
+        for n in lens.tolist():
+            nq = min(chunk, n)
+            prefill.append((row, row + nq, n, 0))
+            row += nq
+        qp = torch.randn(row, 16, d, device=device, generator=gen).half()
+        out = torch.zeros(row, 16, d, device=device)
+        fn = pf.prefill_attention_dense if path == "dense" else pf.prefill_attention_fused
+        fn(store, qp, out, prefill, list(range(5)), table_d, d ** -0.5)
+        torch.cuda.synchronize()
+        ref = OA.prefill_attention(ps, qp.float().cpu().numpy(), prefill, list(range(5)), table, d ** -0.5,
+                                   vectorized=True)
+        check(f"prefill {path} D{d} VG{vg} int{bits}", out, ref)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_decode_over_a_layer_view_spanning_more_than_4_gib(device, bits):
+    """One layer's view of a pool interleaved across 32 layers (page stride = 32
+    pages): 4,000 blocks span about 5 GB, and the sequences' blocks sit above
+    4 GiB while their pool chunks sit near the start. Decode must equal exact
+    attention over the view's own gathered K/V (the gather kernel addresses
+    pages with 64-bit arithmetic and is pinned to the oracle elsewhere)."""
+    h, d, bs, kg, vg = 8, 128, 16, 16, 32
+    page = bs * TieredLayout.per_token_bytes(h, d, 8, kg, vg)
+    layers, nb = 32, 4000
+    stride = page * layers
+    assert nb * stride > 4 * 2 ** 30 + 2 ** 28
+    backing = torch.zeros(nb * stride, dtype=torch.uint8, device=device)
+    pages = torch.as_strided(backing, (nb, page), (stride, 1), storage_offset=5 * page)
+    lens = np.array([700, 1500, 33, 2049])
+    rng = np.random.default_rng(7)
+    need = int((-(-(lens + 1) // bs)).sum())
+    high = rng.permutation(np.arange(nb - 400, nb))[:need]
+    table = np.zeros((len(lens), int((-(-(lens + 1) // bs)).max())), np.int64)
+    o = 0
+    for i, n in enumerate((-(-(lens + 1) // bs)).tolist()):
+        table[i, :n] = high[o : o + n]
+        o += n
+    assert (table[table > 0] * stride > 4 * 2 ** 30).all()
+    store, _ = build_layer(device, lens, bits, seed=7, pages=pages, table=table)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(77)
+    q = torch.randn(len(lens), 32, d, device=device, generator=gen).half()
+    got = dec.decode_attention(store, q, table_d, torch.from_numpy(lens).to(device), d ** -0.5, tier=bits)
+    ref = np.zeros(q.shape)
+    for i, n in enumerate(lens.tolist()):
+        pos = torch.arange(n, device=device)
+        k, v = store.gather(table_d[i].long()[pos // bs], pos % bs)
+        ref[i] = OA.attend(q[i].float().cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), d ** -0.5)
+    check(f"> 4 GiB view int{bits}", got, ref)
+    del backing

@@ -125,6 +125,24 @@ def test_prefill_oracle_and_gather_match_reference_output(cfg1_sims):
     prefill, req_of, pq = S.cfg1_prefill(s)
     out = OA.prefill_attention(sim.ps, pq, prefill, req_of, s.meta["table"], s.d ** -0.5)
     assert np.abs(out - g["prefill_out"]).max() < 2e-5
+    vec = OA.prefill_attention(sim.ps, pq, prefill, req_of, s.meta["table"], s.d ** -0.5, vectorized=True)
+    assert np.abs(vec - g["prefill_out"]).max() < 2e-5
+    assert np.abs(vec - out).max() < 1e-12  # the blocked form computes the loop's values
+
+
+def test_blocked_causal_attention_equals_per_query_loop():
+    """attend_causal (one matrix product per head) against attend with the
+    bottom-right limit, query by query, on GQA 3 and a chunk shorter than the context."""
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((7, 6, 16))
+    k = rng.standard_normal((20, 2, 16))
+    v = rng.standard_normal((20, 2, 16))
+    got = OA.attend_causal(q, k, v, 0.3)
+    for i in range(7):
+        ref = OA.attend(q[i], k, v, 0.3, limit=20 - 7 + i + 1)
+        assert np.abs(got[i] - ref).max() < 1e-12
+    # the last query sees every key; the first sees 14
+    assert np.abs(got[6] - OA.attend(q[6], k, v, 0.3)).max() < 1e-12
 
 
 # ---- canary.py:59-89 -----------------------------------------------------------
