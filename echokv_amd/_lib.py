@@ -22,7 +22,7 @@ _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTS = (
     "echokv_error_string", "echokv_write_tokens", "echokv_finalize_k", "echokv_seal_groups", "echokv_gather",
-    "echokv_store_blocks", "echokv_decode", "echokv_prefill", "echokv_prefill_dense", "echokv_prefill_dense_workspace",
+    "echokv_store_blocks", "echokv_decode", "echokv_decode_static", "echokv_prefill", "echokv_prefill_dense", "echokv_prefill_dense_workspace",
     "echokv_dequant_dense", "echokv_canary_kl",
 )
 
@@ -56,6 +56,8 @@ _SIGS = {
     "echokv_store_blocks": [LP, P, P, I64, P, P, I32, P],
     "echokv_decode": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, P, P, P, I64,
                       I64, I32, P],
+    "echokv_decode_static": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, P, I64,
+                             I64, I32, P],
     "echokv_prefill": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, I32, P, I64, FL, P],
     "echokv_prefill_dense": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, P, I64, I32, P, I64,
                              P, I64, FL, P],

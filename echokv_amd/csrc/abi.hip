@@ -61,6 +61,7 @@ const char* echokv_error_string(int code) {
     case ECHOKV_ESHAPE: return "layout or head shape not supported by this build";
     case ECHOKV_EDTYPE: return "unsupported dtype";
     case ECHOKV_ELAUNCH: return "kernel launch failed";
+    case ECHOKV_ETOOBIG: return "the request needs more than the library's static scratch buffer";
     default: return "unknown error";
   }
 }
@@ -178,6 +179,16 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   // ceil(2^32 / KC) is exact for chunk ids < 2^24 (fractions of id / KC are multiples of 1 / KC >= 1/4).
   a.kc_mul = L->chunks_per_page == 1 ? 0u : (uint32_t)((0x100000000ull + L->chunks_per_page - 1) / L->chunks_per_page);
   if (L->num_blocks * L->chunks_per_page >= (1LL << 24)) return ECHOKV_ESHAPE;
+  if (static_scratch) {
+    // acc [S, Hq, splits, D] then ml [S, Hq, splits, 2], float32, in the static array.
+    if (num_seqs > (1LL << 31) / num_q_heads / num_splits) return ECHOKV_ETOOBIG;
+    const int64_t rows = num_seqs * num_q_heads * num_splits;
+    if (rows * (L->head_size + 2) * 4 > (int64_t)ek::kDecodeScratchBytes) return ECHOKV_ETOOBIG;
+    void* base = nullptr;
+    if (ek::decode_scratch(&base) != hipSuccess) return ECHOKV_ELAUNCH;
+    acc = (float*)base;
+    ml = acc + rows * L->head_size;
+  }
   a.acc = acc;
   a.ml = ml;
   hipError_t e = ek::launch_decode(a, num_seqs, (hipStream_t)stream);
@@ -200,6 +211,18 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
   return decode_run(L, pages, block_res, res_group, res, query, q_s0, q_s1, q_dtype, num_q_heads, q_rows,
                     block_table, bt_s0, bt_rows, seq_lens, num_seqs, softmax_scale, num_splits, blocks_per_split,
                     tier, acc, ml, false, out, o_s0, o_s1, out_dtype, stream);
+}
+
+int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                         const int64_t* res_group, const echokv_residual* res, const void* query, int64_t q_s0,
+                         int64_t q_s1, int32_t q_dtype, int32_t num_q_heads, const int64_t* q_rows,
+                         const int32_t* block_table, int64_t bt_s0, const int64_t* bt_rows, const int64_t* seq_lens,
+                         int64_t num_seqs, float softmax_scale, int32_t num_splits, int32_t blocks_per_split,
+                         int32_t tier, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                         echokv_stream_t stream) {
+  return decode_run(L, pages, block_res, res_group, res, query, q_s0, q_s1, q_dtype, num_q_heads, q_rows,
+                    block_table, bt_s0, bt_rows, seq_lens, num_seqs, softmax_scale, num_splits, blocks_per_split,
+                    tier, nullptr, nullptr, true, out, o_s0, o_s1, out_dtype, stream);
 }
 
 int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,

@@ -198,6 +198,11 @@ inline hipError_t ensure_lds_limit(const void* kernel, int bytes, std::atomic<ui
   return e;
 }
 
+// Static scratch of echokv_decode_static (decode.hip): its size, and its address on
+// the current device (resolved once per device).
+constexpr size_t kDecodeScratchBytes = 64u << 20;
+hipError_t decode_scratch(void** ptr);
+
 hipError_t launch_write_tokens(const WriteTokArgs& a, long n_rows, hipStream_t s);
 hipError_t launch_finalize_k(const FinArgs& a, long rows, hipStream_t s);
 hipError_t launch_seal(const SealArgs& a, long n, hipStream_t s);

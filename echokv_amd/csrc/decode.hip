@@ -1219,6 +1219,31 @@ hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
+// The workspaces (acc, ml) of echokv_decode_static: a file-scope device array.
+// Each GPU the library runs on holds its own copy, at its own address, until the
+// process ends. Host code never passes `scratch` itself to a kernel (in host code
+// the name is a host-side stand-in, not a device address); it resolves the
+// current device's address once with hipGetSymbolAddress and passes that.
+static __device__ __align__(256) uint8_t scratch[kDecodeScratchBytes];
+
+hipError_t decode_scratch(void** ptr) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> per_device[kMaxDevices];  // zero-initialized: not resolved yet
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  void* p = per_device[dev].load(std::memory_order_acquire);
+  if (!p) {  // first call on this device (a racing thread resolves the same address)
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    per_device[dev].store(p, std::memory_order_release);
+  }
+  *ptr = p;
+  return hipSuccess;
+}
+
 hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s) {
   (void)num_seqs;
   const long wgs = (a.rows + 3) / 4;

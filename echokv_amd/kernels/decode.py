@@ -45,7 +45,7 @@ def decode_attention(
     out: torch.Tensor | None = None,
     max_len: int | None = None,
     num_splits: int | None = None,
-    workspace: tuple[torch.Tensor, torch.Tensor] | None = None,
+    workspace: tuple[torch.Tensor, torch.Tensor] | str | None = None,
     tier: int | None = None,
 ) -> torch.Tensor:
     """Attention of one query token per sequence over each sequence's cache.
@@ -55,7 +55,9 @@ def decode_attention(
     included). Without ``out`` returns float32 ``[S, Hq, D]``; with ``out``
     writes sequence ``i`` to ``out[q_rows[i]]`` in ``out``'s dtype; length-0
     sequences (graph padding) leave their row untouched. ``workspace`` =
-    caller-owned ``(acc [S, Hq, splits, D], ml [S, Hq, splits, 2])`` float32.
+    caller-owned ``(acc [S, Hq, splits, D], ml [S, Hq, splits, 2])`` float32, or
+    ``"static"``: the library's static scratch (no allocation at all, for code under
+    graph capture; at most 64 MiB of workspace, and calls on one GPU must not overlap).
     ``tier`` selects the kernel specialised for the layer's tier (the backend passes
     the layer controller's tier); by default the store's most common opened tier.
     Blocks of other tiers are read correctly either way.
@@ -80,7 +82,12 @@ def decode_attention(
         out = torch.empty(s if q_rows is None else query.shape[0], hq, d, device=dev, dtype=torch.float32)
     if out.stride(2) != 1:
         raise ValueError("out rows must be contiguous along head_dim")
-    if workspace is None:
+    static = isinstance(workspace, str)
+    if static:
+        if workspace != "static":
+            raise ValueError(f"workspace must be a (acc, ml) pair or 'static', got {workspace!r}")
+        acc = ml = None
+    elif workspace is None:
         acc = torch.empty(s, hq, num_splits, d, device=dev, dtype=torch.float32)
         ml = torch.empty(s, hq, num_splits, 2, device=dev, dtype=torch.float32)
     else:
@@ -95,5 +102,8 @@ def decode_attention(
             _lib.ptr(q_rows), _lib.ptr(block_table), block_table.stride(0), _lib.ptr(bt_rows), _lib.ptr(lens), s,
             float(softmax_scale), int(num_splits), int(blocks_per_split), int(tier))
     tail = (_lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out), _lib.stream())
-    _lib.call("echokv_decode", *head, _lib.ptr(acc), _lib.ptr(ml), *tail)
+    if static:
+        _lib.call("echokv_decode_static", *head, *tail)
+    else:
+        _lib.call("echokv_decode", *head, _lib.ptr(acc), _lib.ptr(ml), *tail)
     return out

@@ -32,6 +32,7 @@ enum {
   ECHOKV_ESHAPE = 2,     /* layout or head shape this build does not support */
   ECHOKV_EDTYPE = 3,     /* unsupported dtype code */
   ECHOKV_ELAUNCH = 4,    /* the HIP launch itself failed */
+  ECHOKV_ETOOBIG = 5,    /* the request exceeds the library's static scratch buffer */
 };
 
 /* One layer's page layout (echokv_vllm/tiered_cache.py:76-147, TieredLayout):
@@ -114,6 +115,22 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
                   float softmax_scale, int32_t num_splits, int32_t blocks_per_split, int32_t tier,
                   float* acc, float* ml, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
                   echokv_stream_t stream);
+
+/* echokv_decode without workspace arguments, for callers that cannot allocate
+ * (code under HIP-graph capture, serving loops that forbid allocation): acc and
+ * ml live in a static device array of the library (64 MiB per GPU, held until the
+ * process ends), so num_seqs * num_q_heads * num_splits * (head_size + 2) * 4
+ * must be at most 64 MiB, else ECHOKV_ETOOBIG and nothing is launched. The call
+ * allocates nothing. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams, or host threads) race and must be
+ * ordered by the caller. No counterpart in the reference. */
+int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                         const int64_t* res_group, const echokv_residual* res,
+                         const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype, int32_t num_q_heads,
+                         const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
+                         const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs,
+                         float softmax_scale, int32_t num_splits, int32_t blocks_per_split, int32_t tier,
+                         void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream);
 
 /* Chunked-prefill attention over the tiered pages (MFMA tiles), bottom-right causal:
  * tiles [n_tiles, 5] int32 = (first query row, tokens, first query position, ctx,
