@@ -1,4 +1,6 @@
-"""Build ``echokv_amd/libechokv.so`` (gfx950) from ``echokv_amd/csrc/*.hip`` with hipcc.
+"""Build ``echokv_amd/libechokv.so`` (gfx950) from ``echokv_amd/csrc/*.hip`` with hipcc,
+and the native host planner ``echokv_amd/libechokv_host.so`` from ``echokv_amd/host/plan.cpp``
+with g++.
 
     python -m echokv_amd.build            # or __graft_entry__.build()
 
@@ -47,6 +49,19 @@ def _run(cmd):
     return err
 
 
+HOST_SRC = PKG / "host" / "plan.cpp"
+HOST_OUT = PKG / "libechokv_host.so"
+
+
+def build_host() -> str:
+    """The native host planner (CPU code, g++): ``libechokv_host.so``."""
+    tmp = HOST_OUT.with_suffix(".so.tmp")
+    log = _run([os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
+                f"-I{PKG.parent / 'include'}", str(HOST_SRC), "-o", str(tmp)])
+    os.replace(tmp, HOST_OUT)
+    return log
+
+
 def build_library(verbose: bool = False) -> Path:
     srcs = sorted(CSRC.glob("*.hip"))
     obj_dir = PKG / "_build"
@@ -58,6 +73,7 @@ def build_library(verbose: bool = False) -> Path:
     tmp = OUT.with_suffix(".so.tmp")
     logs.append(_run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]))
     os.replace(tmp, OUT)
+    logs.append(build_host())
     if verbose:
         for l in logs:
             if l.strip():

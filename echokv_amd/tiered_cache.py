@@ -15,20 +15,21 @@ is the block's own page, later chunks come from a per-layer pool of chunk
 slots 1.. of every page (INT4 takes 1, INT8 takes 3). A block's tier is
 fixed when offset 0 is written (forward-only), using the layer's tier then.
 
-Host decisions (pool, demotion victims, counters) live in ``ChunkPool`` and
-``WritePlanner``; every device effect -- token writes, K-group finalize, seal,
-demotion, reads -- is a HIP kernel of ``libechokv.so``, launched on the
-current stream. Page-header and residual-map updates are small index writes.
+Host decisions (pool, demotion victims, counters) are native (``ChunkPool``
+and ``WritePlanner`` wrap ``libechokv_host.so``); every device effect -- token
+writes, K-group finalize, seal, demotion, reads -- is a HIP kernel of
+``libechokv.so``, launched on the current stream. Page-header and residual-map updates are small index writes.
 """
 
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass
 
 import numpy as np
 import torch
 
-from echokv_amd import _lib
+from echokv_amd import _host, _lib
 from echokv_amd._util import to_device
 from echokv_amd.write_plan import Eviction, SharedState, WriteMeta, WritePlan, stage_plan
 
@@ -112,108 +113,103 @@ class TieredLayout:
 
 class ChunkPool:
     """Host side of one layer's store: the pool of extra chunks, each block's tier
-    and chunk table, demotion victims, and the per-tier counters
-    (``tiered_cache.py:196-347``). Pure numpy; the caller applies device effects."""
+    and chunk table, demotion victims and the per-tier counters, in native code
+    (``ekh_pool_*``, ``echokv_amd/host/plan.cpp``) over the cache group's shared
+    bookkeeping. The caller applies the device effects (demotion, headers)."""
+
+    _COUNTERS = 23
 
     def __init__(self, layout: TieredLayout, num_blocks: int, shared: SharedState) -> None:
+        lib = _host.lib()
+        if shared.num_blocks != num_blocks:
+            raise ValueError("shared state does not match this layer's cache")
+        h = lib.ekh_pool_new(shared.planner._h, layout.chunks_per_page)
+        if not h:
+            raise ValueError(f"bad pool: {layout.chunks_per_page} chunks per page")
+        self._h = C.c_void_p(h)
+        self._free_fn = lib.ekh_pool_free
+        self._planner = shared.planner  # keeps the bookkeeping the pool reads alive
         self.layout = layout
         self.n = num_blocks
         self.shared = shared
-        k = layout.chunks_per_page
-        # Ids page*k + slot for slots 1..k-1, handed out lowest id first.
-        self.free: list[int] = np.arange(num_blocks * k).reshape(num_blocks, k)[:, 1:].reshape(-1)[::-1].tolist()
-        self.pool_size = len(self.free)
-        self.tag_h = np.zeros(num_blocks, np.int64)
-        self.table_h = np.zeros((num_blocks, 3), np.int64)
-        self.mark_h = np.zeros(num_blocks, np.int64)
-        self.tok_tier = np.zeros(9, np.int64)
-        self.reset_counters()
+        self.tag_h = _host.view_i64(lib.ekh_pool_tags(self._h), num_blocks, self)
+
+    def __del__(self) -> None:
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._free_fn(h)
+            self._h = None
 
     # -- counters ------------------------------------------------------------
-    def settle(self, blocks: np.ndarray) -> None:
-        cum = self.shared.cum_h[blocks]
-        np.add.at(self.tok_tier, self.tag_h[blocks], cum - self.mark_h[blocks])
-        self.mark_h[blocks] = cum
+    def _counters(self) -> np.ndarray:
+        out = np.zeros(self._COUNTERS, np.int64)
+        _host.lib().ekh_pool_counters(self._h, _host.i64p(out))
+        return out
 
     @property
     def tokens_written(self) -> dict:
-        pending = np.bincount(self.tag_h, weights=self.shared.cum_h - self.mark_h, minlength=9)
-        return {b: int(self.tok_tier[b] + pending[b]) for b in SUPPORTED_BITS}
+        c = self._counters()
+        return {b: int(c[b]) for b in SUPPORTED_BITS}
+
+    @property
+    def blocks_opened(self) -> dict:
+        c = self._counters()
+        return {b: int(c[9 + b]) for b in SUPPORTED_BITS}
+
+    @property
+    def downgraded_blocks(self) -> int:
+        return int(self._counters()[18])
+
+    @property
+    def demoted_blocks(self) -> int:
+        return int(self._counters()[19])
+
+    @property
+    def sealed_groups(self) -> int:
+        return int(self._counters()[20])
+
+    @property
+    def pool_size(self) -> int:
+        return int(self._counters()[22])
+
+    @property
+    def free(self) -> list:
+        """Free chunk ids, bottom to top (the last is handed out next)."""
+        out = np.zeros(int(self._counters()[21]), np.int64)
+        _host.lib().ekh_pool_free_list(self._h, _host.i64p(out), out.size)
+        return out.tolist()
 
     def reset_counters(self) -> None:
-        self.tok_tier[:] = 0
-        self.mark_h[:] = self.shared.cum_h
-        self.blocks_opened = {b: 0 for b in SUPPORTED_BITS}
-        self.downgraded_blocks = 0
-        self.demoted_blocks = 0
-        self.sealed_groups = 0
+        _host.lib().ekh_pool_reset_counters(self._h)
 
     # -- decisions -----------------------------------------------------------
-    def lru_victims(self, chunks_needed: int, keep: set) -> list[int]:
-        """Least recently written full INT4/INT8 blocks whose chunks cover the need."""
-        fill, last = self.shared.fill_h, self.shared.last_h
-        cand = np.flatnonzero((self.tag_h >= 4) & (fill == self.layout.block_size))
-        cand = [b for b in cand[np.argsort(last[cand], kind="stable")].tolist() if b not in keep]
-        victims, freed = [], 0
-        for b in cand:
-            if freed >= chunks_needed:
-                break
-            victims.append(b)
-            freed += NEXTRA[int(self.tag_h[b])]
-        return victims
-
-    def release_victims(self, victims: list[int]) -> None:
-        """Host bookkeeping after the victims were requantized to INT2 on the device."""
-        self.settle(np.asarray(victims, np.int64))
-        for b in victims:
-            self.free.extend(self.table_h[b, : NEXTRA[int(self.tag_h[b])]].tolist())
-            self.tag_h[b] = 2
-        self.demoted_blocks += len(victims)
-
     def open(self, blocks: np.ndarray, target_bits: int, protect, demote) -> tuple[np.ndarray, np.ndarray]:
         """(Re)open ``blocks`` at ``target_bits`` or the best tier the pool allows.
 
-        Old chunks return to the pool; if still short, ``demote(victims)`` is
-        called with least recently written full blocks (never ``blocks`` or
-        ``protect``) before allocation. Greedy in block order: INT8 while it fits,
-        then INT4, then INT2. Returns ``(blocks, headers [n, 16] uint8)``."""
-        self.settle(blocks)
-        for b in blocks.tolist():
-            self.free.extend(self.table_h[b, : NEXTRA.get(int(self.tag_h[b]), 0)].tolist())
-            self.tag_h[b] = 0
-        need = NEXTRA[target_bits] * blocks.size
-        if need > len(self.free):
-            keep = set(blocks.tolist()) | (set() if protect is None else set(np.asarray(protect).tolist()))
-            victims = self.lru_victims(need - len(self.free), keep)
-            if victims:
-                demote(victims)
-                self.release_victims(victims)
-        tiers = np.full(blocks.size, 2, np.int64)
-        start = 0
-        for bits in (b for b in (8, 4) if b <= target_bits):
-            ne = NEXTRA[bits]
-            take = min(blocks.size - start, len(self.free) // ne)
-            if take:
-                ids = self.free[len(self.free) - take * ne :][::-1]
-                del self.free[len(self.free) - take * ne :]
-                self.table_h[blocks[start : start + take], :ne] = np.asarray(ids, np.int64).reshape(take, ne)
-                tiers[start : start + take] = bits
-                start += take
-        for bits in SUPPORTED_BITS:
-            self.blocks_opened[bits] += int((tiers == bits).sum())
-        self.downgraded_blocks += int((tiers < target_bits).sum())
-        self.tag_h[blocks] = tiers
+        When the pool runs short, ``demote(victims)`` is called with the least
+        recently written full blocks the pool chose (never ``blocks`` or
+        ``protect``) before the new headers exist. Returns ``(blocks, headers [n, 16])``."""
+        blocks = _host.as_i64(blocks)
+        prot = _host.as_i64(() if protect is None else protect)
         headers = np.zeros((blocks.size, 16), np.uint8)
-        headers[:, 0] = tiers
-        headers[:, 4:] = np.ascontiguousarray(self.table_h[blocks].astype(np.int32)).view(np.uint8)
+        victims = np.zeros(self.n, np.int64)
+        nv = C.c_int64(0)
+        rc = _host.lib().ekh_pool_open(self._h, _host.i64p(blocks), blocks.size, int(target_bits), _host.i64p(prot),
+                                       prot.size, headers.ctypes.data_as(_host.PU8), _host.i64p(victims),
+                                       C.byref(nv))
+        if rc != _host.OK:
+            raise ValueError(f"cannot open blocks {blocks.tolist()[:8]} at {target_bits} bits")
+        if nv.value:
+            demote(victims[: nv.value].tolist())
         return blocks, headers
 
-    def seal_row(self, ev: Eviction, planner) -> list[int]:
+    def seal_row(self, ev: Eviction, planner=None) -> list[int]:
         """Device row (slot, block, group, fill, bits, mask) sealing ``ev``."""
-        self.sealed_groups += 1
-        bits = int(self.tag_h[ev.block]) or 2
-        mask = planner.sealed.get(ev.block, 1 << ev.group)
-        return [ev.slot, ev.block, ev.group, ev.fill, bits, mask]
+        row = np.zeros(6, np.int64)
+        e = np.array([ev.slot, ev.block, ev.group, ev.fill], np.int64)
+        if _host.lib().ekh_pool_seal_row(self._h, _host.i64p(e), _host.i64p(row)) != _host.OK:
+            raise ValueError(f"eviction of block {ev.block} is outside this pool")
+        return row.tolist()
 
     def majority_tier(self) -> int:
         """The tier most of the opened blocks are stored at (4 when nothing is open)."""
@@ -298,7 +294,7 @@ class TieredKVCache:
 
     @property
     def pool_free(self) -> int:
-        return len(self.pool.free)
+        return int(self.pool._counters()[21])
 
     @property
     def residual_free(self) -> int:

@@ -1,36 +1,39 @@
 """Host planning of one engine step's KV writes, shared by every layer.
 
 Interface of ``echokv_vllm/write_plan.py`` (``Eviction`` 28-33, ``WritePlan``
-40-74, ``WritePlanner.plan`` 98-240, ``SharedState`` 243-271, ``WriteMeta``
-274-282, ``stage_plan`` 285-315). Everything a write decides without looking
-at tensor values is computed here from the slot mapping, once per step, as
-numpy arrays indexed by token row:
+40-74, ``WritePlanner`` 77-240, ``SharedState`` 243-271, ``WriteMeta`` 274-282,
+``stage_plan`` 285-315). The planning runs in native code
+(``echokv_amd/host/plan.cpp`` through ``libechokv_host.so``): from the step's slot
+mapping it decides, without looking at tensor values,
 
-* blocks (re)opened this step (a write at offset 0);
-* K groups that complete this step (one ``fin`` row each, naming the token
-  row of every position, or -1 where the key is already in the residual);
-* keys of still-open groups, which go to a residual slot; a slot is taken
-  from a LIFO free list, and when none is free the least recently written
-  unprotected slot is evicted (its group is *sealed*: quantized with the
-  tokens present, later tokens reuse those stats);
-* the K_ref ring row of the step's last ``kref_window`` keys.
+* which blocks (re)open (a write at offset 0);
+* which K groups complete (one ``fin`` row each: the token row of every position,
+  or -1 where the key already sits in the residual);
+* which keys of still-open groups go to a residual slot, evicting (sealing) the
+  least recently written unprotected slot when none is free;
+* where the step's last ``kref_window`` keys land in the K_ref ring;
 
-The device only ever sees ``WriteMeta`` (the write kernels' input contract)
-and index updates, so a captured HIP graph replays the step unchanged.
+and writes the result as the int64 image the device reads, so staging a plan is
+one pinned host-to-device copy. This module wraps the native objects with the
+reference's classes and attribute names.
 """
 
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass, field
 
 import numpy as np
 import torch
 
+from echokv_amd import _host
 from echokv_amd._util import to_device
 
 
 @dataclass
 class Eviction:
+    """A residual slot evicted this step: its group is sealed with ``fill`` tokens."""
+
     slot: int
     block: int
     group: int
@@ -43,12 +46,12 @@ def _none() -> np.ndarray:
 
 @dataclass
 class WritePlan:
-    """One step's writes as host arrays (``write_plan.py:40-74``).
+    """One step's writes as host arrays (views into ``stage``, the device image).
 
-    Per token row: ``tok_slot`` (-1 = no write), ``tok_res`` (residual slot
-    or -1), ``tok_sealed`` (1 = quantize the key under the group's stored
-    stats), ``tok_kref`` (K_ref row or -1). ``fin [f, 3 + k_group]``:
-    ``[block, group, residual slot or -1, token row per position (-1 = residual)]``.
+    Per token row: ``tok_slot`` (-1 = no write), ``tok_res`` (residual slot or
+    -1), ``tok_sealed`` (1 = quantize the key under the group's stored stats),
+    ``tok_kref`` (K_ref row or -1). ``fin [f, 3 + k_group]``: ``[block, group,
+    residual slot or -1, token row per position (-1 = residual)]``.
     """
 
     step: int
@@ -69,6 +72,8 @@ class WritePlan:
     res_group_value: np.ndarray = field(default_factory=_none)
     block_size: int = 0
     k_group: int = 0
+    stage: np.ndarray = field(default_factory=_none)  # [n_fin | tok | fin | residual map | residual groups]
+    touched: np.ndarray = field(default_factory=lambda: np.zeros((0, 3), np.int64))
 
     @property
     def n_fin(self) -> int:
@@ -76,196 +81,118 @@ class WritePlan:
 
 
 class WritePlanner:
-    """Residual-slot allocator and K_ref cursor of one KV cache group."""
+    """Residual-slot allocator and K_ref cursor of one KV cache group.
 
-    def __init__(self, block_size: int, k_group: int, residual_slots: int, kref_window: int = 64) -> None:
+    ``num_blocks`` fixes the per-block arrays (as ``SharedState`` does); without it
+    they grow with the slots seen, as a standalone planner needs."""
+
+    def __init__(self, block_size: int, k_group: int, residual_slots: int, kref_window: int = 64,
+                 num_blocks: int | None = None) -> None:
+        lib = _host.lib()
+        h = lib.ekh_planner_new(num_blocks or 0, block_size, k_group, residual_slots, kref_window)
+        if not h:
+            raise ValueError(f"bad planner shape: block_size {block_size}, k_group {k_group}, "
+                             f"residual_slots {residual_slots}, kref_window {kref_window}")
+        self._h = C.c_void_p(h)
+        self._free_fn = lib.ekh_planner_free
         self.bs = block_size
         self.g = k_group
         self.num_slots = residual_slots
-        # LIFO free list: slot 0 is handed out first, a released slot next.
-        self.free: list[int] = list(range(residual_slots - 1, -1, -1))
-        self.block_slot: dict[int, int] = {}
-        # slot -> [block, group, fill, last step]; insertion order breaks
-        # recency ties when choosing an eviction victim.
-        self.slot_info: dict[int, list[int]] = {}
-        self.sealed: dict[int, int] = {}  # block -> bitmask of sealed groups
-        self.step = 0
         self.kref_window = kref_window
-        self.kref_pos = 0
-        self.kref_fill = 0
 
-    def _release(self, slot: int, res_ops: list) -> None:
-        blk = self.slot_info.pop(slot)[0]
-        self.block_slot.pop(blk, None)
-        self.free.append(slot)
-        res_ops.append((blk, -1))
+    def __del__(self) -> None:
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._free_fn(h)
+            self._h = None
 
-    def _take_slot(self, blk: int, grp: int, protected: set, res_ops: list, grp_ops: list,
-                   evictions: list) -> int:
-        if not self.free:
-            victims = [s for s in self.slot_info if s not in protected]
-            if not victims:
-                raise RuntimeError(f"more than {self.num_slots} open K groups in one step")
-            v = min(victims, key=lambda s: self.slot_info[s][3])
-            vb, vg, vf, _ = self.slot_info[v]
-            evictions.append(Eviction(v, vb, vg, vf))
-            self.sealed[vb] = self.sealed.get(vb, 0) | (1 << vg)
-            self._release(v, res_ops)
-        s = self.free.pop()
-        self.slot_info[s] = [blk, grp, 0, 0]
-        self.block_slot[blk] = s
-        protected.add(s)
-        res_ops.append((blk, s))
-        grp_ops.append((s, grp))
-        return s
+    def _state(self, what: int) -> int:
+        return int(_host.lib().ekh_planner_state(self._h, what))
+
+    @property
+    def step(self) -> int:
+        return self._state(_host.STEP)
+
+    @property
+    def kref_pos(self) -> int:
+        return self._state(_host.KREF_POS)
+
+    @property
+    def kref_fill(self) -> int:
+        return self._state(_host.KREF_FILL)
+
+    @property
+    def free(self) -> list:
+        """The free residual slots, bottom to top (the last is handed out next)."""
+        out = np.zeros(self.num_slots, np.int64)
+        n = _host.lib().ekh_residual_free_list(self._h, _host.i64p(out), out.size)
+        return out[:n].tolist()
+
+    def sealed_mask(self, block: int) -> int:
+        return int(_host.lib().ekh_sealed_mask(self._h, int(block)))
+
+    @property
+    def sealed(self) -> dict:
+        """block -> bitmask of its K groups sealed by an eviction (nonzero entries)."""
+        n = self._state(_host.NUM_BLOCKS)
+        return {b: m for b in range(n) if (m := self.sealed_mask(b))}
 
     def plan(self, slot_mapping_cpu) -> WritePlan:
-        self.step += 1
-        bs, g = self.bs, self.g
-        sm = np.asarray(slot_mapping_cpu.numpy() if torch.is_tensor(slot_mapping_cpu) else slot_mapping_cpu)
-        sm = sm.astype(np.int64).reshape(-1)
-        n_rows = sm.size
-        rows = np.flatnonzero(sm >= 0)
-        slots = sm[rows]
-        n = slots.size
-        blk = slots // bs
-        off = slots % bs
-        grp = off // g
-        pos = off % g
+        sm = slot_mapping_cpu.numpy() if torch.is_tensor(slot_mapping_cpu) else slot_mapping_cpu
+        sm = _host.as_i64(sm)
+        v = _host.PlanView()
+        rc = _host.lib().ekh_plan(self._h, _host.i64p(sm), sm.size, C.byref(v))
+        if rc == _host.ESLOTS:
+            raise RuntimeError(f"more than {self.num_slots} open K groups in one step")
+        if rc != _host.OK:
+            raise ValueError("slot mapping names a block past the planner's pool")
+        return _plan_from_view(v, self.bs, self.g)
 
-        res_ops: list = []  # (block, slot or -1) in order; the last one per block wins
-        grp_ops: list = []  # (slot, group)
-        opened = np.unique(blk[off == 0])
-        for b in opened.tolist():
-            s = self.block_slot.get(b)
-            if s is not None:
-                self._release(s, res_ops)
-            self.sealed.pop(b, None)
 
-        # Tokens grouped by (block, K group), positions ascending inside each.
-        gkey = blk * (bs // g) + grp
-        order = np.lexsort((pos, gkey))
-        if n:
-            sk = gkey[order]
-            starts = np.flatnonzero(np.r_[True, sk[1:] != sk[:-1]])
-        else:
-            starts = _none()
-        counts = np.diff(np.r_[starts, n]).astype(np.int64)
-        first = order[starts]
-        ublk, ugrp = blk[first], grp[first]
-
-        # Whole groups inside this batch (prefill): finalize straight from the
-        # key rows, no residual involved.
-        whole = counts == g
-        if self.sealed:
-            whole &= np.array([not ((self.sealed.get(int(b), 0) >> int(r)) & 1) for b, r in zip(ublk, ugrp)],
-                              dtype=bool)
-        wi = np.flatnonzero(whole)
-        if wi.size:
-            whole_rows = rows[order[starts[wi][:, None] + np.arange(g)]]
-        else:
-            whole_rows = np.zeros((0, g), np.int64)
-        for b in ublk[wi].tolist():  # a group rewritten while its slot was open (rare)
-            s = self.block_slot.get(b)
-            if s is not None and self.slot_info[s][1] in set(ugrp[wi][ublk[wi] == b].tolist()):
-                self._release(s, res_ops)
-
-        tok_res = np.full(n, -1, np.int64)
-        tok_sealed = np.zeros(n, np.int64)
-        fin_head, fin_rows, evictions = [], [], []
-        protected = {self.block_slot[b] for b in np.unique(blk).tolist() if b in self.block_slot}
-        for u in np.flatnonzero(~whole).tolist():
-            idx = order[starts[u] : starts[u] + counts[u]]
-            b, r = int(ublk[u]), int(ugrp[u])
-            p = pos[idx]
-            if (self.sealed.get(b, 0) >> r) & 1:
-                tok_sealed[idx] = 1
-                continue
-            s = self.block_slot.get(b)
-            if s is not None and self.slot_info[s][1] != r:
-                s = None
-            top = int(p.max())
-            if top == g - 1:  # the group completes now
-                fin_head.append((b, r, -1 if s is None else s))
-                rr = np.full(g, -1, np.int64)
-                rr[p] = rows[idx]
-                fin_rows.append(rr)
-                if s is not None:
-                    self._release(s, res_ops)
-                continue
-            if s is None:
-                s = self._take_slot(b, r, protected, res_ops, grp_ops, evictions)
-            tok_res[idx] = s
-            info = self.slot_info[s]
-            info[2] = max(info[2], top + 1)
-            info[3] = self.step
-
-        head = np.concatenate([
-            np.stack([ublk[wi], ugrp[wi], np.full(wi.size, -1, np.int64)], 1).reshape(-1, 3),
-            np.asarray(fin_head, np.int64).reshape(-1, 3),
-        ])
-        body = np.concatenate([whole_rows.reshape(-1, g), np.asarray(fin_rows, np.int64).reshape(-1, g)])
-        fin = np.concatenate([head, body], 1).astype(np.int64)
-
-        # Per touched block: highest offset written + 1, and token count.
-        if n:
-            bsorted = blk[order]
-            bstarts = np.flatnonzero(np.r_[True, bsorted[1:] != bsorted[:-1]])
-            touched = bsorted[bstarts]
-            touched_fill = np.maximum.reduceat(off[order] + 1, bstarts)
-            touched_count = np.diff(np.r_[bstarts, n]).astype(np.int64)
-        else:
-            touched = touched_fill = touched_count = _none()
-
-        # The step's last kref_window keys enter the K_ref ring in order.
-        k = min(n, self.kref_window)
-        kref = np.full(n, -1, np.int64)
-        if k:
-            kref[n - k :] = (self.kref_pos + np.arange(k)) % self.kref_window
-            self.kref_pos = (self.kref_pos + k) % self.kref_window
-            self.kref_fill = min(self.kref_window, self.kref_fill + k)
-
-        def per_row(a):
-            o = np.full(n_rows, -1, np.int64)
-            o[rows] = a
-            return o
-
-        res_map = dict(res_ops)
-        grp_map = dict(grp_ops)
-        return WritePlan(
-            step=self.step, n_rows=n_rows, tok_slot=sm, tok_res=per_row(tok_res),
-            tok_sealed=np.maximum(per_row(tok_sealed), 0), tok_kref=per_row(kref), fin=fin,
-            evictions=evictions, open_np=opened, touched_np=touched, touched_fill=touched_fill,
-            touched_count=touched_count,
-            res_map_block=np.fromiter(res_map.keys(), np.int64, len(res_map)),
-            res_map_value=np.fromiter(res_map.values(), np.int64, len(res_map)),
-            res_group_slot=np.fromiter(grp_map.keys(), np.int64, len(grp_map)),
-            res_group_value=np.fromiter(grp_map.values(), np.int64, len(grp_map)),
-            block_size=bs, k_group=g,
-        )
+def _plan_from_view(v: _host.PlanView, bs: int, g: int) -> WritePlan:
+    stage = _host.copy_i64(v.stage, v.stage_len)
+    t, f, w = v.n_rows, v.n_fin, 3 + g
+    o = 1 + 4 * t
+    tok = stage[1:o].reshape(4, t)
+    fin = stage[o : o + f * w].reshape(f, w)
+    o += f * w
+    maps = []
+    for n in (v.n_res_map, v.n_res_map, v.n_grp_map, v.n_grp_map):
+        maps.append(stage[o : o + n])
+        o += n
+    ev = _host.copy_i64(v.evict, 4 * v.n_evict).reshape(-1, 4)
+    touched = _host.copy_i64(v.touched, 3 * v.n_touched).reshape(-1, 3)
+    return WritePlan(
+        step=int(v.step), n_rows=int(t), tok_slot=tok[0], tok_res=tok[1], tok_sealed=tok[2], tok_kref=tok[3],
+        fin=fin, evictions=[Eviction(*map(int, e)) for e in ev], open_np=_host.copy_i64(v.open, v.n_open),
+        touched_np=touched[:, 0], touched_fill=touched[:, 1], touched_count=touched[:, 2],
+        res_map_block=maps[0], res_map_value=maps[1], res_group_slot=maps[2], res_group_value=maps[3],
+        block_size=bs, k_group=g, stage=stage, touched=touched)
 
 
 class SharedState:
-    """State every layer of one KV cache group shares (``write_plan.py:243-271``):
-    the planner, per-block host bookkeeping, and the device residual map read
-    by the attention kernels."""
+    """What every layer of one KV cache group shares (``write_plan.py:243-271``):
+    the planner, per-block host bookkeeping (``fill_h``, ``last_h``, ``cum_h``:
+    numpy views of the native arrays) and the device residual map read by the
+    attention kernels."""
 
     def __init__(self, num_blocks: int, block_size: int, k_group: int, residual_slots: int,
                  kref_window: int, device) -> None:
         self.num_blocks = num_blocks
-        self.planner = WritePlanner(block_size, k_group, residual_slots, kref_window)
-        self.fill_h = np.zeros(num_blocks, np.int64)
-        self.last_h = np.zeros(num_blocks, np.int64)
-        self.cum_h = np.zeros(num_blocks, np.int64)
+        self.planner = WritePlanner(block_size, k_group, residual_slots, kref_window, num_blocks=num_blocks)
+        lib = _host.lib()
+        self.fill_h, self.last_h, self.cum_h = (
+            _host.view_i64(lib.ekh_block_array(self.planner._h, which), num_blocks, self.planner)
+            for which in (_host.FILL, _host.LAST, _host.CUM))
         self.block_res = torch.full((num_blocks,), -1, dtype=torch.long, device=device)
         self.res_group = torch.zeros(residual_slots + 1, dtype=torch.long, device=device)
 
     def commit(self, plan: WritePlan) -> None:
-        t = plan.touched_np
-        if t.size:
-            self.fill_h[t] = np.maximum(self.fill_h[t], plan.touched_fill)
-            self.last_h[t] = plan.step
-            self.cum_h[t] += plan.touched_count
+        """Record the step's touched blocks (after every layer prepared the step)."""
+        t = np.ascontiguousarray(plan.touched)
+        rc = _host.lib().ekh_commit(self.planner._h, plan.step, _host.i64p(t), t.shape[0])
+        if rc != _host.OK:
+            raise ValueError("plan names a block past this cache group's pool")
 
     def apply_res_map(self, blocks, values, slots, groups) -> None:
         if blocks.numel():
@@ -286,22 +213,25 @@ class WriteMeta:
 
 
 def stage_plan(plan: WritePlan, device, opened=None):
-    """One host-to-device copy of ``plan`` (and of ``opened`` headers): ``(WriteMeta, extra)``
-    with ``extra = (res blocks, res values, group slots, group values, opened ids, headers)``."""
+    """``plan.stage`` (and ``opened`` headers) in one host-to-device copy: returns
+    ``(WriteMeta, (res blocks, res values, group slots, group values, opened ids, headers))``."""
     t, f, w = plan.n_rows, plan.n_fin, 3 + plan.k_group
-    parts = [np.array([f]), plan.tok_slot, plan.tok_res, plan.tok_sealed, plan.tok_kref, plan.fin,
-             plan.res_map_block, plan.res_map_value, plan.res_group_slot, plan.res_group_value]
+    image = plan.stage
+    n_open = 0
     if opened is not None:
-        parts += [opened[0], np.ascontiguousarray(opened[1]).view(np.int64)]
-    flat = [np.asarray(p, dtype=np.int64).reshape(-1) for p in parts]
-    dev = to_device(torch.from_numpy(np.concatenate(flat)), device)
-    views, o = [], 0
-    for a in flat:
-        views.append(dev[o : o + a.size])
-        o += a.size
-    meta = WriteMeta(tok=dev[1 : 1 + 4 * t].view(4, t), fin=views[5].view(f, w), fin_count=views[0],
-                     n_rows=t, n_fin=f)
+        ids = _host.as_i64(opened[0])
+        n_open = ids.size
+        image = np.concatenate([image, ids, np.ascontiguousarray(opened[1]).view(np.int64).reshape(-1)])
+    dev = to_device(torch.from_numpy(image), device)
+    o = 1 + 4 * t
+    meta = WriteMeta(tok=dev[1:o].view(4, t), fin=dev[o : o + f * w].view(f, w), fin_count=dev[0:1], n_rows=t,
+                     n_fin=f)
+    o += f * w
+    maps = []
+    for n in (plan.res_map_block.size, plan.res_map_value.size, plan.res_group_slot.size, plan.res_group_value.size):
+        maps.append(dev[o : o + n])
+        o += n
     headers = (None, None)
     if opened is not None:
-        headers = (views[10], views[11].view(-1, 2).view(torch.uint8))
-    return meta, (*views[6:10], *headers)
+        headers = (dev[o : o + n_open], dev[o + n_open : o + 3 * n_open].view(-1, 2).view(torch.uint8))
+    return meta, (*maps, *headers)
