@@ -62,7 +62,8 @@ _SIGS = {
     "echokv_prefill_dense": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, P, I64, I32, P, I64,
                              P, I64, FL, P],
     "echokv_dequant_dense": [LP, P, P, P, RP, P, I64, P, I64, P, P, I64, I64, I32, P],
-    "echokv_canary_kl": [P, I32, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32, I32, I32, I32, I32, I32, FL, P, P],
+    "echokv_canary_kl": [P, I32, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32, I32, I32, I32, I32, I32, FL, P, P,
+                         P],
 }
 
 _lib = None

@@ -331,22 +331,23 @@ int echokv_dequant_dense(const echokv_layout* L, const uint8_t* pages, const int
 int echokv_canary_kl(const void* query, int32_t q_dtype, int64_t q_sl, int64_t q_s0, int64_t q_s1, const float* kref,
                      int64_t k_sl, int64_t k_s0, int64_t k_s1, int32_t num_layers, int32_t nq, int32_t num_q_heads,
                      int32_t num_kv_heads, int32_t head_size, int32_t window, int32_t nbits, int32_t bits_packed,
-                     int32_t k_group, float softmax_scale, float* out, echokv_stream_t stream) {
+                     int32_t k_group, float softmax_scale, float* partial, float* out, echokv_stream_t stream) {
   if (!dtype_ok(q_dtype)) return ECHOKV_EDTYPE;
-  if (num_layers < 0 || nq < 1 || num_kv_heads < 1 || num_q_heads % num_kv_heads || k_group < 1) return ECHOKV_EINVAL;
-  // Only the last floor(window / k_group) * k_group keys are scored and staged.
-  if (head_size < 1 || head_size > ek::kCanaryMaxD || window < k_group ||
-      (window / k_group) * k_group > ek::kCanaryMaxKeys)
-    return ECHOKV_ESHAPE;
+  if (num_layers < 0 || nq < 1 || num_kv_heads < 1 || num_q_heads < 1 || num_q_heads % num_kv_heads || k_group < 1)
+    return ECHOKV_EINVAL;
   if (nbits < 1 || nbits > ek::kCanaryMaxTiers) return ECHOKV_EINVAL;
   for (int t = 0; t < nbits; ++t) {
     const int b = (bits_packed >> (8 * t)) & 0xff;
     if (b != 2 && b != 4 && b != 8) return ECHOKV_EINVAL;
   }
+  // Only the last floor(window / k_group) * k_group keys are scored.
+  if (head_size < 1 || head_size > ek::kCanaryMaxD || window < k_group) return ECHOKV_ESHAPE;
+  const int rows = (num_q_heads / num_kv_heads) * nq;  // query rows one workgroup scores
+  if (ek::canary_lds_bytes(head_size, nbits, rows) > ek::kLdsBytes) return ECHOKV_ESHAPE;
   if (num_layers == 0) return ECHOKV_OK;
-  if (!query || !kref || !out) return ECHOKV_EINVAL;
+  if (!query || !kref || !partial || !out) return ECHOKV_EINVAL;
   ek::CanaryArgs a{query, q_dtype, q_sl, q_s0, q_s1, kref, k_sl, k_s0, k_s1, nq, num_q_heads, num_kv_heads,
-                   head_size, window, nbits, bits_packed, k_group, softmax_scale, out};
+                   head_size, window, nbits, bits_packed, k_group, softmax_scale, partial, out};
   return launched(ek::launch_canary(a, num_layers, (hipStream_t)stream));
 }
 

@@ -8,9 +8,9 @@
 namespace ek {
 
 constexpr int kThreads = 256;        // store / dequant kernels
-constexpr int kCanaryMaxKeys = 64;   // canary: keys staged in LDS per KV head
 constexpr int kCanaryMaxTiers = 3;
-constexpr int kCanaryMaxD = 128;
+constexpr int kCanaryMaxD = 256;
+constexpr size_t kLdsBytes = 160 * 1024;  // LDS per CU on gfx950
 constexpr int kPrefillRows = 128;    // prefill: query rows (tokens x GQA heads) per workgroup
 
 // Query tokens per prefill tile for a GQA group size.
@@ -137,6 +137,7 @@ struct CanaryArgs {
   long k_sl, k_s0, k_s1;
   int nq, hq, h, d, window, nbits, bits_packed, kg;
   float scale;
+  float* partial;  // [layers, H, nbits]: KL sums of each (layer, KV head)
   float* out;
 };
 
@@ -212,6 +213,7 @@ hipError_t launch_dequant_dense(const DenseArgs& a, long n, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s);
 hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s);
 hipError_t launch_canary(const CanaryArgs& a, int num_layers, hipStream_t s);
+size_t canary_lds_bytes(int d, int nbits, int rows);  // one canary workgroup's LDS
 hipError_t launch_prefill(const PrefillArgs& a, long n_tiles, hipStream_t s);
 hipError_t launch_prefill_pack(const PackArgs& a, long n_packs, hipStream_t s);
 hipError_t launch_prefill_flash(const FlashArgs& a, hipStream_t s);

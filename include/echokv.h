@@ -177,16 +177,17 @@ int echokv_dequant_dense(const echokv_layout* L, const uint8_t* pages, const int
 
 /* Canary: for each layer and tier bits[j], the mean over query rows and heads of
  * KL(softmax(q K~ᵀ s) || softmax(q K_refᵀ s)), K~ = per-channel storage round trip
- * of the last floor(window/k_group)*k_group keys; clamped >= 0.
+ * of the last floor(window/k_group)*k_group keys; clamped >= 0. Any window length.
  * query [L, nq, Hq, D] (strides q_sl, q_s0, q_s1), kref f32 [L, window, H, D]
  * oldest first (strides k_sl, k_s0, k_s1) -> out f32 [L, nbits]; tier j is byte j of
- * bits_packed (each 2, 4 or 8).
+ * bits_packed (each 2, 4 or 8). partial: f32 workspace [L, H, nbits] (the KL sums of
+ * each layer's KV heads, added in head order). D <= 256.
  * Replaces echokv_vllm/canary.py:59-89 (canary_kl). */
 int echokv_canary_kl(const void* query, int32_t q_dtype, int64_t q_sl, int64_t q_s0, int64_t q_s1,
                      const float* kref, int64_t k_sl, int64_t k_s0, int64_t k_s1,
                      int32_t num_layers, int32_t nq, int32_t num_q_heads, int32_t num_kv_heads,
                      int32_t head_size, int32_t window, int32_t nbits, int32_t bits_packed, int32_t k_group,
-                     float softmax_scale, float* out, echokv_stream_t stream);
+                     float softmax_scale, float* partial, float* out, echokv_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -49,3 +49,23 @@ def test_canary_head_size_not_multiple_of_16(device, d):
     kref = rng.standard_normal((2, 48, 2, d)).astype(np.float32)  # [layers, W, H, D]
     got = canary_kl(torch.from_numpy(q).to(device), torch.from_numpy(kref).to(device), (2, 4, 8), 16, d ** -0.5)
     _close(got, OC.canary_kl(q, kref, (2, 4, 8), 16, d ** -0.5))
+
+
+@pytest.mark.parametrize("window,kg,d,hq,h,nq", [
+    (200, 16, 128, 32, 8, 8),    # three 64-key chunks and a partial one
+    (100, 32, 128, 64, 8, 8),    # oldest 4 keys dropped; 64 query rows per workgroup
+    (256, 128, 128, 8, 2, 4),    # K groups longer than a chunk: stats from memory
+    (96, 16, 256, 16, 4, 2),     # head size 256: 32-key chunks
+    (64, 64, 64, 4, 4, 8),       # one group, GQA 1
+])
+def test_canary_windows_beyond_one_chunk(device, window, kg, d, hq, h, nq):
+    rng = np.random.default_rng(window + kg + d)
+    layers = 3
+    q = rng.standard_normal((layers, nq, hq, d)).astype(np.float32)
+    kref = (rng.standard_normal((layers, window, h, d)) * 2).astype(np.float32)
+    got = canary_kl(torch.from_numpy(q).to(device), torch.from_numpy(kref).to(device), (2, 4, 8), kg, d ** -0.5)
+    ref = OC.canary_kl(q, kref, (2, 4, 8), kg, d ** -0.5)
+    print(f"[canary W{window} KG{kg} D{d}] max rel err {float(np.abs(got.cpu().numpy() / ref - 1).max()):.2e}",
+          flush=True)
+    _close(got, ref)
+    assert (ref[:, 0] > ref[:, 1]).all() and (ref[:, 1] > ref[:, 2]).all()
