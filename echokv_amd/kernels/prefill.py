@@ -153,9 +153,12 @@ def use_dense(prefill, head_size: int) -> bool:
 
 
 def prefill_attention_dense(store, query: torch.Tensor, output: torch.Tensor, prefill, req_of,
-                            block_table: torch.Tensor, softmax_scale: float, plan: DensePlan | None = None) -> None:
+                            block_table: torch.Tensor, softmax_scale: float, plan: DensePlan | None = None,
+                            workspace: torch.Tensor | None = None) -> None:
     """Two-pass prefill (echokv_vllm/kernels/prefill.py:133-167): dequantize each
-    context once into a workspace of 64-key tiles, then flash attention over it."""
+    context once into a workspace of 64-key tiles, then flash attention over it.
+    ``plan`` / ``workspace`` (uint8, ``dense_workspace_bytes``) may be built once per
+    step and shared by every layer."""
     if not prefill:
         return
     L = store.layout
@@ -173,7 +176,11 @@ def prefill_attention_dense(store, query: torch.Tensor, output: torch.Tensor, pr
     block_table = _bt(block_table)
     n_packs = plan.packs.shape[0]
     ws_bytes = dense_workspace_bytes(store, n_packs)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=query.device)
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=query.device)
+    elif workspace.dtype != torch.uint8 or workspace.numel() < ws_bytes:
+        raise ValueError(f"prefill workspace holds {workspace.numel()} bytes, the plan needs {ws_bytes}")
+    ws = workspace
     res = _lib.residual(store.res_k)
     _lib.call(
         "echokv_prefill_dense", _lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(store.block_res),
@@ -189,14 +196,17 @@ def prefill_attention(store, query: torch.Tensor, output: torch.Tensor, prefill,
     """Write attention for every prefill chunk into ``output [T, Hq, D]``.
 
     A batch with a chunk longer than ``FUSED_MAX_CHUNK`` takes the two-pass
-    path (``dense`` may carry its prebuilt ``DensePlan``); otherwise the fused
-    kernel over ``tiles``. ``gather`` (the reference's PyTorch-path index) is
-    accepted and unused."""
+    path; ``dense`` carries its step-wide inputs, built once for every layer: a
+    ``DensePlan`` or ``(DensePlan, workspace)`` (the reference builder's dense
+    tuple has the same role). Otherwise the fused kernel over ``tiles``.
+    ``gather`` (the reference's PyTorch-path index) is accepted and unused."""
     if not prefill:
         return
     if use_dense(prefill, store.layout.head_size):
-        prefill_attention_dense(store, query, output, prefill, req_of, block_table, softmax_scale,
-                                dense if isinstance(dense, DensePlan) else None)
+        plan, ws = (dense, None) if isinstance(dense, DensePlan) else (dense or (None, None))
+        if plan is not None and not isinstance(plan, DensePlan):
+            raise ValueError("dense must be a DensePlan or a (DensePlan, workspace) pair")
+        prefill_attention_dense(store, query, output, prefill, req_of, block_table, softmax_scale, plan, ws)
     else:
         prefill_attention_fused(store, query, output, prefill, req_of, block_table, softmax_scale, tiles)
 

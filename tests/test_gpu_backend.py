@@ -1,0 +1,246 @@
+"""GPU: the vLLM backend driven through a serving sequence with fake vLLM
+objects (as tests/echokv_vllm/test_vllm_e2e.py drives the real engine): 3 layers
+whose caches are views of one layer-interleaved pool, a chunked prefill (long
+and short chunks), eager decode steps, then decode steps replayed from one
+captured HIP graph, with the canary firing. Every layer's attention output is
+checked against the float64 oracle over that layer's own page bytes, and the
+canary's δ̂ against the oracle canary on the rows it stashed."""
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from echokv_amd import _vllm
+from echokv_amd.backend import EchoKVAttentionImpl, EchoKVMetadataBuilder
+from echokv_amd.controller import SUPPORTED_BITS
+from echokv_amd.tiered_cache import TieredLayout
+from oracle import attention as OA
+from oracle import canary as OC
+from oracle import store as OS
+
+pytestmark = pytest.mark.gpu
+
+H, HQ, D, BS, KG, LAYERS = 8, 32, 128, 16, 16, 3
+PROMPTS = [40, 150, 17, 300]
+TOL = 2e-3
+
+
+def oracle_of(impl):
+    st = impl.store
+    L = st.layout
+    OL = OS.Layout(L.num_kv_heads, L.head_size, L.block_size, L.mem_bits, L.k_group, L.v_group)
+    return OS.PageStore.over(OL, st.pages.cpu().numpy(), st.res_k.float().cpu().numpy(), st.block_res.cpu().numpy(),
+                             st.res_group.cpu().numpy())
+
+
+@pytest.fixture
+def env(monkeypatch):
+    for k, v in {"ECHOKV_K_GROUP": "16", "ECHOKV_MEM_BITS": "8", "ECHOKV_CANARY_INTERVAL": "2",
+                 "ECHOKV_KREF_WINDOW": "32", "ECHOKV_RESIDUAL_SLOTS": "24"}.items():
+        monkeypatch.setenv(k, v)
+    yield
+    _vllm.set_forward_metadata(None)
+
+
+def make_engine(device, tiers):
+    per_token = TieredLayout.per_token_bytes(H, D, 8, KG, 32)
+    num_blocks = 128
+    pool = torch.zeros(num_blocks, LAYERS, BS, per_token, dtype=torch.uint8, device=device)
+    layers = []
+    for li in range(LAYERS):
+        impl = EchoKVAttentionImpl(HQ, D, D ** -0.5, H)
+        # vLLM builds layers under the model's dtype (fp16 here): residual and stash follow it.
+        impl.residual, impl.stash = impl.residual.half(), impl.stash.half()
+        impl.controller.bits = tiers[li]
+        layers.append(SimpleNamespace(kv_cache=pool[:, li : li + 1], impl=impl, layer_name=f"model.layers.{li}.attn"))
+    cfg = SimpleNamespace(
+        model_config=SimpleNamespace(max_model_len=2048, dtype=torch.float16,
+                                     get_num_attention_heads=lambda pc: HQ),
+        parallel_config=None, scheduler_config=SimpleNamespace(max_num_seqs=8),
+        compilation_config=SimpleNamespace(max_cudagraph_capture_size=16), speculative_config=None)
+    spec = SimpleNamespace(block_size=BS, num_kv_heads=H, head_size=D)
+    builder = EchoKVMetadataBuilder(spec, [l.layer_name for l in layers], cfg, device)
+    builder.bind_layers(layers)
+    return builder, layers, pool
+
+
+class CanaryCheck:
+    """Snapshot what a fire step stashed (query rows, K_ref ring in ring order), then
+    check the δ̂ the next build computed from it against the oracle canary."""
+
+    def __init__(self, builder, layers):
+        self.builder, self.layers = builder, layers
+        self.snap = None
+        self.checked = 0
+
+    def after_step(self, md):
+        if not md.fire:
+            return
+        torch.cuda.synchronize()
+        pl = self.builder.shared.planner
+        k = self.builder.measured[0]
+        self.snap = []
+        for l in self.layers:
+            ring = l.impl.kref_buf.cpu().numpy()
+            order = (np.arange(pl.kref_fill) + pl.kref_pos - pl.kref_fill) % ring.shape[0]
+            self.snap.append((l.impl.stash[:k].float().cpu().numpy(), ring[order]))
+
+    def after_build(self):
+        if self.snap is None or self.builder.pending is None:
+            return
+        deltas = self.builder.pending[0].cpu().numpy()
+        for li, (q, ring) in enumerate(self.snap):
+            ref = OC.canary_kl(q, ring, SUPPORTED_BITS, KG, D ** -0.5)
+            np.testing.assert_allclose(deltas[li], ref, rtol=2e-3, atol=2e-6)
+        print(f"[backend canary] delta = {deltas[0].round(6).tolist()} (layer 0) matches the oracle", flush=True)
+        self.snap = None
+        self.checked += 1
+
+
+class Batch:
+    """The step's CommonAttentionMetadata (the fields the builder reads)."""
+
+    def __init__(self, device, table, starts, lens, slots, n_tokens):
+        self.num_reqs = len(lens)
+        self.num_actual_tokens = n_tokens
+        self.query_start_loc_cpu = torch.tensor(starts, dtype=torch.int32)
+        self.seq_lens = torch.tensor(lens, dtype=torch.int32, device=device)
+        self.seq_lens_cpu_upper_bound = None  # not a known vLLM table: the builder copies the device mapping
+        self.slot_mapping = torch.tensor(slots, dtype=torch.int64, device=device)
+        self.block_table_tensor = table
+        self.causal = True
+        self.req_idx = None
+
+
+def slots_for(table_np, lens_before, counts):
+    out = []
+    for r, (p0, n) in enumerate(zip(lens_before, counts)):
+        pos = np.arange(p0, p0 + n)
+        out.append(table_np[r][pos // BS] * BS + pos % BS)
+    return np.concatenate(out)
+
+
+def run_layers(layers, md, q, k, v):
+    _vllm.set_forward_metadata(md)
+    outs = []
+    for li, layer in enumerate(layers):
+        out = torch.zeros(q[li].shape[0], HQ * D, device=q[li].device, dtype=torch.float16)
+        layer.impl.do_kv_cache_update(layer, k[li], v[li], layer.kv_cache, md.slot_mapping)
+        layer.impl.forward(layer, q[li], k[li], v[li], layer.kv_cache, md, out)
+        outs.append(out)
+    return outs
+
+
+def fp16_err(got, ref) -> float:
+    """The error of an fp16 output beyond its own rounding: max over elements of
+    |got - ref| minus half the fp16 spacing at ref (the float64 oracle value), so a
+    value stored as the fp16 neighbour of an exact result is not counted against
+    the kernel, and anything more is."""
+    ref = np.asarray(ref, np.float64)
+    g = got.detach().float().cpu().numpy().astype(np.float64)
+    half_ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) / 2
+    return float((np.abs(g - ref) - half_ulp).max())
+
+
+def check_decode(layers, table_np, lens, q, outs, label):
+    worst = 0.0
+    for li, layer in enumerate(layers):
+        ps = oracle_of(layer.impl)
+        n = len(lens)
+        ref = OA.decode_attention(ps, q[li][:n].float().cpu().numpy(), table_np, np.asarray(lens), D ** -0.5,
+                                  vectorized=True)
+        worst = max(worst, fp16_err(outs[li].view(-1, HQ, D)[:n], ref))
+    print(f"[backend {label}] max err {worst:.3e}", flush=True)
+    assert worst <= TOL, f"{label}: {worst}"
+
+
+def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
+    rng = np.random.default_rng(12)
+    builder, layers, pool = make_engine(device, tiers=[4, 8, 2])
+    nreq = len(PROMPTS)
+    table_np = rng.permutation(128)[: nreq * 32].reshape(nreq, 32).astype(np.int64)
+    table = torch.from_numpy(table_np).to(device, torch.int32)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(5)
+
+    def rand(n, heads):
+        return [torch.randn(n, heads, D, device=device, generator=gen).half() for _ in range(LAYERS)]
+
+    # Step 1: the prompts as one chunked-prefill batch (long and short chunks).
+    starts = np.concatenate([[0], np.cumsum(PROMPTS)])
+    slots = slots_for(table_np, [0] * nreq, PROMPTS)
+    md = builder.build(0, Batch(device, table, starts, PROMPTS, slots, int(starts[-1])))
+    assert md.prefill and md.prefill_dense is not None and md.decode_rows is None
+    q, k, v = rand(int(starts[-1]), HQ), rand(int(starts[-1]), H), rand(int(starts[-1]), H)
+    outs = run_layers(layers, md, q, k, v)
+    torch.cuda.synchronize()
+    worst = 0.0
+    for li, layer in enumerate(layers):
+        ps = oracle_of(layer.impl)
+        ref = OA.prefill_attention(ps, q[li].float().cpu().numpy(), md.prefill, md.prefill_reqs, table_np,
+                                   D ** -0.5, vectorized=True)
+        worst = max(worst, fp16_err(outs[li].view(-1, HQ, D), ref))
+        assert int(layer.impl.store.tag[table_np[1, 0]]) == layer.impl.controller.bits
+    print(f"[backend prefill] max err {worst:.3e}", flush=True)
+    assert worst <= TOL
+
+    lens = list(PROMPTS)
+    pad = 6  # a graph batch: 4 live requests + 2 padding rows
+
+    # One block table for every decode step (as vLLM keeps its tables in fixed
+    # buffers): a captured graph reads the table at the address it was captured with.
+    bt = torch.cat([table, torch.zeros(pad - nreq, table.shape[1], dtype=table.dtype, device=device)])
+
+    def decode_batch():
+        slots = np.concatenate([slots_for(table_np, lens, [1] * nreq), -np.ones(pad - nreq, np.int64)])
+        new_lens = [x + 1 for x in lens] + [0] * (pad - nreq)
+        starts = np.arange(pad + 1)
+        return Batch(device, bt, starts, new_lens, slots, pad), new_lens[:nreq]
+
+    canary = CanaryCheck(builder, layers)
+
+    # Steps 2-3: eager decode.
+    for step in range(2):
+        cm, new_lens = decode_batch()
+        md = builder.build(0, cm)
+        canary.after_build()
+        assert md.decode_rows is not None and md.decode_lens.shape[0] == pad and not md.prefill
+        q, k, v = rand(pad, HQ), rand(pad, H), rand(pad, H)
+        outs = run_layers(layers, md, q, k, v)
+        torch.cuda.synchronize()
+        canary.after_step(md)
+        lens = new_lens
+        check_decode(layers, table_np, lens, q, outs, f"eager decode {step}")
+
+    # Steps 4-9: one graph captured at the decode shape, replayed with fresh metadata.
+    sq, sk, sv = rand(pad, HQ), rand(pad, H), rand(pad, H)
+    souts = [torch.zeros(pad, HQ * D, device=device, dtype=torch.float16) for _ in range(LAYERS)]
+    cm, new_lens = decode_batch()
+    md = builder.build(0, cm)
+    canary.after_build()
+    _vllm.set_forward_metadata(md)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for li, layer in enumerate(layers):
+            layer.impl.do_kv_cache_update(layer, sk[li], sv[li], layer.kv_cache, md.slot_mapping)
+            layer.impl.forward(layer, sq[li], sk[li], sv[li], layer.kv_cache, md, souts[li])
+    for step in range(6):
+        if step:
+            cm, new_lens = decode_batch()
+            md = builder.build(0, cm)
+            canary.after_build()
+        for li in range(LAYERS):
+            sq[li].copy_(torch.randn(pad, HQ, D, device=device, generator=gen).half())
+            sk[li].copy_(torch.randn(pad, H, D, device=device, generator=gen).half())
+            sv[li].copy_(torch.randn(pad, H, D, device=device, generator=gen).half())
+        graph.replay()
+        torch.cuda.synchronize()
+        canary.after_step(md)
+        lens = new_lens
+        check_decode(layers, table_np, lens, sq, souts, f"graph decode {step}")
+    assert canary.checked >= 2, "the canary fired and was scored, eagerly and from graph-replayed steps"
+    assert all(l.impl.controller.fires >= 1 for l in layers), "every controller observed a δ̂"
+    for layer in layers:
+        assert layer.impl.forward_calls == 4  # prefill, 2 eager decodes, the captured call; replays stay in the graph
