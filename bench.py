@@ -136,6 +136,7 @@ def run(args) -> dict:
     ws = (torch.empty(S, HQ, num_splits, D, device=dev), torch.empty(S, HQ, num_splits, 2, device=dev))
     int4 = [li for li in range(LAYERS) if tiers[li] == 4]
     scale = D ** -0.5
+    inv = args.schedule == "split"
 
     def step(i):
         pos = ctx - 1 + i  # position of this step's new token
@@ -152,7 +153,7 @@ def run(args) -> dict:
                 s.write_headers(to_device(torch.from_numpy(opened[li][0]), dev), to_device(torch.from_numpy(opened[li][1]), dev))
             s.apply(meta, kn[li], vn[li], krefs[li])
             decode_attention(s, q[li], table_d, lens_d, scale, blocks_per_split=args.bps, out=out[li],
-                             num_splits=num_splits, workspace=ws, tier=int(tiers[li]))
+                             num_splits=num_splits, workspace=ws, tier=int(tiers[li]), batch_invariant=inv)
         return lens
 
     # End to end, eager: the host plans every step; all 32 layers write and attend.
@@ -180,7 +181,7 @@ def run(args) -> dict:
         for li, s in enumerate(stores):
             s.apply(gmeta, kn[li], vn[li], krefs[li], capturing=True)
             decode_attention(s, q[li], table_d, lens_buf, scale, blocks_per_split=args.bps, out=out[li],
-                             num_splits=num_splits, workspace=ws, tier=int(tiers[li]))
+                             num_splits=num_splits, workspace=ws, tier=int(tiers[li]), batch_invariant=inv)
 
     all_layers()  # warm-up with nothing staged: no row written, every length 0
     torch.cuda.synchronize()
@@ -225,7 +226,7 @@ def run(args) -> dict:
     def int4_decode():
         for li in int4:
             decode_attention(stores[li], q[li], table_d, lens_d, scale, blocks_per_split=args.bps, out=out[li],
-                             num_splits=num_splits, workspace=ws, tier=4)
+                             num_splits=num_splits, workspace=ws, tier=4, batch_invariant=inv)
 
     int4_decode()
     torch.cuda.synchronize()
@@ -555,6 +556,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--bps", type=int, default=16, help="blocks per decode split")
     ap.add_argument("--max-splits", type=int, default=64, help="cap on decode splits per sequence")
+    ap.add_argument("--schedule", choices=("balanced", "split"), default="balanced",
+                    help="decode schedule: the batch's blocks spread evenly over the GPU's workgroups, "
+                         "or each sequence split by its own length (batch-invariant)")
     ap.add_argument("--reps", type=int, default=50, help="graph replays of the 16 INT4 layers' decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill measurement")

@@ -18,6 +18,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "libechokv.so"
 
 F32, F16, BF16 = 0, 1, 2
+DECODE_BATCH_INVARIANT = 1
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTS = (
@@ -54,10 +55,10 @@ _SIGS = {
     "echokv_seal_groups": [LP, P, P, I64, RP, P],
     "echokv_gather": [LP, P, P, P, RP, P, P, I64, P, P, P],
     "echokv_store_blocks": [LP, P, P, I64, P, P, I32, P],
-    "echokv_decode": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, P, P, P, I64,
-                      I64, I32, P],
-    "echokv_decode_static": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, P, I64,
-                             I64, I32, P],
+    "echokv_decode": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, I32, P, P, P,
+                      I64, I64, I32, P],
+    "echokv_decode_static": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, I32, P,
+                             I64, I64, I32, P],
     "echokv_prefill": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, I32, P, I64, FL, P],
     "echokv_prefill_dense": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, P, I64, I32, P, I64,
                              P, I64, FL, P],

@@ -133,8 +133,8 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
                const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
                int32_t num_q_heads, const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
                const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs, float softmax_scale,
-               int32_t num_splits, int32_t blocks_per_split, int32_t tier, float* acc, float* ml, bool static_scratch,
-               void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
+               int32_t num_splits, int32_t blocks_per_split, int32_t tier, int32_t flags, float* acc, float* ml,
+               bool static_scratch, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;
   if (L->head_size != 64 && L->head_size != 128) return ECHOKV_ESHAPE;
   if (L->v_group % (L->head_size / 16)) return ECHOKV_ESHAPE;
@@ -146,6 +146,7 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
   if (num_seqs < 0 || num_splits <= 0 || blocks_per_split <= 0 || !res_ok(res)) return ECHOKV_EINVAL;
   if (tier != 2 && tier != 4 && tier != 8) return ECHOKV_EINVAL;
+  if (flags & ~ECHOKV_DECODE_BATCH_INVARIANT) return ECHOKV_EINVAL;
   if (num_seqs == 0) return ECHOKV_OK;
   if (!pages || !block_res || !res_group || !query || !block_table || !seq_lens || !out) return ECHOKV_EINVAL;
   if (!static_scratch && (!acc || !ml)) return ECHOKV_EINVAL;
@@ -191,8 +192,15 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   }
   a.acc = acc;
   a.ml = ml;
+  a.out = out;
+  a.o_s0 = o_s0;
+  a.o_s1 = o_s1;
+  a.out_dtype = out_dtype;
+  a.ranges = 0;
+  if (!(flags & ECHOKV_DECODE_BATCH_INVARIANT) && ek::decode_ranges(a, a.ranges) != hipSuccess) return ECHOKV_ELAUNCH;
   hipError_t e = ek::launch_decode(a, num_seqs, (hipStream_t)stream);
   if (e != hipSuccess) return ECHOKV_ELAUNCH;
+  if (a.ranges > 0) return launched(ek::launch_merge_balanced(a, (hipStream_t)stream));
   ek::MergeArgs m{acc, ml, seq_lens, q_rows, out, o_s0, o_s1, out_dtype, num_q_heads, L->head_size,
                   L->block_size, num_splits, blocks_per_split, num_seqs * num_q_heads};
   return launched(ek::launch_merge(m, num_seqs, (hipStream_t)stream));
@@ -206,11 +214,11 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
                   const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
                   int32_t num_q_heads, const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
                   const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs, float softmax_scale,
-                  int32_t num_splits, int32_t blocks_per_split, int32_t tier, float* acc, float* ml, void* out,
-                  int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
+                  int32_t num_splits, int32_t blocks_per_split, int32_t tier, int32_t flags, float* acc, float* ml,
+                  void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
   return decode_run(L, pages, block_res, res_group, res, query, q_s0, q_s1, q_dtype, num_q_heads, q_rows,
                     block_table, bt_s0, bt_rows, seq_lens, num_seqs, softmax_scale, num_splits, blocks_per_split,
-                    tier, acc, ml, false, out, o_s0, o_s1, out_dtype, stream);
+                    tier, flags, acc, ml, false, out, o_s0, o_s1, out_dtype, stream);
 }
 
 int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
@@ -218,11 +226,11 @@ int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int
                          int64_t q_s1, int32_t q_dtype, int32_t num_q_heads, const int64_t* q_rows,
                          const int32_t* block_table, int64_t bt_s0, const int64_t* bt_rows, const int64_t* seq_lens,
                          int64_t num_seqs, float softmax_scale, int32_t num_splits, int32_t blocks_per_split,
-                         int32_t tier, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                         int32_t tier, int32_t flags, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
                          echokv_stream_t stream) {
   return decode_run(L, pages, block_res, res_group, res, query, q_s0, q_s1, q_dtype, num_q_heads, q_rows,
                     block_table, bt_s0, bt_rows, seq_lens, num_seqs, softmax_scale, num_splits, blocks_per_split,
-                    tier, nullptr, nullptr, true, out, o_s0, o_s1, out_dtype, stream);
+                    tier, flags, nullptr, nullptr, true, out, o_s0, o_s1, out_dtype, stream);
 }
 
 int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,

@@ -116,6 +116,13 @@ struct DecodeArgs {
   uint32_t kc_mul;
   float* acc;  // [S, Hq, splits, D]
   float* ml;   // [S, Hq, splits, 2] = (running max in log2 units, sum)
+  // Balanced schedule (ranges > 0): `ranges` equal block ranges; partial slot p of
+  // query head qh is row p * Hq + qh of acc / ml (2 * ranges slots); sequences
+  // inside one range are written to `out` directly. 0: the split schedule.
+  long ranges;
+  void* out;
+  long o_s0, o_s1;
+  int out_dtype;
 };
 
 struct MergeArgs {
@@ -211,6 +218,10 @@ hipError_t launch_store_blocks(const StoreBlkArgs& a, long n, hipStream_t s);
 hipError_t launch_gather(const GatherArgs& a, long n, hipStream_t s);
 hipError_t launch_dequant_dense(const DenseArgs& a, long n, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s);
+// Ranges of the balanced schedule for a batch on the current device: one per
+// workgroup slot the chip holds for the layer's tier, at most num_seqs * num_splits / 2.
+hipError_t decode_ranges(const DecodeArgs& a, long& ranges);
+hipError_t launch_merge_balanced(const DecodeArgs& a, hipStream_t s);
 hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s);
 hipError_t launch_canary(const CanaryArgs& a, int num_layers, hipStream_t s);
 size_t canary_lds_bytes(int d, int nbits, int rows);  // one canary workgroup's LDS

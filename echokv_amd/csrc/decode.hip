@@ -121,6 +121,18 @@ __device__ __forceinline__ h8_t kfrag(const uint32_t* w, int hf, const CodeK& k)
   }
 }
 
+// Eight byte-wide codes (two words) as an MFMA fragment of the codes themselves:
+// 1024 + c minus 1024 is exact in fp16. Unlike kfrag<8>, no 1024 bias enters the
+// fp32 score sums, whose rounding would otherwise scale with 1024 * |q * k_scale|
+// rather than with the score (INT2 / INT4 codes are small next to the bias).
+__device__ __forceinline__ h8_t kfrag_bytes(const uint32_t* w) {
+  const uint32_t m = 0x64646464u;
+  const h2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+  const h2_t a = u2h(perm(m, w[0], 0x04010400u)) - k1024, b = u2h(perm(m, w[0], 0x04030402u)) - k1024;
+  const h2_t c = u2h(perm(m, w[1], 0x04010400u)) - k1024, d = u2h(perm(m, w[1], 0x04030402u)) - k1024;
+  return w2h8(h2u(a), h2u(b), h2u(c), h2u(d));
+}
+
 // Fragment j (channels 8j..8j+7 of the lane's slice) from the lane's K words.
 template <int BITS>
 __device__ __forceinline__ h8_t kfrag_j(const uint32_t* kw, int j, const CodeK& k) {
@@ -283,7 +295,8 @@ struct Wave {
 
 // S^T of one 16-token tile from its codes, K group by 32-channel block j:
 //   S^T += codes_j . (q * k_scale)_j^T   as fp16 hi / lo pairs (two chains)
-//        - 1024 * sum_d (q * k_scale)_j  (INT8 fragments carry 1024 + c)
+//        - 1024 * sum_d (q * k_scale)_j  (BITS 8: fragments carry 1024 + c;
+//                                           any other BITS: the codes themselves)
 //        + k_min_j . q_j^T               (and q lo for float32 queries)
 // The products q * s are exact in fp32; hi = fp16(q * s), lo = fp16(fma(q, s,
 // -hi)) keeps S accurate to ~2^-22 relative. Each block's operands are built
@@ -368,8 +381,12 @@ __device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, cons
   float p[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], w.scale, -w.m_run));
-  w.l_lane += (p[0] + p[1]) + (p[2] + p[3]);
   const h4_t pb = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+  // The sum takes the fp16 weights the PV product uses, so the output is a properly
+  // normalized average of the values: a dominant token's weight rounding cancels.
+  const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+  w.l_lane = __builtin_amdgcn_fdot2(h2_t{pb[2], pb[3]}, one, __builtin_amdgcn_fdot2(h2_t{pb[0], pb[1]}, one, w.l_lane, false),
+                                    false);
 #pragma unroll
   for (int j = 0; j < Wave<D, QLO>::CPM; ++j)
     w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j], pb, w.acc[j], 0, 0, 0);
@@ -447,13 +464,12 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
 #pragma unroll
       for (int i = 0; i < CPL / 4; ++i) kw[i] = 0;
     }
-    const CodeK ck = code_consts<8>();
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
       uint32_t ks[4], km[4];
       load_bytes<16>(pages + blk * L.stride + L.o_ks + 2 * e0 + 16 * j, ks);
       load_bytes<16>(pages + blk * L.stride + L.o_km + 2 * e0 + 16 * j, km);
-      s_block<D, QLO, 8>(w, ks, km, kfrag_j<8>(kw, j, ck), j, sh, sl);
+      s_block<D, QLO, 0>(w, ks, km, kfrag_bytes(kw + 2 * j), j, sh, sl);
     }
   }
 #pragma unroll
@@ -917,18 +933,24 @@ __device__ __forceinline__ bool locate(const DecodeArgs& a, long si, int lane, i
   return false;
 }
 
-// One work item: split `split` of sequence `seq` for KV head h (one wave).
+// Where a span's result goes: the normalized output row of the sequence (the span
+// is the whole sequence), or unnormalized partials (acc, and (max, sum) in ml) at
+// row part_row0 + qh * part_stride of the workspaces, merged later.
+struct SpanSink {
+  long part_row0;
+  int part_stride;
+  bool direct;
+};
+
+// Blocks [b_start, b_end) of sequence `seq` for the KV heads of head group hg
+// (one wave per head).
 template <int D, int BITS, bool QLO>
-__device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int split, int hg, int wv, int lane,
-                                            uint8_t* ring, uint32_t ring0) {
+__device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b_start, int b_end, int hg, int wv,
+                                            int lane, uint8_t* ring, uint32_t ring0, SpanSink sink) {
   using W = Wave<D, QLO>;
   using R = Ring<D, BITS>;
   const Lay& L = a.L;
   const int seq_len = (int)a.lens[seq];
-  const int n_blocks = (seq_len + L.BS - 1) >> a.bs_shift;
-  const int bps = split_blocks(a, n_blocks);
-  const int b_start = split * bps;
-  const int b_end = b_start + bps < n_blocks ? b_start + bps : n_blocks;
   const long q_row = a.q_rows ? a.q_rows[seq] : seq;
   const long bt_row = a.bt_rows ? a.bt_rows[seq] : seq;
   const int c = lane >> 4, n = lane & 15;
@@ -1055,7 +1077,19 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, long seq, int s
   const float l = rows_sum(w.l_lane);
   if (live && n < a.gqa) {
     const long qh = (long)h * a.gqa + n;
-    const long row = (seq * a.hq + qh) * a.num_splits + split;
+    if (sink.direct) {  // lane (c, n): channels (4c + i) * CPM + j of query head qh
+      const float inv = 1.0f / l;
+      const long o = q_row * a.o_s0 + qh * a.o_s1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v[W::CPM];
+#pragma unroll
+        for (int j = 0; j < W::CPM; ++j) v[j] = w.acc[j][i] * inv;
+        st_n<W::CPM>(a.out, a.out_dtype, o + (4 * c + i) * W::CPM, v);
+      }
+      return;
+    }
+    const long row = sink.part_row0 + qh * sink.part_stride;
     float* dst = a.acc + row * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1096,7 +1130,185 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   long seq;
   int split;
   if (!locate(a, item / n_hg, lane, incl0, seq, split)) return;
-  decode_item<D, BITS, QLO>(a, seq, split, (int)(item % n_hg), wv, lane, ring_lds, ring0);
+  const int n_blocks = ((int)a.lens[seq] + a.L.BS - 1) >> a.bs_shift;
+  const int bps = split_blocks(a, n_blocks);
+  const int b_start = split * bps;
+  const int b_end = b_start + bps < n_blocks ? b_start + bps : n_blocks;
+  decode_span<D, BITS, QLO>(a, seq, b_start, b_end, (int)(item % n_hg), wv, lane, ring_lds, ring0,
+                            SpanSink{seq * a.hq * a.num_splits + split, a.num_splits, false});
+}
+
+// ---------------------------------------------------------------------------
+// Balanced schedule. The batch's blocks, sequence after sequence, are cut into
+// `ranges` contiguous ranges of equal block count, range r = [r T / R, (r+1) T / R)
+// (T blocks in all): one persistent workgroup per range and head group, as many
+// as the chip holds at once, so every workgroup streams the same number of
+// bytes and none waits for a late one. A sequence that lies inside one range
+// is written straight to its output row; the pieces of a longer one (each
+// range's first and last span) go to partial slots 2r and 2r + 1 and a merge
+// kernel combines them. Ranges depend on the whole batch, so results are not
+// batch-invariant (the split schedule is).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int seq_blocks(const DecodeArgs& a, long s) {
+  const long len = s < a.num_seqs ? a.lens[s] : 0;
+  return len > 0 ? (int)((len + a.L.BS - 1) >> a.bs_shift) : 0;
+}
+
+// A wave-uniform value held in a scalar register (the compiler cannot tell that a
+// reduction's result is the same in every lane).
+__device__ __forceinline__ long uni(long x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (long)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ long wave_total(long x) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+
+// Total blocks of the batch (every lane gets it).
+__device__ __forceinline__ long batch_blocks(const DecodeArgs& a, int lane) {
+  long t = 0;
+  for (long s0 = 0; s0 < a.num_seqs; s0 += 64) t += wave_total(seq_blocks(a, s0 + lane));
+  return t;
+}
+
+// First block of range r (of `ranges` over T blocks).
+__device__ __forceinline__ long range_begin(long r, long ranges, long T) { return r * T / ranges; }
+
+// The sequence holding global block x, and that sequence's first global block.
+__device__ __forceinline__ void seq_of_block(const DecodeArgs& a, long x, int lane, long& seq, long& first) {
+  long base = 0;
+  for (long s0 = 0; s0 < a.num_seqs; s0 += 64) {
+    const int nb = seq_blocks(a, s0 + lane);
+    const int incl = wave_incl_scan(nb, lane);
+    const int tot = __builtin_amdgcn_readlane(incl, 63);
+    if (x < base + tot) {
+      const int k = __builtin_popcountll(__builtin_amdgcn_ballot_w64(base + incl <= x));  // lanes ending at or before x
+      seq = s0 + k;
+      first = base + __builtin_amdgcn_readlane(incl, k) - __builtin_amdgcn_readlane(nb, k);
+      return;
+    }
+    base += tot;
+  }
+  seq = a.num_seqs;
+  first = base;
+}
+
+template <int D, int BITS, bool QLO>
+__global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_balanced_kernel(DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)ring_lds);
+  const int n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  // A range's head groups 8 dispatches apart: same XCD, shared L2 lines.
+  const long span = 8L * n_hg;
+  const long rr = blockIdx.x % span;
+  const long item = blockIdx.x - rr + (rr % 8) * n_hg + rr / 8;
+  const long r = item / n_hg;
+  const int hg = (int)(item % n_hg);
+  if (r >= a.ranges) return;
+  const long T = uni(batch_blocks(a, lane));
+  const long lo = range_begin(r, a.ranges, T), hi = range_begin(r + 1, a.ranges, T);
+  if (lo >= hi) return;
+  long seq, first;
+  seq_of_block(a, lo, lane, seq, first);
+  seq = uni(seq);
+  first = uni(first);
+  for (long pos = lo; pos < hi && seq < a.num_seqs;) {
+    const int nb = (int)uni(seq_blocks(a, seq));
+    const long end = first + nb < hi ? first + nb : hi;
+    if (nb > 0) {
+      const bool whole = pos == first && end == first + nb;
+      const long slot = 2 * r + (pos == lo ? 0 : 1);
+      decode_span<D, BITS, QLO>(a, seq, (int)(pos - first), (int)(end - first), hg, wv, lane, ring_lds, ring0,
+                                SpanSink{slot * a.hq, 1, whole});
+    }
+    pos = end;
+    first += nb;
+    ++seq;
+  }
+}
+
+// Merge of a balanced decode: one wave per (sequence, query head) whose blocks
+// span several ranges; the pieces sit in slot 2 rf + 1 (or 2 rf when the
+// sequence starts its first range) and 2 r for the ranges after it. Lane i
+// takes piece g + i's (max, sum) pair; the partial rows are then requested 16
+// at a time, so a sequence's merge costs a few memory round trips rather than
+// one per piece. A range left empty (fewer blocks than ranges) holds no piece:
+// its weight is 0 and its slot is not read.
+template <int D>
+__global__ __launch_bounds__(256) void merge_balanced_kernel(DecodeArgs a) {
+  constexpr int C = D / 64;
+  const int lane = threadIdx.x & 63;
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);  // seq * hq + head
+  if (row >= a.num_seqs * a.hq) return;
+  const long seq = row / a.hq;
+  const int head = (int)(row % a.hq);
+  const int nb = seq_blocks(a, seq);
+  if (nb == 0) return;
+  long first = 0;
+  for (long s0 = 0; s0 < seq; s0 += 64) first += wave_total(s0 + lane < seq ? seq_blocks(a, s0 + lane) : 0);
+  first = uni(first);
+  const long T = uni(batch_blocks(a, lane));
+  const long R = a.ranges;
+  auto range_of = [&](long x) {  // the range holding block x: floor(x R / T), then past empty ends
+    long q = x * R / T;
+    while (range_begin(q + 1, R, T) <= x) ++q;
+    return q;
+  };
+  const long rf = range_of(first), rl = range_of(first + nb - 1);
+  if (rf == rl) return;  // written directly by the decode kernel
+  const bool rf_second = first > range_begin(rf, R, T);
+  auto slot_of = [&](long q) { return 2 * q + (q == rf && rf_second ? 1 : 0); };
+  const long n = rl - rf + 1;
+  float m = -__builtin_inff();
+  for (long g = 0; g < n; g += 64) {
+    const long q = rf + g + lane;
+    if (q <= rl && range_begin(q, R, T) < range_begin(q + 1, R, T)) m = fmaxf(m, a.ml[(slot_of(q) * a.hq + head) * 2]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  float num[C] = {};
+  float den = 0.f;
+  for (long g = 0; g < n; g += 64) {
+    const long q = rf + g + lane;
+    float w = 0.f;
+    if (q <= rl && range_begin(q, R, T) < range_begin(q + 1, R, T)) {
+      const long pr = slot_of(q) * a.hq + head;
+      w = __builtin_amdgcn_exp2f(a.ml[pr * 2] - m);
+      den += a.ml[pr * 2 + 1] * w;
+    }
+    const int cnt = (int)(n - g < 64 ? n - g : 64);
+    for (int u0 = 0; u0 < cnt; u0 += 16) {
+      float x[16][C], wu[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        wu[u] = __shfl(w, (u0 + u) & 63, 64);  // piece g + u0 + u's weight (0 past the last)
+        const float* src = a.acc + (slot_of(rf + g + u0 + u) * a.hq + head) * D + C * lane;
+#pragma unroll
+        for (int e = 0; e < C; ++e) x[u][e] = 0.f;
+        if (u0 + u < cnt && wu[u] > 0.f) {
+#pragma unroll
+          for (int e = 0; e < C; ++e) x[u][e] = src[e];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+#pragma unroll
+        for (int e = 0; e < C; ++e) num[e] += x[u][e] * wu[u];
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+  const long o_row = a.q_rows ? a.q_rows[seq] : seq;
+  float o[C];
+#pragma unroll
+  for (int e = 0; e < C; ++e) o[e] = num[e] / den;
+  st_n<C>(a.out, a.out_dtype, o_row * a.o_s0 + head * a.o_s1 + C * lane, o);
 }
 
 // Merge of the splits: one wave per (sequence, query head); lane l holds
@@ -1194,14 +1406,72 @@ template <int D, int BITS, bool QLO>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
   const dim3 block(64 * kHeadsPerGroup);
   const size_t lds = (size_t)Ring<D, BITS>::WG_BYTES;
-  static std::atomic<uint64_t> attr_done{0};  // devices whose limit is raised, one bit each
+  const long n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  const long span = 8 * n_hg;  // the kernels permute workgroups within runs of `span`
+  if (a.ranges > 0) {
+    static std::atomic<uint64_t> attr_done{0};  // devices whose limit is raised, one bit each
+    if (ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO>, (int)lds, &attr_done) != hipSuccess)
+      return hipErrorInvalidValue;
+    const long wgs = (a.ranges * n_hg + span - 1) / span * span;
+    hipLaunchKernelGGL((decode_balanced_kernel<D, BITS, QLO>), dim3((unsigned)wgs), block, lds, s, a);
+    return hipGetLastError();
+  }
+  static std::atomic<uint64_t> attr_done{0};
   if (ensure_lds_limit((const void*)decode_kernel<D, BITS, QLO>, (int)lds, &attr_done) != hipSuccess)
     return hipErrorInvalidValue;
-  const long n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
-  const long span = 8 * n_hg;  // the kernel permutes workgroups within runs of `span`
   const long items = (a.num_seqs * a.num_splits * n_hg + span - 1) / span * span;
   hipLaunchKernelGGL((decode_kernel<D, BITS, QLO>), dim3((unsigned)items), block, lds, s, a);
   return hipGetLastError();
+}
+
+// Workgroups of the balanced kernel the current device holds at once (cached per device).
+template <int D, int BITS, bool QLO>
+hipError_t balanced_slots(long& slots) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<long> per_device[kMaxDevices];
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  long v = per_device[dev].load(std::memory_order_acquire);
+  if (v <= 0) {
+    int cus = 0, per_cu = 0;
+    const size_t lds = (size_t)Ring<D, BITS>::WG_BYTES;
+    static std::atomic<uint64_t> attr_done{0};
+    if ((e = ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO>, (int)lds, &attr_done)) != hipSuccess)
+      return e;
+    if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)decode_balanced_kernel<D, BITS, QLO>,
+                                                          64 * kHeadsPerGroup, lds)) != hipSuccess)
+      return e;
+    v = (long)(cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+    per_device[dev].store(v, std::memory_order_release);
+  }
+  slots = v;
+  return hipSuccess;
+}
+
+template <int D, bool QLO>
+hipError_t decode_slots_d(const DecodeArgs& a, long& slots) {
+  if (a.tier == 8) return balanced_slots<D, 8, QLO>(slots);
+  if (a.tier == 2) return balanced_slots<D, 2, QLO>(slots);
+  return balanced_slots<D, 4, QLO>(slots);
+}
+
+hipError_t decode_ranges(const DecodeArgs& a, long& ranges) {
+  const bool qlo = a.q_dtype == ECHOKV_F32;
+  long slots = 0;
+  hipError_t e;
+  if (a.L.D == 128) e = qlo ? decode_slots_d<128, true>(a, slots) : decode_slots_d<128, false>(a, slots);
+  else if (a.L.D == 64) e = qlo ? decode_slots_d<64, true>(a, slots) : decode_slots_d<64, false>(a, slots);
+  else return hipErrorInvalidValue;
+  if (e != hipSuccess) return e;
+  const long n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
+  long r = slots / n_hg;
+  const long cap = a.num_seqs * a.num_splits / 2;  // two partial slots per range in the workspaces
+  if (r > cap) r = cap;
+  ranges = r > 0 ? r : 1;
+  return hipSuccess;
 }
 
 template <int D, bool QLO>
@@ -1217,6 +1487,14 @@ hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
   if (a.L.D == 128) return qlo ? launch_decode_d<128, true>(a, s) : launch_decode_d<128, false>(a, s);
   if (a.L.D == 64) return qlo ? launch_decode_d<64, true>(a, s) : launch_decode_d<64, false>(a, s);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_merge_balanced(const DecodeArgs& a, hipStream_t s) {
+  const long wgs = (a.num_seqs * a.hq + 3) / 4;
+  if (a.L.D == 128) hipLaunchKernelGGL(merge_balanced_kernel<128>, dim3((unsigned)wgs), dim3(256), 0, s, a);
+  else if (a.L.D == 64) hipLaunchKernelGGL(merge_balanced_kernel<64>, dim3((unsigned)wgs), dim3(256), 0, s, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 // The workspaces (acc, ml) of echokv_decode_static: a file-scope device array.

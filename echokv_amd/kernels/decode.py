@@ -47,6 +47,7 @@ def decode_attention(
     num_splits: int | None = None,
     workspace: tuple[torch.Tensor, torch.Tensor] | str | None = None,
     tier: int | None = None,
+    batch_invariant: bool = False,
 ) -> torch.Tensor:
     """Attention of one query token per sequence over each sequence's cache.
 
@@ -60,7 +61,10 @@ def decode_attention(
     graph capture; at most 64 MiB of workspace, and calls on one GPU must not overlap).
     ``tier`` selects the kernel specialised for the layer's tier (the backend passes
     the layer controller's tier); by default the store's most common opened tier.
-    Blocks of other tiers are read correctly either way.
+    Blocks of other tiers are read correctly either way. By default the batch's
+    blocks are spread evenly over every workgroup the GPU holds (a sequence's result
+    then depends on the rest of the batch only through float rounding);
+    ``batch_invariant`` splits each sequence by its own length instead.
     """
     L = store.layout
     if L.k_group < 16:
@@ -100,7 +104,8 @@ def decode_attention(
     head = (_lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(store.block_res), _lib.ptr(store.res_group),
             _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1), _lib.dtype_code(query), hq,
             _lib.ptr(q_rows), _lib.ptr(block_table), block_table.stride(0), _lib.ptr(bt_rows), _lib.ptr(lens), s,
-            float(softmax_scale), int(num_splits), int(blocks_per_split), int(tier))
+            float(softmax_scale), int(num_splits), int(blocks_per_split), int(tier),
+            _lib.DECODE_BATCH_INVARIANT if batch_invariant else 0)
     tail = (_lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out), _lib.stream())
     if static:
         _lib.call("echokv_decode_static", *head, *tail)

@@ -35,6 +35,9 @@ enum {
   ECHOKV_ETOOBIG = 5,    /* the request exceeds the library's static scratch buffer */
 };
 
+/* echokv_decode flags. */
+enum { ECHOKV_DECODE_BATCH_INVARIANT = 1 };
+
 /* One layer's page layout (echokv_vllm/tiered_cache.py:76-147, TieredLayout):
  * header [0, block_size); V scale/min fp16 [block_size, H, D/v_group];
  * K scale/min fp16 [block_size/k_group, H, D]; then chunks_per_page chunks of
@@ -97,14 +100,19 @@ int echokv_gather(const echokv_layout* L, const uint8_t* pages, const int64_t* b
 int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* blocks, int64_t n,
                         const float* k, const float* v, int32_t bits, echokv_stream_t stream);
 
-/* Split-KV paged decode attention + split merge: sequence i attends with query row
- * q_rows[i] (NULL = i) over block-table row bt_rows[i] (NULL = i) for seq_lens[i]
- * tokens and writes out[q_rows[i]]; seq_lens[i] == 0 leaves the row untouched.
- * Split size = max(blocks_per_split, ceil(blocks / num_splits)) of the sequence's own
- * length (batch invariant). acc: [num_seqs, Hq, num_splits, D] f32, ml:
- * [num_seqs, Hq, num_splits, 2] f32 workspaces. tier (2, 4 or 8) selects the kernel
- * specialised for the layer's tier; blocks stored at another tier, and each block's
- * open K group, are still read correctly on a slower path.
+/* Paged decode attention: sequence i attends with query row q_rows[i] (NULL = i)
+ * over block-table row bt_rows[i] (NULL = i) for seq_lens[i] tokens and writes
+ * out[q_rows[i]]; seq_lens[i] == 0 leaves the row untouched. acc:
+ * [num_seqs, Hq, num_splits, D] f32, ml: [num_seqs, Hq, num_splits, 2] f32 workspaces.
+ * Default schedule: the batch's blocks are cut into equal ranges, one per workgroup
+ * the chip holds (at most num_seqs * num_splits / 2); a sequence inside one range is
+ * written directly, the others merged from partials. With flags &
+ * ECHOKV_DECODE_BATCH_INVARIANT: split-KV with splits of
+ * max(blocks_per_split, ceil(blocks / num_splits)) blocks of the sequence's own
+ * length, so a sequence's result does not depend on the rest of the batch. tier
+ * (2, 4 or 8) selects the kernel specialised for the layer's tier; blocks stored at
+ * another tier, and each block's open K group, are still read correctly on a slower
+ * path.
  * Replaces echokv_vllm/kernels/decode.py:44-92 (decode_attention) with its kernels
  * decode.py:135-224 (_decode_kernel) and decode.py:227-262 (_merge_kernel). */
 int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
@@ -113,8 +121,8 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
                   const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
                   const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs,
                   float softmax_scale, int32_t num_splits, int32_t blocks_per_split, int32_t tier,
-                  float* acc, float* ml, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
-                  echokv_stream_t stream);
+                  int32_t flags, float* acc, float* ml, void* out, int64_t o_s0, int64_t o_s1,
+                  int32_t out_dtype, echokv_stream_t stream);
 
 /* echokv_decode without workspace arguments, for callers that cannot allocate
  * (code under HIP-graph capture, serving loops that forbid allocation): acc and
@@ -130,7 +138,8 @@ int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int
                          const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
                          const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs,
                          float softmax_scale, int32_t num_splits, int32_t blocks_per_split, int32_t tier,
-                         void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream);
+                         int32_t flags, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                         echokv_stream_t stream);
 
 /* Chunked-prefill attention over the tiered pages (MFMA tiles), bottom-right causal:
  * tiles [n_tiles, 5] int32 = (first query row, tokens, first query position, ctx,

@@ -37,6 +37,28 @@ def t(a, device, dtype=None):
     return x if dtype is None else x.to(dtype)
 
 
+_MANTISSA = {torch.float16: (10, -14), torch.bfloat16: (7, -126)}  # mantissa bits, min normal exponent
+
+
+def half_ulp(ref, dtype) -> np.ndarray:
+    """Half the spacing of ``dtype`` at each reference value: the rounding error
+    an output stored in that dtype carries however exact the kernel is."""
+    if dtype not in _MANTISSA:
+        return np.zeros(np.shape(ref))
+    mant, emin = _MANTISSA[dtype]
+    a = np.abs(np.asarray(ref, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** emin)))  # subnormals share the min-normal spacing
+    return np.exp2(e - mant) / 2
+
+
 def maxdiff(got, ref) -> float:
-    g = got.detach().float().cpu().numpy() if torch.is_tensor(got) else np.asarray(got, np.float64)
-    return float(np.abs(g.astype(np.float64) - np.asarray(ref, np.float64)).max())
+    """Max |got - ref| over elements; for an fp16 / bf16 output, beyond half the
+    output dtype's spacing at ref, so storing the dtype's neighbour of an exact
+    result is not counted against the kernel and anything more is."""
+    ref = np.asarray(ref, np.float64)
+    if torch.is_tensor(got):
+        slack = half_ulp(ref, got.dtype)
+        g = got.detach().float().cpu().numpy().astype(np.float64)
+    else:
+        slack, g = 0.0, np.asarray(got, np.float64)
+    return float((np.abs(g - ref) - slack).max())

@@ -16,6 +16,7 @@ from echokv_amd import _vllm
 from echokv_amd.backend import EchoKVAttentionImpl, EchoKVMetadataBuilder
 from echokv_amd.controller import SUPPORTED_BITS
 from echokv_amd.tiered_cache import TieredLayout
+from gpu_util import maxdiff
 from oracle import attention as OA
 from oracle import canary as OC
 from oracle import store as OS
@@ -133,17 +134,6 @@ def run_layers(layers, md, q, k, v):
     return outs
 
 
-def fp16_err(got, ref) -> float:
-    """The error of an fp16 output beyond its own rounding: max over elements of
-    |got - ref| minus half the fp16 spacing at ref (the float64 oracle value), so a
-    value stored as the fp16 neighbour of an exact result is not counted against
-    the kernel, and anything more is."""
-    ref = np.asarray(ref, np.float64)
-    g = got.detach().float().cpu().numpy().astype(np.float64)
-    half_ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64) / 2
-    return float((np.abs(g - ref) - half_ulp).max())
-
-
 def check_decode(layers, table_np, lens, q, outs, label):
     worst = 0.0
     for li, layer in enumerate(layers):
@@ -151,7 +141,7 @@ def check_decode(layers, table_np, lens, q, outs, label):
         n = len(lens)
         ref = OA.decode_attention(ps, q[li][:n].float().cpu().numpy(), table_np, np.asarray(lens), D ** -0.5,
                                   vectorized=True)
-        worst = max(worst, fp16_err(outs[li].view(-1, HQ, D)[:n], ref))
+        worst = max(worst, maxdiff(outs[li].view(-1, HQ, D)[:n], ref))
     print(f"[backend {label}] max err {worst:.3e}", flush=True)
     assert worst <= TOL, f"{label}: {worst}"
 
@@ -181,7 +171,7 @@ def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
         ps = oracle_of(layer.impl)
         ref = OA.prefill_attention(ps, q[li].float().cpu().numpy(), md.prefill, md.prefill_reqs, table_np,
                                    D ** -0.5, vectorized=True)
-        worst = max(worst, fp16_err(outs[li].view(-1, HQ, D), ref))
+        worst = max(worst, maxdiff(outs[li].view(-1, HQ, D), ref))
         assert int(layer.impl.store.tag[table_np[1, 0]]) == layer.impl.controller.bits
     print(f"[backend prefill] max err {worst:.3e}", flush=True)
     assert worst <= TOL

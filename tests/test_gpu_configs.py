@@ -127,6 +127,8 @@ def test_cfg2_full_layer_decode_matches_oracle(device, bits):
         ref = OA.decode_attention(ps, qt.float().cpu().numpy(), table, lens, scale, vectorized=True)
         got = dec.decode_attention(store, qt, table_d, lens_d, scale, tier=bits)
         check(f"cfg2 int{bits} {name}", got, ref)
+        got = dec.decode_attention(store, qt, table_d, lens_d, scale, tier=bits, batch_invariant=True)
+        check(f"cfg2 int{bits} {name} split schedule", got, ref)
         if name == "fp16 q":  # every tile through the generic path (the layer's tier set elsewhere)
             other = 4 if bits != 4 else 8
             got = dec.decode_attention(store, qt, table_d, lens_d, scale, tier=other)
@@ -214,9 +216,11 @@ def test_cfg4_gqa8_long_context_split_paths(device):
     scale = 128 ** -0.5
     ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, scale, vectorized=True)
     nblk = -(-32768 // 16)
-    for label, kw in (("default splits", {}),
-                      ("4 splits of 513 blocks", {"num_splits": 4}),
-                      ("187 splits of 11 blocks", {"num_splits": 200, "blocks_per_split": 1})):
+    for label, kw in (("balanced, 32 ranges", {}),
+                      ("balanced, 2 ranges of 1024 blocks", {"num_splits": 4}),
+                      ("default splits", {"batch_invariant": True}),
+                      ("4 splits of 513 blocks", {"num_splits": 4, "batch_invariant": True}),
+                      ("187 splits of 11 blocks", {"num_splits": 200, "blocks_per_split": 1, "batch_invariant": True})):
         got = dec.decode_attention(store, q, table_d, lens_d, scale, tier=4, **kw)
         check(f"cfg4 {label}", got, ref)
     assert -(-nblk // 4) > 64 and -(-nblk // -(-nblk // 200)) > 64
@@ -250,11 +254,15 @@ def test_more_than_64_sequences_with_padding_rows(device):
     out = torch.full((150, 32, 128), 7.0, device=device)
     dec.decode_attention(store, q, torch.from_numpy(table).to(device, torch.int32), torch.from_numpy(run).to(device),
                          128 ** -0.5, out=out)
+    split = torch.full((150, 32, 128), 7.0, device=device)
+    dec.decode_attention(store, q, torch.from_numpy(table).to(device, torch.int32), torch.from_numpy(run).to(device),
+                         128 ** -0.5, out=split, batch_invariant=True)
     live = np.flatnonzero(run > 0)
     ref = OA.decode_attention(ps, q[live].float().cpu().numpy(), table[live], lens[live], 128 ** -0.5,
                               vectorized=True)
     check("150 sequences", out[live], ref)
-    assert (out[[3, 100]] == 7.0).all()
+    check("150 sequences, split schedule", split[live], ref)
+    assert (out[[3, 100]] == 7.0).all() and (split[[3, 100]] == 7.0).all()
 
 
 @pytest.mark.parametrize("d,vg", [(128, 16), (128, 64), (64, 32), (64, 16)])
