@@ -22,7 +22,8 @@ DECODE_BATCH_INVARIANT = 1
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTS = (
-    "echokv_error_string", "echokv_write_tokens", "echokv_finalize_k", "echokv_seal_groups", "echokv_gather",
+    "echokv_error_string", "echokv_write_tokens", "echokv_finalize_k", "echokv_write_step", "echokv_seal_groups",
+    "echokv_gather",
     "echokv_store_blocks", "echokv_decode", "echokv_decode_static", "echokv_prefill", "echokv_prefill_dense", "echokv_prefill_dense_workspace",
     "echokv_dequant_dense", "echokv_canary_kl",
 )
@@ -52,6 +53,7 @@ LP, RP = C.POINTER(Layout), C.POINTER(Residual)
 _SIGS = {
     "echokv_write_tokens": [LP, P, P, I64, I64, P, I64, I64, I32, P, I64, I64, RP, P, I64, I64, P],
     "echokv_finalize_k": [LP, P, P, I64, I64, I32, P, P, I64, RP, P],
+    "echokv_write_step": [LP, P, P, I64, I64, P, I64, I64, I32, P, I64, I64, P, P, I64, RP, P, I64, I64, P],
     "echokv_seal_groups": [LP, P, P, I64, RP, P],
     "echokv_gather": [LP, P, P, P, RP, P, P, I64, P, P, P],
     "echokv_store_blocks": [LP, P, P, I64, P, P, I32, P],

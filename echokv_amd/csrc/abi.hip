@@ -92,6 +92,23 @@ int echokv_finalize_k(const echokv_layout* L, uint8_t* pages, const void* key, i
   return launched(ek::launch_finalize_k(a, grid_rows, (hipStream_t)stream));
 }
 
+int echokv_write_step(const echokv_layout* L, uint8_t* pages, const void* key, int64_t k_s0, int64_t k_s1,
+                      const void* value, int64_t v_s0, int64_t v_s1, int32_t kv_dtype, const int64_t* tok,
+                      int64_t tok_s0, int64_t n_rows, const int64_t* fin, const int64_t* fin_count, int64_t fin_grid,
+                      const echokv_residual* res, float* kref, int64_t kref_s0, int64_t kref_s1,
+                      echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (L->k_group > ek::kMaxDeferred) return ECHOKV_ESHAPE;
+  if (!dtype_ok(kv_dtype)) return ECHOKV_EDTYPE;
+  if (n_rows < 0 || fin_grid < 0 || tok_s0 < n_rows || !res_ok(res)) return ECHOKV_EINVAL;
+  if (n_rows + fin_grid == 0) return ECHOKV_OK;
+  if (!pages || !key || !fin_count || (n_rows && (!value || !tok)) || (fin_grid && !fin)) return ECHOKV_EINVAL;
+  ek::StepArgs a{ek::WriteTokArgs{to_lay(L), pages, key, k_s0, k_s1, value, v_s0, v_s1, kv_dtype, tok, tok_s0,
+                                  to_res(res), kref, kref_s0, kref_s1},
+                 fin, fin_count, fin_grid, n_rows};
+  return launched(ek::launch_write_step(a, (hipStream_t)stream));
+}
+
 int echokv_seal_groups(const echokv_layout* L, uint8_t* pages, const int64_t* ev, int64_t n,
                        const echokv_residual* res, echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;

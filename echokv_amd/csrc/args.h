@@ -49,6 +49,16 @@ struct FinArgs {
   Res res;
 };
 
+// A fused step: token rows plus fin rows (fin: [>= fin_grid, 3 + KG]).
+constexpr int kMaxDeferred = 256;  // k_group bound of the fused step (a slot's group has < k_group rows in a step)
+struct StepArgs {
+  WriteTokArgs w;
+  const int64_t* fin;
+  const int64_t* fin_count;
+  long fin_grid;
+  long n_rows;
+};
+
 struct SealArgs {
   Lay L;
   uint8_t* pages;
@@ -213,6 +223,7 @@ hipError_t decode_scratch(void** ptr);
 
 hipError_t launch_write_tokens(const WriteTokArgs& a, long n_rows, hipStream_t s);
 hipError_t launch_finalize_k(const FinArgs& a, long rows, hipStream_t s);
+hipError_t launch_write_step(const StepArgs& a, hipStream_t s);
 hipError_t launch_seal(const SealArgs& a, long n, hipStream_t s);
 hipError_t launch_store_blocks(const StoreBlkArgs& a, long n, hipStream_t s);
 hipError_t launch_gather(const GatherArgs& a, long n, hipStream_t s);

@@ -848,13 +848,21 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
 }
 
 // Wait for this wave's part of the tile about to be read: `ahead` tiles were
-// issued after it, M DMA instructions each (NB - 2 at most).
+// issued after it (wave-uniform, NB - 2 at most), M DMA instructions each, so at
+// most ahead * M of this wave's loads may stay in flight.
+template <int M, int K>
+__device__ __forceinline__ void wait_ahead(int ahead) {
+  if constexpr (K <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= K) wait_vmcnt<K * M>();
+    else wait_ahead<M, K - 1>(ahead);
+  }
+}
 template <int D, int BITS, int NB>
 __device__ __forceinline__ void wait_tile(int ahead) {
-  constexpr int M = Ring<D, BITS>::M;
-  if (NB >= 4 && ahead >= 2) wait_vmcnt<2 * M>();
-  else if (ahead >= 1) wait_vmcnt<M>();
-  else wait_vmcnt<0>();
+  static_assert((NB - 2) * Ring<D, BITS>::M <= 63, "vmcnt holds at most 63");
+  wait_ahead<Ring<D, BITS>::M, NB - 2>(ahead);
 }
 
 __device__ __forceinline__ uint32_t rl(uint32_t v, int lane) { return __builtin_amdgcn_readlane(v, lane); }

@@ -15,9 +15,10 @@ namespace ek {
 // write_tokens (echokv_vllm/kernels/write.py:29-36, 172-229)
 // ---------------------------------------------------------------------------
 
-__global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) {
+// Token row t; res_here: this workgroup stores the row's K to the residual (a
+// fused step leaves that store to the workgroup finalizing the slot's old group).
+__device__ __forceinline__ void write_token_row(const WriteTokArgs& a, long t, bool res_here) {
   const Lay& L = a.L;
-  const long t = blockIdx.x;
   const long slot = a.tok[t];
   if (slot < 0) return;
   const long blk = slot / L.BS;
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) 
     store_codes4(a.pages + rb + side + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
 
     // K: residual (open group), codes under the sealed stats, K_ref ring.
-    if (rslot >= 0 && rslot < a.res.rows)
+    if (res_here && rslot >= 0 && rslot < a.res.rows)
       st_n<4>(a.res.ptr, a.res.dtype, rslot * a.res.s0 + (long)(off % L.KG) * a.res.s1 + h * a.res.s2 + 4 * c, k);
     if (sealed != 0) {
       uint32_t kq[4];
@@ -86,6 +87,8 @@ __global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) 
     }
   }
 }
+
+__global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) { write_token_row(a, blockIdx.x, true); }
 
 // ---------------------------------------------------------------------------
 // K-group quantization shared by finalize_k, seal and store_blocks: the group's
@@ -233,20 +236,31 @@ __device__ __forceinline__ void finalize_group(const FinArgs a, const int64_t* r
   }
 }
 
-__global__ __launch_bounds__(kThreads) void finalize_k_kernel(FinArgs a) {
+// Deferred residual stores of a fused step: token rows whose K goes to the slot
+// a fin row releases, with the residual row each one writes.
+struct Deferred {
+  long t[kMaxDeferred];
+  int row[kMaxDeferred];
+  int n;
+};
+
+// Fin row f, one (head, quad) item per thread pass; after an item's reads (its
+// stats and codes depend on them), the residual K stores of the token rows in
+// `def` for the same item: a thread overwrites only residual words it has read.
+__device__ __forceinline__ void finalize_row(const FinArgs& a, long f, const WriteTokArgs* w, const Deferred* def) {
   const Lay& L = a.L;
-  const long f = blockIdx.x;
-  if (f >= *a.fin_count) return;
   const int64_t* row = a.fin + f * (3 + L.KG);
   const long blk = row[0];
   const int grp = (int)row[1];
   const long rs = row[2] < 0 ? 0 : row[2];
-  if (blk < 0 || blk >= L.nb || grp < 0 || grp >= L.BS / L.KG || rs >= a.res.rows) return;
+  const bool ok = blk >= 0 && blk < L.nb && grp >= 0 && grp < L.BS / L.KG && rs < a.res.rows;
   const int quads = L.D / 4;
   const bool same = a.kv_dtype == a.res.dtype && L.KG <= 32;
+  const int n_def = def ? def->n : 0;
   for (int i = threadIdx.x; i < L.H * quads; i += kThreads) {
     const int h = i / quads, c = i % quads;
-    if (same && a.kv_dtype == ECHOKV_F16) {
+    if (!ok) {
+    } else if (same && a.kv_dtype == ECHOKV_F16) {
       finalize_group<_Float16>(a, row, blk, grp, rs, h, c);
     } else if (same && a.kv_dtype == ECHOKV_F32) {
       finalize_group<float>(a, row, blk, grp, rs, h, c);
@@ -259,7 +273,65 @@ __global__ __launch_bounds__(kThreads) void finalize_k_kernel(FinArgs a) {
       };
       quantize_k_group(L, a.pages, blk, grp, grp * L.KG, L.KG, bits, h, c, fetch);
     }
+    for (int d = 0; d < n_def; ++d) {
+      float k[4];
+      ld_n<4>(w->key, w->kv_dtype, def->t[d] * w->k_s0 + h * w->k_s1 + 4 * c, k);
+      st_n<4>(a.res.ptr, a.res.dtype, row[2] * a.res.s0 + (long)def->row[d] * a.res.s1 + h * a.res.s2 + 4 * c, k);
+    }
   }
+}
+
+__global__ __launch_bounds__(kThreads) void finalize_k_kernel(FinArgs a) {
+  const long f = blockIdx.x;
+  if (f >= *a.fin_count) return;
+  finalize_row(a, f, nullptr, nullptr);
+}
+
+// One step's writes in one launch (the pair finalize_k, write_tokens). Workgroups
+// [0, fin_grid) take fin rows (masked by the device count), the rest token rows.
+// The pair's order matters only where a token's K goes to a residual slot that a
+// fin row of the step releases (the slot's old group completes now and is read
+// from it): both sides see that from the plan itself -- fin row f's slot
+// fin[f][2] equals the token's residual slot -- and that one store moves to the
+// fin row's workgroup, after its reads; nothing waits on another workgroup.
+__global__ __launch_bounds__(kThreads) void write_step_kernel(StepArgs s) {
+  const WriteTokArgs& a = s.w;
+  const int w = 3 + a.L.KG;
+  const long count = *s.fin_count;
+  if ((long)blockIdx.x < s.fin_grid) {
+    const long f = blockIdx.x;
+    if (f >= count) return;
+    const long rs = s.fin[f * w + 2];
+    __shared__ Deferred def;
+    if (threadIdx.x == 0) def.n = 0;
+    __syncthreads();
+    if (rs >= 0 && rs < a.res.rows) {
+      for (long t = threadIdx.x; t < s.n_rows; t += kThreads) {
+        const long slot = a.tok[t];
+        if (a.tok[a.tok_s0 + t] == rs && slot >= 0) {
+          const int i = atomicAdd(&def.n, 1);  // LDS counter: at most k_group - 1 rows take a slot in a step
+          if (i < kMaxDeferred) {
+            def.t[i] = t;
+            def.row[i] = (int)((slot % a.L.BS) % a.L.KG);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (def.n > kMaxDeferred) def.n = kMaxDeferred;  // not reached: the host checks k_group <= kMaxDeferred
+    const FinArgs fa{a.L, a.pages, a.key, a.k_s0, a.k_s1, a.kv_dtype, s.fin, s.fin_count, a.res};
+    finalize_row(fa, f, &a, &def);
+    return;
+  }
+  const long t = (long)blockIdx.x - s.fin_grid;
+  const long rslot = a.tok[a.tok_s0 + t];
+  bool hit = false;
+  if (rslot >= 0) {  // fin rows past the device count are never read (a graph's buffer may hold fewer)
+    const long nf = count < s.fin_grid ? count : s.fin_grid;
+    for (long f = threadIdx.x; f < nf; f += kThreads) hit = hit || s.fin[f * w + 2] == rslot;
+  }
+  const bool deferred = __syncthreads_or(hit);
+  write_token_row(a, t, !deferred);
 }
 
 // ---------------------------------------------------------------------------
@@ -455,6 +527,10 @@ hipError_t launch_write_tokens(const WriteTokArgs& a, long n_rows, hipStream_t s
 }
 hipError_t launch_finalize_k(const FinArgs& a, long rows, hipStream_t s) {
   hipLaunchKernelGGL(finalize_k_kernel, dim3((unsigned)rows), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+hipError_t launch_write_step(const StepArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(write_step_kernel, dim3((unsigned)(a.fin_grid + a.n_rows)), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 hipError_t launch_seal(const SealArgs& a, long n, hipStream_t s) {

@@ -366,10 +366,13 @@ class TieredKVCache:
     def apply(self, meta: WriteMeta, key: torch.Tensor, value: torch.Tensor, kref: torch.Tensor | None = None,
               capturing: bool = False) -> None:
         """Device side: finalize completed K groups, then store the step's tokens
-        (``tiered_cache.py:415-432``). ``capturing`` launches full grids masked by the
-        device counts, as a replayed graph needs."""
-        from echokv_amd.kernels.write import finalize_k, write_tokens
+        (``tiered_cache.py:415-432``), as one launch. ``capturing`` launches full
+        grids masked by the device counts, as a replayed graph needs."""
+        from echokv_amd.kernels.write import FUSED_MAX_K_GROUP, finalize_k, write_step, write_tokens
 
+        if self.layout.k_group <= FUSED_MAX_K_GROUP:
+            write_step(self, key, value, meta, kref, full_grid=capturing)
+            return
         if capturing or meta.n_fin:
             finalize_k(self, key, meta, full_grid=capturing)
         if meta.n_rows:

@@ -81,6 +81,22 @@ int echokv_finalize_k(const echokv_layout* L, uint8_t* pages,
                       const int64_t* fin, const int64_t* fin_count, int64_t grid_rows,
                       const echokv_residual* res, echokv_stream_t stream);
 
+/* One step's writes in one launch: echokv_finalize_k's fin rows (workgroups
+ * [0, fin_grid), rows >= *fin_count skipped) and echokv_write_tokens' token rows
+ * (n_rows of them), with the same arguments and results as the finalize-then-write
+ * pair. A token whose residual slot is released by a fin row of the same step
+ * has its residual K stored by that fin row's workgroup after it has read the
+ * slot, so the two launches' order is kept without a second launch.
+ * Requires k_group <= 256. Replaces the pair as echokv_vllm/tiered_cache.py:415-432
+ * (apply) issues it: finalize_k (write.py:39-50), then write_tokens (write.py:29-36). */
+int echokv_write_step(const echokv_layout* L, uint8_t* pages,
+                      const void* key, int64_t k_s0, int64_t k_s1,
+                      const void* value, int64_t v_s0, int64_t v_s1, int32_t kv_dtype,
+                      const int64_t* tok, int64_t tok_s0, int64_t n_rows,
+                      const int64_t* fin, const int64_t* fin_count, int64_t fin_grid,
+                      const echokv_residual* res, float* kref, int64_t kref_s0, int64_t kref_s1,
+                      echokv_stream_t stream);
+
 /* Seal evicted residual groups: ev [n, 6] int64 = (slot, block, group, fill, bits, mask).
  * Replaces the device ops of echokv_vllm/tiered_cache.py:379-394 (_seal). */
 int echokv_seal_groups(const echokv_layout* L, uint8_t* pages, const int64_t* ev, int64_t n,

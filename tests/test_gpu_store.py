@@ -158,3 +158,61 @@ def test_decode_cases_store_oracle_bytes(device):
         store, *_ = gpu_replay(s, device)
         bad = np.flatnonzero((store.pages.cpu().numpy() != sim.ps.pages).any(axis=1))
         assert bad.size == 0, f"{s.name}: pages {bad.tolist()} differ"
+
+
+def slot_reuse_script():
+    """Sixteen sequences decoding in lock step with staggered lengths (block 32,
+    K group 16): whenever one sequence's token completes a group from the
+    residual, another opens a group in the same step and takes the freed slot
+    (the planner's stack hands it out next), so those rows' residual stores
+    must follow the finalize's reads of that slot."""
+    bs, kg, h, d = 32, 16, 2, 64
+    start = np.array([15, 16, 47, 0, 31, 32, 79, 64, 15, 48, 47, 80, 63, 0, 31, 16])
+    steps_n = 64
+    nbs = -(-(start + steps_n) // bs)
+    rng = np.random.default_rng(9)
+    num_blocks = int(nbs.sum()) + 2
+    perm = rng.permutation(num_blocks)
+    table, o = [], 0
+    for n in nbs:
+        table.append(perm[o : o + n])
+        o += n
+    pre = np.concatenate([table[i][np.arange(n) // bs] * bs + np.arange(n) % bs for i, n in enumerate(start)])
+    steps = [(pre.astype(np.int64), 4)]
+    for t in range(steps_n):
+        pos = start + t
+        steps.append((np.array([table[i][p // bs] * bs + p % bs for i, p in enumerate(pos)], np.int64), 4))
+    return S.Script("slot_reuse", h, d, bs, 8, kg, 32, num_blocks, 20, steps, seed=3, dtype="f16",
+                    kref_window=32, full_bytes=False)
+
+
+def test_fused_step_matches_finalize_then_write_and_oracle(device, monkeypatch):
+    """The fused write step stores the bytes of the finalize-then-write pair and of
+    the CPU oracle, on a script whose steps hand a slot released by a finalize to
+    another group (the deferred residual stores are taken: counted on the host)."""
+    from echokv_amd.kernels import write as W
+    from echokv_amd.write_plan import WritePlanner
+    from host_sim import replay
+
+    s = slot_reuse_script()
+    pl = WritePlanner(s.bs, s.kg, s.residual_slots, kref_window=s.kref_window, num_blocks=s.num_blocks)
+    deferred = 0
+    for slots, *_ in s.steps:
+        plan = pl.plan(slots)
+        freed = {int(x) for x in plan.fin[:, 2] if x >= 0}
+        deferred += sum(int(x) in freed for x in plan.tok_res)
+    assert deferred >= 10, f"the script defers only {deferred} residual stores"
+    fused, *_, kref_f = gpu_replay(s, device)
+    monkeypatch.setattr(W, "FUSED_MAX_K_GROUP", 0)  # the store's apply takes the two-launch pair
+    pair, *_, kref_p = gpu_replay(s, device)
+    torch.cuda.synchronize()
+    print(f"[store] slot_reuse: {deferred} deferred residual stores", flush=True)
+    assert torch.equal(fused.pages, pair.pages)
+    assert torch.equal(fused.block_res, pair.block_res)
+    live = fused.block_res[fused.block_res >= 0]
+    assert live.numel() and torch.equal(fused.res_k[live], pair.res_k[live])
+    assert torch.equal(kref_f, kref_p)
+    sim = replay(s)
+    bad = np.flatnonzero((fused.pages.cpu().numpy() != sim.ps.pages).any(axis=1))
+    assert bad.size == 0, f"pages {bad.tolist()} differ from the oracle"
+    np.testing.assert_array_equal(fused.res_k[live].float().cpu().numpy(), sim.ps.res_k[live.cpu().numpy()])
