@@ -15,10 +15,18 @@ needs): the 16 INT4 layers' decode (decode + merge kernels, each layer over its
 own pages, at the lengths the timed steps reached) captured as one HIP graph
 and replayed ``--reps`` times between HIP events on the launch stream, so the
 time is GPU work only; ``roofline`` puts it against 8 TB/s. ``ms_per_step`` and
-``e2e_decode_tok_s`` time the whole 32-layer step (host planning included) over
-the ``--steps`` timed steps, each replayed as one HIP graph (the plan staged into
-fixed device buffers); ``e2e_eager_*`` times the same steps launched one kernel at
-a time.
+``attn_write_step_tok_s`` time the whole 32-layer attention + KV-write step (host
+planning included; no model: no projections, MLP or sampling) over the
+``--steps`` timed steps, each replayed as one HIP graph (the plan staged into
+fixed device buffers); ``attn_write_step_eager_*`` times the same steps launched
+one kernel at a time. ``host_plan_us`` is the host's share of a step (plan,
+chunk-pool opens, staging) at 64 sequences, and at 256 on the planner alone.
+``hbm_copy_ceiling_GBs`` is the same run's 1 GiB device copy rate (read + write).
+
+``cpu_baseline``: the reference's PyTorch path restated in torch on the host cores
+(``oracle/torch_cpu.py``): decode of a sample of the INT4 layer's sequences
+(``value``, GB/s of the same algorithmic bytes), one step's writes, one prefill
+chunk and one canary fire of a layer.
 
 ``prefill`` (one layer): 16 sequences x 4096 tokens written
 and attended in 512-token chunks over an INT4 cache, bf16 activations; per
@@ -189,7 +197,10 @@ def run(args) -> dict:
     with torch.cuda.graph(step_graph):
         all_layers()
 
+    host_s = [0.0]
+
     def gstep(i):
+        t_host = time.perf_counter()
         pos = ctx - 1 + i
         slots = table[np.arange(S), pos // BS] * BS + pos % BS
         plan = shared.planner.plan(slots)
@@ -205,6 +216,7 @@ def run(args) -> dict:
             fin_buf[: meta.n_fin].copy_(meta.fin)
         cnt_buf.copy_(meta.fin_count)
         lens_buf.copy_(to_device(torch.from_numpy(pos + 1), dev))
+        host_s[0] += time.perf_counter() - t_host
         step_graph.replay()
         return pos + 1
 
@@ -212,6 +224,7 @@ def run(args) -> dict:
     for i in range(g0, g0 + 2):
         gstep(i)
     torch.cuda.synchronize()
+    host_s[0] = 0.0
     t0 = time.perf_counter()
     for i in range(g0 + 2, g0 + 2 + args.steps):
         lens = gstep(i)
@@ -268,9 +281,10 @@ def run(args) -> dict:
             "seq_len": int(ctx.mean()),
             "parallelism": "single GPU",
         },
-        "e2e_decode_tok_s": round(S * args.steps / wall, 1),
-        "e2e_eager_ms_per_step": round(wall_eager * 1e3 / args.steps, 3),
-        "e2e_eager_tok_s": round(S * args.steps / wall_eager, 1),
+        "attn_write_step_tok_s": round(S * args.steps / wall, 1),
+        "host_plan_us": {"64": round(host_s[0] / args.steps * 1e6, 1), "256 (planner only)": plan_only_us(256)},
+        "attn_write_step_eager_ms": round(wall_eager * 1e3 / args.steps, 3),
+        "attn_write_step_eager_tok_s": round(S * args.steps / wall_eager, 1),
         "int4_decode_us_per_layer": round(avg_ms * 1e3, 2),
         "roofline": {
             "bound": "hbm",
@@ -283,8 +297,9 @@ def run(args) -> dict:
             "alg_bytes_per_launch": int(per_layer_bytes),
         },
     }
+    res["hbm_copy_ceiling_GBs"] = copy_ceiling(dev)
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(stores[int4[0]], q[int4[0]], table, ctx + args.warmup + args.steps - 1)
+        res["cpu_baseline"] = cpu_baseline(stores[int4[0]], shared, q[int4[0]], kn[int4[0]], vn[int4[0]], table, lens)
     if not args.no_prefill:
         res["prefill"] = run_prefill()
     return res
@@ -519,34 +534,85 @@ def run_cfg4(reps: int = 5) -> dict:
     }
 
 
-def cpu_baseline(store, q, table, lens) -> dict:
-    """The numpy oracle's decode (vectorized gather + float64 SDPA) on the host: one INT4
-    layer-step over a bounded sample of the batch's sequences."""
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(store, shared, q, kn, vn, table, lens) -> dict:
+    """The reference's PyTorch path restated in torch (``oracle/torch_cpu.py``) on the
+    host cores, on bounded samples of the benchmark's own data (one INT4 layer):
+
+    * decode (``value``): gather + dequantize + SDPA of a sample of the batch's
+      sequences, GB/s of the same algorithmic bytes as the GPU figure;
+    * write: one decode step's quantize-on-write of the layer (finalize of the
+      completing groups, then the 64 token rows), microseconds;
+    * prefill: the last 512-token chunk of one 4096-token context (bottom-right
+      causal), TFLOP/s of 4 D Hq per visible pair;
+    * canary: the per-tier KL of one layer (64 K_ref keys, 4 query rows).
+    """
     import torch
 
-    from oracle.attention import decode_attention as oracle_decode
+    from oracle import torch_cpu as TC
     from oracle.store import Layout, PageStore
 
-    n_seq = S
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1))
+    torch.set_num_threads(threads)
     L = Layout(H, D, BS, MEM, KG, VG)
-    ps = PageStore.__new__(PageStore)
-    ps.L, ps.n = L, store.num_blocks
-    ps.pages = store.pages.cpu().numpy()
-    ps.res_k = store.res_k.float().cpu().numpy()
-    ps.block_res = store.block_res.cpu().numpy()
-    ps.res_group = store.res_group.cpu().numpy()
-    qn = q[:n_seq].float().cpu().numpy()
+    ps = PageStore.over(L, store.pages.cpu().numpy().copy(), store.res_k.float().cpu().numpy(),
+                        store.block_res.cpu().numpy(), store.res_group.cpu().numpy())
+    qc = q.float().cpu()
+    out = {"cores": threads, "cpu": _cpu_model(), "kind": "port"}
+
+    # Decode: the whole layer-step (every sequence of the batch).
+    n_seq = S
     t0 = time.perf_counter()
-    oracle_decode(ps, qn, table[:n_seq], lens[:n_seq], D ** -0.5, vectorized=True)
+    TC.decode(ps, qc[:n_seq], table[:n_seq], lens[:n_seq], D ** -0.5)
     dt = time.perf_counter() - t0
-    g = D // VG
-    ln = lens[:n_seq]
-    b = int(((ln // KG) * KG * (2 * H * D // 2 + H * g * 4) + (ln // KG) * H * D * 4
-             + (ln % KG) * (H * D // 2 + H * g * 4 + H * D * 2)).sum()) + 2 * n_seq * HQ * D * 2
-    return {"value": round(b / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle decode of one INT4 layer-step, {n_seq} of 64 sequences "
-                      f"({int(ln.sum())} tokens), {dt:.1f}s on {os.cpu_count()} visible cores, single-threaded",
-            "seconds": round(dt, 2)}
+    gbs = alg_bytes(lens[:n_seq], 4) / dt / 1e9
+    out["value"] = round(gbs, 3)
+    out["unit"] = "GB/s"
+    out["sample"] = (f"torch CPU decode of one INT4 layer-step over {n_seq} of {S} sequences "
+                     f"({int(lens[:n_seq].sum())} tokens), {dt:.2f}s on {threads} threads")
+
+    # Write: the next step's plan for this layer (positions lens), on the host copy.
+    slots = table[np.arange(S), lens // BS] * BS + lens % BS
+    plan = shared.planner.plan(slots)
+    ps.apply_res_map(plan.res_map_block, plan.res_map_value, plan.res_group_slot, plan.res_group_value)
+    tok = np.stack([plan.tok_slot, plan.tok_res, plan.tok_sealed, plan.tok_kref])
+    kc, vc = kn.float().cpu(), vn.float().cpu()
+    reps = 20
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        TC.write_step(ps, kc, vc, tok, plan.fin)
+    out["write_us_per_layer_step"] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+    out["write_sample"] = f"{S} token rows + {plan.n_fin} completing K groups of one layer, {reps} repeats"
+
+    # Prefill: the last chunk of a 4096-token context, for the 8 longest sequences.
+    rows = [int(r) for r in np.argsort(lens)[-8:]]
+    ctx = min(int(lens[rows].min()), PF_CTX)
+    pq = torch.randn(len(rows) * PF_CHUNK, HQ, D)
+    chunks = [(i * PF_CHUNK, (i + 1) * PF_CHUNK, ctx, 0) for i in range(len(rows))]
+    t0 = time.perf_counter()
+    TC.prefill(ps, pq, chunks, rows, table, D ** -0.5)
+    dt = time.perf_counter() - t0
+    out["prefill_tflops"] = round(prefill_flops(ctx, PF_CHUNK, len(rows)) / dt / 1e12, 4)
+    out["prefill_sample"] = f"{len(rows)} x one {PF_CHUNK}-token chunk over a {ctx}-token INT4 context, {dt:.2f}s"
+
+    # Canary: one layer's per-tier KL.
+    qr = torch.randn(4, HQ, D)
+    kref = torch.randn(64, H, D)
+    reps = 20
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        TC.canary_kl(qr, kref, (2, 4, 8), KG, D ** -0.5)
+    out["canary_us_per_layer"] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+    return out
 
 
 def main():
@@ -581,6 +647,46 @@ def main():
         print(json.dumps({"cfg4": run_cfg4()}), flush=True)
         return
     print(json.dumps(run(args)), flush=True)
+
+
+def plan_only_us(n_seq: int, steps: int = 50) -> float:
+    """Host time of the native planner alone (plan + commit) per decode step of
+    ``n_seq`` sequences at random positions, block 16 / K group 16."""
+    from echokv_amd.write_plan import SharedState
+
+    rng = np.random.default_rng(3)
+    ctx = rng.integers(512, 8193, n_seq)
+    nbs = -(-(ctx + steps + 1) // BS)
+    base = np.concatenate([[0], np.cumsum(nbs)[:-1]])
+    sh = SharedState(int(nbs.sum()), BS, KG, n_seq + 16, kref_window=64, device="cpu")
+    total = 0.0
+    for i in range(steps):
+        pos = ctx + i
+        slots = (base + pos // BS) * BS + pos % BS
+        t0 = time.perf_counter()
+        sh.commit(sh.planner.plan(slots))
+        total += time.perf_counter() - t0
+    return round(total / steps * 1e6, 1)
+
+
+def copy_ceiling(dev, nbytes: int = 1 << 30, reps: int = 10) -> float:
+    """The same run's device-to-device copy rate (bytes read + written per second, GB/s):
+    what a plain streaming kernel reaches on this GPU."""
+    import torch
+
+    a = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del a, b
+    return round(gbs, 1)
 
 
 def copy_calibration(nbytes: int = 1 << 30, reps: int = 5) -> None:
