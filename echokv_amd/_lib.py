@@ -24,7 +24,8 @@ _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 EXPORTS = (
     "echokv_error_string", "echokv_write_tokens", "echokv_finalize_k", "echokv_write_step", "echokv_seal_groups",
     "echokv_gather",
-    "echokv_store_blocks", "echokv_decode", "echokv_decode_static", "echokv_prefill", "echokv_prefill_dense", "echokv_prefill_dense_workspace",
+    "echokv_store_blocks", "echokv_decode", "echokv_decode_static", "echokv_prefill", "echokv_prefill_dense",
+    "echokv_prefill_dense_workspace", "echokv_prefill_own_group",
     "echokv_dequant_dense", "echokv_canary_kl",
 )
 
@@ -61,9 +62,11 @@ _SIGS = {
                       I64, I64, I32, P],
     "echokv_decode_static": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, I32, P,
                              I64, I64, I32, P],
-    "echokv_prefill": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, I32, P, I64, FL, P],
+    "echokv_prefill": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, I32, P, I64, FL, I32, P, P],
+    "echokv_prefill_own_group": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, P, I64, P, I64, I64,
+                                 P, P, I64, I64, I32, FL, P],
     "echokv_prefill_dense": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, P, I64, I32, P, I64,
-                             P, I64, FL, P],
+                             P, I64, FL, I32, P, P],
     "echokv_dequant_dense": [LP, P, P, P, RP, P, I64, P, I64, P, P, I64, I64, I32, P],
     "echokv_canary_kl": [P, I32, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32, I32, I32, I32, I32, I32, FL, P, P,
                          P],

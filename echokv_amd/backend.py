@@ -132,6 +132,7 @@ class EchoKVMetadata:
     prefill_reqs: list  # block-table row of each prefill entry
     prefill_tiles: torch.Tensor | None  # fused-kernel tiles (every chunk <= 64 tokens)
     prefill_dense: object | None  # (DensePlan, workspace) of the two-pass path (longer chunks)
+    own_group_rows: torch.Tensor | None = None  # own-group-exact prefill rows (ECHOKV_OWN_GROUP_EXACT=1)
 
 
 class StepImage:
@@ -370,6 +371,7 @@ class EchoKVMetadataBuilder(AttentionMetadataBuilder):
                 plan = pf.build_dense_plan(prefill, prefill_reqs, self.gqa, dev)
                 nbytes = pf.dense_workspace_bytes(self.impls[0].store, plan.packs.shape[0])
                 prefill_dense = (plan, torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev))
+        og_rows = pf.build_own_group_rows(prefill, prefill_reqs, dev) if prefill and self.cfg.own_group_exact else None
         return EchoKVMetadata(
             num_actual_tokens=t, num_reqs=n, query_start_loc_cpu=cm.query_start_loc_cpu[: n + 1].cpu(),
             seq_lens_cpu=lens_cpu, block_table=cm.block_table_tensor, slot_mapping=cm.slot_mapping, write=write,
@@ -377,7 +379,8 @@ class EchoKVMetadataBuilder(AttentionMetadataBuilder):
             decode_reqs=dec_views[1] if d_idx.size else None, decode_lens=dec_views[2] if d_idx.size else None,
             num_splits=self.num_splits,
             decode_workspace=self.workspace if d_idx.size and d_idx.size <= self.cap else None,
-            prefill=prefill, prefill_reqs=prefill_reqs, prefill_tiles=prefill_tiles, prefill_dense=prefill_dense)
+            prefill=prefill, prefill_reqs=prefill_reqs, prefill_tiles=prefill_tiles, prefill_dense=prefill_dense,
+            own_group_rows=og_rows)
 
     def _plan(self, slots_cpu: torch.Tensor, canary: np.ndarray, decode: tuple):
         """Host side of the step's writes for every layer, then one upload."""
@@ -483,8 +486,12 @@ class EchoKVAttentionImpl(AttentionImpl):
         store = self.store
         out = output.view(output.shape[0], -1, query.shape[-1])
         if md.prefill:
+            og_key = None
+            if md.own_group_rows is not None:  # own-group-exact: this step's key rows, aligned with the queries
+                og_key = key.view(key.shape[0], self.num_kv_heads, self.head_size)
             pf.prefill_attention(store, query, out, md.prefill, md.prefill_reqs, md.block_table, self.scale,
-                                 tiles=md.prefill_tiles, dense=md.prefill_dense)
+                                 tiles=md.prefill_tiles, dense=md.prefill_dense, own_group_key=og_key,
+                                 own_group_rows=md.own_group_rows)
         if md.decode_rows is not None:
             # Query / block-table rows by index, output rows written in place.
             dec.decode_attention(store, query, md.block_table, md.decode_lens, self.scale, q_rows=md.decode_rows,

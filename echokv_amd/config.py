@@ -49,6 +49,7 @@ class EchoKVConfig:
     canary_interval: int = 64
     kref_window: int = 64
     canary_max_q: int = 8
+    own_group_exact: bool = False
     controller: ControllerParams = field(default_factory=ControllerParams)
 
 
@@ -103,6 +104,10 @@ SETTINGS: tuple[Setting, ...] = (
     Setting("ECHOKV_KREF_WINDOW", "kref_window", int, lambda s: 64,
             lambda v, s: None if v >= s["k_group"] else "ECHOKV_KREF_WINDOW must be >= ECHOKV_K_GROUP"),
     Setting("ECHOKV_CANARY_MAX_Q", "canary_max_q", int, lambda s: 8),
+    # This build's own (no reference counterpart): prefill sees each query's own K group
+    # at full precision, as decode did (the fix docs/ECHOKV_VLLM_PLUGIN.md:261-266 names).
+    Setting("ECHOKV_OWN_GROUP_EXACT", "own_group_exact", _flag, lambda s: False,
+            lambda v, s: None if not v or s["k_group"] <= 64 else "ECHOKV_OWN_GROUP_EXACT needs ECHOKV_K_GROUP <= 64"),
 )
 
 _CONTROLLER_KEYS = ("tau0", "l0", "tau_scaling", "alpha", "init_bits", "fixed_bits", "frozen")

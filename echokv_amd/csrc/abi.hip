@@ -254,12 +254,14 @@ int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* 
                    const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
                    int32_t num_q_heads, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
                    const int32_t* tiles, int64_t n_tiles, int32_t tile_m, const int32_t* block_table, int64_t bt_s0,
-                   float softmax_scale, echokv_stream_t stream) {
+                   float softmax_scale, int32_t own_group, float* lse, echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;
   if (L->head_size != 64 && L->head_size != 128) return ECHOKV_ESHAPE;
   if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
   const int gqa = num_q_heads / L->num_kv_heads;
   if (gqa > ek::kPrefillRows || tile_m != ek::prefill_tile_tokens(gqa)) return ECHOKV_ESHAPE;
+  if (own_group != 0 && own_group != 1) return ECHOKV_EINVAL;
+  if (own_group && (L->k_group & (L->k_group - 1))) return ECHOKV_ESHAPE;
   if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
   if (n_tiles < 0 || !res_ok(res)) return ECHOKV_EINVAL;
   if (n_tiles == 0) return ECHOKV_OK;
@@ -284,6 +286,8 @@ int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* 
   a.bt = block_table;
   a.bt_s0 = bt_s0;
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  a.og_mask = own_group ? ~(L->k_group - 1) : 0;
+  a.lse = lse;
   return launched(ek::launch_prefill(a, n_tiles, (hipStream_t)stream));
 }
 
@@ -299,12 +303,15 @@ int echokv_prefill_dense(const echokv_layout* L, const uint8_t* pages, const int
                          int64_t q_s1, int32_t q_dtype, int32_t num_q_heads, void* out, int64_t o_s0, int64_t o_s1,
                          int32_t out_dtype, const int32_t* packs, int64_t n_packs, const int32_t* qtiles,
                          int64_t n_qtiles, int32_t tile_m, const int32_t* block_table, int64_t bt_s0, void* workspace,
-                         int64_t workspace_bytes, float softmax_scale, echokv_stream_t stream) {
+                         int64_t workspace_bytes, float softmax_scale, int32_t own_group, float* lse,
+                         echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;
   if (L->head_size != 64 && L->head_size != 128) return ECHOKV_ESHAPE;
   if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
   const int gqa = num_q_heads / L->num_kv_heads;
   if (gqa > 32 * ek::kDenseWaves || tile_m != ek::dense_tile_tokens(gqa)) return ECHOKV_ESHAPE;
+  if (own_group != 0 && own_group != 1) return ECHOKV_EINVAL;
+  if (own_group && (L->k_group & (L->k_group - 1))) return ECHOKV_ESHAPE;
   if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
   if (n_packs < 0 || n_qtiles < 0 || n_qtiles > INT32_MAX / L->num_kv_heads || !res_ok(res)) return ECHOKV_EINVAL;
   if (n_qtiles == 0) return ECHOKV_OK;
@@ -336,7 +343,58 @@ int echokv_prefill_dense(const echokv_layout* L, const uint8_t* pages, const int
   f.D = L->head_size;
   f.n_packs = n_packs;
   f.scale_log2 = softmax_scale * 1.4426950408889634f;
+  f.og_mask = own_group ? ~(L->k_group - 1) : 0;
+  f.lse = lse;
+  f.hq = num_q_heads;
   return launched(ek::launch_prefill_flash(f, s));
+}
+
+int echokv_prefill_own_group(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                             const int64_t* res_group, const echokv_residual* res, const void* query, int64_t q_s0,
+                             int64_t q_s1, int32_t q_dtype, int32_t num_q_heads, const void* key, int64_t k_s0,
+                             int64_t k_s1, int32_t k_dtype, const int32_t* rows, int64_t n_rows,
+                             const int32_t* block_table, int64_t bt_s0, const float* part, int64_t p_s0, int64_t p_s1,
+                             const float* lse, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                             float softmax_scale, echokv_stream_t stream) {
+  if (!lay_ok(L)) return ECHOKV_ESHAPE;
+  if (L->head_size > ek::kOgMaxD || L->k_group > ek::kOgMaxKeys || (L->k_group & (L->k_group - 1)))
+    return ECHOKV_ESHAPE;
+  if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads || num_q_heads / L->num_kv_heads > ek::kOgMaxGqa)
+    return ECHOKV_ESHAPE;
+  if (!dtype_ok(q_dtype) || !dtype_ok(k_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
+  if (n_rows < 0 || !res_ok(res)) return ECHOKV_EINVAL;
+  if (n_rows == 0) return ECHOKV_OK;
+  if (!pages || !block_res || !res_group || !query || !key || !rows || !block_table || !part || !lse || !out)
+    return ECHOKV_EINVAL;
+  ek::OwnGroupArgs a;
+  a.L = to_lay(L);
+  a.pages = pages;
+  a.block_res = block_res;
+  a.res_group = res_group;
+  a.res = to_res(res);
+  a.q = query;
+  a.q_s0 = q_s0;
+  a.q_s1 = q_s1;
+  a.q_dtype = q_dtype;
+  a.hq = num_q_heads;
+  a.gqa = num_q_heads / L->num_kv_heads;
+  a.key = key;
+  a.k_s0 = k_s0;
+  a.k_s1 = k_s1;
+  a.k_dtype = k_dtype;
+  a.rows = rows;
+  a.bt = block_table;
+  a.bt_s0 = bt_s0;
+  a.part = part;
+  a.p_s0 = p_s0;
+  a.p_s1 = p_s1;
+  a.lse = lse;
+  a.out = out;
+  a.o_s0 = o_s0;
+  a.o_s1 = o_s1;
+  a.out_dtype = out_dtype;
+  a.scale_log2 = softmax_scale * 1.4426950408889634f;
+  return launched(ek::launch_own_group(a, n_rows, (hipStream_t)stream));
 }
 
 int echokv_dequant_dense(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,

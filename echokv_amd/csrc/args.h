@@ -59,6 +59,41 @@ struct StepArgs {
   long n_rows;
 };
 
+// The keys a prefill query at position p sees are those < og_limit(p): p + 1
+// (bottom-right causal), or with own_group on (og_mask = ~(k_group - 1)) the keys
+// before its own K group -- unless p closes the group: decode read that group
+// back quantized, so the whole prefix stays.
+__device__ __forceinline__ int og_limit(int p, int og_mask) {
+  return og_mask && ((p + 1) & ~og_mask) ? (p & og_mask) : p + 1;
+}
+
+// Own-group attention of prefill chunks (own_group_kernel): rows [n, 4] =
+// (query row, position, chunk's first position c0, block-table row).
+constexpr int kOgMaxKeys = 64, kOgMaxD = 128, kOgMaxGqa = 16;
+struct OwnGroupArgs {
+  Lay L;
+  const uint8_t* pages;
+  const int64_t* block_res;
+  const int64_t* res_group;
+  Res res;
+  const void* q;
+  long q_s0, q_s1;
+  int q_dtype, hq, gqa;
+  const void* key;
+  long k_s0, k_s1;
+  int k_dtype;
+  const int32_t* rows;
+  const int32_t* bt;
+  long bt_s0;
+  const float* part;  // [q rows][hq][D] fp32: attention over the keys before each query's group
+  long p_s0, p_s1;
+  const float* lse;   // [q rows][hq]: its log2-domain log-sum-exp (-inf: no such key)
+  void* out;
+  long o_s0, o_s1;
+  int out_dtype;
+  float scale_log2;
+};
+
 struct SealArgs {
   Lay L;
   uint8_t* pages;
@@ -174,6 +209,8 @@ struct PrefillArgs {
   const int32_t* bt;
   long bt_s0;
   float scale_log2;
+  int og_mask;  // nonzero: a query at position p sees keys < (p & og_mask) (its own K group left out)
+  float* lse;   // nullable: [rows, hq] log2-domain log-sum-exp of each query row's scores
 };
 
 struct PackArgs {
@@ -200,6 +237,9 @@ struct FlashArgs {
   int n_qtiles, H, gqa, D;
   long n_packs;  // workspace tiles present: reads stay below this
   float scale_log2;
+  int og_mask;  // as PrefillArgs::og_mask
+  float* lse;   // as PrefillArgs::lse
+  int hq;
 };
 
 // Raise `kernel`'s dynamic-LDS limit to `bytes` on the current device, once per
@@ -224,6 +264,7 @@ hipError_t decode_scratch(void** ptr);
 hipError_t launch_write_tokens(const WriteTokArgs& a, long n_rows, hipStream_t s);
 hipError_t launch_finalize_k(const FinArgs& a, long rows, hipStream_t s);
 hipError_t launch_write_step(const StepArgs& a, hipStream_t s);
+hipError_t launch_own_group(const OwnGroupArgs& a, long n, hipStream_t s);
 hipError_t launch_seal(const SealArgs& a, long n, hipStream_t s);
 hipError_t launch_store_blocks(const StoreBlkArgs& a, long n, hipStream_t s);
 hipError_t launch_gather(const GatherArgs& a, long n, hipStream_t s);

@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   // Query fragments (B operand of S^T): row = 32*wave + 16*rb + n, channels
   // 32j + 8c .. +8 in natural order.
   h8_t qf[2][NQK], qfl[2][QLO ? NQK : 1];
-  int qpos[2];
+  int qpos[2], qlim[2];  // keys < qlim are visible
   bool rvalid[2];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
@@ -59,6 +59,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     const int tok = rvalid[rb] ? r / gqa : 0;
     const int hh = h * gqa + (rvalid[rb] ? r % gqa : 0);
     qpos[rb] = q_pos0 + tok;
+    qlim[rb] = og_limit(qpos[rb], a.og_mask);
     const long qb = (q_row0 + tok) * a.q_s0 + (long)hh * a.q_s1;
 #pragma unroll
     for (int j = 0; j < NQK; ++j) {
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int kp = k0 + 16 * kh + 4 * c + i;
-          const bool ok = kp < kv_end && kp <= qpos[rb];
+          const bool ok = kp < kv_end && kp < qlim[rb];
           const float v = ok ? s[kh][i] * a.scale_log2 : -__builtin_inff();
           p[4 * kh + i] = v;
           mt = fmaxf(mt, v);
@@ -205,6 +206,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     const int r = 32 * wave + 16 * rb + n;
     const long ob = (q_row0 + r / gqa) * a.o_s0 + (long)(h * gqa + r % gqa) * a.o_s1;
     const float inv = l > 0.f ? 1.f / l : 0.f;
+    if (a.lse && c == 0) a.lse[(q_row0 + r / gqa) * a.hq + h * gqa + r % gqa] = l > 0.f ? m_run[rb] + __log2f(l) : -__builtin_inff();
 #pragma unroll
     for (int j = 0; j < NPV; ++j) {
 #pragma unroll

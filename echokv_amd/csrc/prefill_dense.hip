@@ -248,6 +248,8 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
   const bool active = 32 * wave < n_rows;
   const int qpos = q_pos0 + r / gqa;
   const int qmin = q_pos0 + (32 * wave) / gqa;
+  const int qlim = og_limit(qpos, a.og_mask);                      // keys < qlim are visible
+  const int qlim_min = a.og_mask ? (qmin & a.og_mask) : qmin + 1;  // at most the wave's smallest limit
   const int kend_w = active ? min(kv_end, q_pos0 + last_r / gqa + 1) : 0;  // keys this wave needs
 
   // DMA lane offsets inside a workspace tile (swizzled so that LDS reads are
@@ -363,13 +365,13 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
   auto softmax = [&](int kbase) {
     __builtin_amdgcn_sched_barrier(0);
     // Causal / context limit, only where this tile reaches it.
-    if (kbase + kDenseKeys > qmin + 1 || kbase + kDenseKeys > kv_end) {
+    if (kbase + kDenseKeys > qlim_min || kbase + kDenseKeys > kv_end) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int kk = kbase + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
-          if (!(kk < kv_end && kk <= qpos)) s[kb][i] = -kInf;
+          if (!(kk < kv_end && kk < qlim)) s[kb][i] = -kInf;
         }
       }
     }
@@ -448,6 +450,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
   if (!rv) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   const long ob = (q_row0 + r / gqa) * a.o_s0 + (long)(h * gqa + r % gqa) * a.o_s1;
+  if (a.lse && hh == 0) a.lse[(q_row0 + r / gqa) * a.hq + h * gqa + r % gqa] = l > 0.f ? m_run + __log2f(l) : -kInf;
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
 #pragma unroll

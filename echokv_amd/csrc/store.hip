@@ -458,6 +458,81 @@ __device__ __forceinline__ void dequant_token4(const Lay& L, const uint8_t* page
   }
 }
 
+// ---------------------------------------------------------------------------
+// Own-group attention of a prefill chunk, merged into the rest. A query at
+// position p attends to its own K group [p & ~(KG-1), p] with the keys at full
+// precision -- this step's key rows where the chunk holds them (positions >= c0),
+// the cache before that -- and V from the cache, as decode saw those keys while
+// the group was open; the prefill kernels attended to every key before the group
+// (part_o, fp32, normalized, and its log2-domain log-sum-exp). The two merge by
+// log-sum-exp into `out`. One workgroup per (query token, KV head).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void own_group_kernel(OwnGroupArgs a) {
+  const Lay& L = a.L;
+  const int32_t* rw = a.rows + (long)blockIdx.x * 4;
+  const long q_row = rw[0];
+  const int p = rw[1], c0 = rw[2];
+  const long bt_row = rw[3];
+  const int h = blockIdx.y;
+  const int gs = p & ~(L.KG - 1);
+  // A query closing its group saw the whole prefix from the cache (the prefill
+  // kernels took it): no own part.
+  const int nk = ((p + 1) & (L.KG - 1)) ? p - gs + 1 : 0;  // <= KG <= kOgMaxKeys
+  const int quads = L.D / 4;
+  __shared__ float ks[kOgMaxKeys][kOgMaxD], vs[kOgMaxKeys][kOgMaxD], qs[kOgMaxGqa][kOgMaxD];
+  __shared__ float sc[kOgMaxGqa][kOgMaxKeys];
+  // K and V of the group's keys (4 channels per item).
+  for (int i = threadIdx.x; i < nk * quads; i += kThreads) {
+    const int j = i / quads, c = i % quads;
+    const int pos = gs + j;
+    const long blk = a.bt[bt_row * a.bt_s0 + pos / L.BS];
+    float k[4] = {0.f, 0.f, 0.f, 0.f}, v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (blk >= 0 && blk < L.nb) {
+      const int bits = tier_of(a.pages[blk * L.stride]);
+      dequant_token4(L, a.pages, a.block_res, a.res_group, a.res, blk, pos % L.BS, bits, h, c, k, v);
+    }
+    if (pos >= c0) ld4(a.key, a.k_dtype, (q_row - (p - pos)) * a.k_s0 + (long)h * a.k_s1 + 4 * c, k);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ks[j][4 * c + e] = k[e];
+      vs[j][4 * c + e] = v[e];
+    }
+  }
+  for (int i = threadIdx.x; i < a.gqa * L.D; i += kThreads) {
+    const int g = i / L.D, d = i % L.D;
+    qs[g][d] = ld(a.q, a.q_dtype, q_row * a.q_s0 + (long)(h * a.gqa + g) * a.q_s1 + d);
+  }
+  __syncthreads();
+  // Scores (log2 units).
+  for (int i = threadIdx.x; i < a.gqa * nk; i += kThreads) {
+    const int g = i / nk, j = i % nk;
+    float x = 0.f;
+    for (int d = 0; d < L.D; ++d) x = __builtin_fmaf(qs[g][d], ks[j][d], x);
+    sc[g][j] = x * a.scale_log2;
+  }
+  __syncthreads();
+  // Softmax over the group per query head, then the merge with the earlier keys.
+  for (int i = threadIdx.x; i < a.gqa * L.D; i += kThreads) {
+    const int g = i / L.D, d = i % L.D;
+    float m = -__builtin_inff();
+    for (int j = 0; j < nk; ++j) m = fmaxf(m, sc[g][j]);
+    float l = 0.f, o = 0.f;
+    for (int j = 0; j < nk; ++j) {
+      const float w = __builtin_amdgcn_exp2f(sc[g][j] - m);
+      l += w;
+      o = __builtin_fmaf(w, vs[j][d], o);
+    }
+    const long qh = (long)h * a.gqa + g;
+    const float lse_b = nk ? m + __log2f(l) : -__builtin_inff();
+    const float lse_a = a.lse[q_row * a.hq + qh];
+    const float o_a = a.part[q_row * a.p_s0 + qh * a.p_s1 + d];
+    const float mm = fmaxf(lse_a, lse_b);
+    const float wa = lse_a == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(lse_a - mm);
+    const float wb = nk ? __builtin_amdgcn_exp2f(lse_b - mm) : 0.f;
+    st(a.out, a.out_dtype, q_row * a.o_s0 + qh * a.o_s1 + d, nk ? (wa * o_a + wb * (o / l)) / (wa + wb) : o_a);
+  }
+}
+
 // gather (echokv_vllm/tiered_cache.py:451-478): never-opened blocks read as zeros.
 
 __global__ __launch_bounds__(kThreads) void gather_kernel(GatherArgs a) {
@@ -543,6 +618,10 @@ hipError_t launch_store_blocks(const StoreBlkArgs& a, long n, hipStream_t s) {
 }
 hipError_t launch_gather(const GatherArgs& a, long n, hipStream_t s) {
   hipLaunchKernelGGL(gather_kernel, dim3((unsigned)n), dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+hipError_t launch_own_group(const OwnGroupArgs& a, long n, hipStream_t s) {
+  hipLaunchKernelGGL(own_group_kernel, dim3((unsigned)n, (unsigned)a.L.H), dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 hipError_t launch_dequant_dense(const DenseArgs& a, long n, hipStream_t s) {

@@ -154,11 +154,12 @@ def use_dense(prefill, head_size: int) -> bool:
 
 def prefill_attention_dense(store, query: torch.Tensor, output: torch.Tensor, prefill, req_of,
                             block_table: torch.Tensor, softmax_scale: float, plan: DensePlan | None = None,
-                            workspace: torch.Tensor | None = None) -> None:
+                            workspace: torch.Tensor | None = None, lse: torch.Tensor | None = None) -> None:
     """Two-pass prefill (echokv_vllm/kernels/prefill.py:133-167): dequantize each
     context once into a workspace of 64-key tiles, then flash attention over it.
     ``plan`` / ``workspace`` (uint8, ``dense_workspace_bytes``) may be built once per
-    step and shared by every layer."""
+    step and shared by every layer. With ``lse`` (float32 ``[T, Hq]``) each query's
+    own K group is left out and the rows' log-sum-exp written (own-group-exact part 1)."""
     if not prefill:
         return
     L = store.layout
@@ -187,33 +188,94 @@ def prefill_attention_dense(store, query: torch.Tensor, output: torch.Tensor, pr
         _lib.ptr(store.res_group), _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1),
         _lib.dtype_code(query), hq, _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out),
         _lib.ptr(plan.packs), n_packs, _lib.ptr(plan.qtiles), n_q, plan.tile_m, _lib.ptr(block_table),
-        block_table.stride(0), _lib.ptr(ws), ws_bytes, float(softmax_scale), _lib.stream(),
+        block_table.stride(0), _lib.ptr(ws), ws_bytes, float(softmax_scale), int(lse is not None), _lib.ptr(lse),
+        _lib.stream(),
     )
 
 
 def prefill_attention(store, query: torch.Tensor, output: torch.Tensor, prefill, req_of, block_table: torch.Tensor,
-                      softmax_scale: float, tiles: torch.Tensor | None = None, gather=None, dense=None) -> None:
+                      softmax_scale: float, tiles: torch.Tensor | None = None, gather=None, dense=None,
+                      own_group_key: torch.Tensor | None = None, own_group_rows: torch.Tensor | None = None) -> None:
     """Write attention for every prefill chunk into ``output [T, Hq, D]``.
 
     A batch with a chunk longer than ``FUSED_MAX_CHUNK`` takes the two-pass
     path; ``dense`` carries its step-wide inputs, built once for every layer: a
     ``DensePlan`` or ``(DensePlan, workspace)`` (the reference builder's dense
     tuple has the same role). Otherwise the fused kernel over ``tiles``.
-    ``gather`` (the reference's PyTorch-path index) is accepted and unused."""
+    ``gather`` (the reference's PyTorch-path index) is accepted and unused.
+
+    ``own_group_key`` (this step's key rows ``[T, H, D]``, aligned with the query
+    rows) turns on own-group-exact attention: each query sees its own K group at
+    full precision, as decode saw it while the group was open (the chunk's keys
+    from ``own_group_key``, earlier ones of the group from the cache); the rest of
+    the context as usual. ``own_group_rows`` (``own_group_rows(prefill, req_of)``)
+    may be built once per step."""
     if not prefill:
         return
+    part, lse = output, None
+    if own_group_key is not None:
+        n = query.shape[0]
+        part = torch.empty(n, query.shape[1], store.layout.head_size, device=query.device, dtype=torch.float32)
+        lse = torch.empty(n, query.shape[1], device=query.device, dtype=torch.float32)
     if use_dense(prefill, store.layout.head_size):
         plan, ws = (dense, None) if isinstance(dense, DensePlan) else (dense or (None, None))
         if plan is not None and not isinstance(plan, DensePlan):
             raise ValueError("dense must be a DensePlan or a (DensePlan, workspace) pair")
-        prefill_attention_dense(store, query, output, prefill, req_of, block_table, softmax_scale, plan, ws)
+        prefill_attention_dense(store, query, part, prefill, req_of, block_table, softmax_scale, plan, ws, lse)
     else:
-        prefill_attention_fused(store, query, output, prefill, req_of, block_table, softmax_scale, tiles)
+        prefill_attention_fused(store, query, part, prefill, req_of, block_table, softmax_scale, tiles, lse)
+    if own_group_key is not None:
+        rows = own_group_rows if own_group_rows is not None else build_own_group_rows(prefill, req_of, query.device)
+        own_group_merge(store, query, own_group_key, rows, block_table, part, lse, output, softmax_scale)
+
+
+def build_own_group_rows(prefill, req_of, device) -> torch.Tensor:
+    """Rows ``[T, 4]`` int32 of the own-group part: (query row, position, the chunk's
+    first position, block-table row) per query token."""
+    parts = []
+    for (qs, qe, ctx, *_), r in zip(prefill, req_of):
+        nq = qe - qs
+        c0 = ctx - nq
+        i = torch.arange(nq, dtype=torch.int32)
+        parts.append(torch.stack([qs + i, c0 + i, torch.full_like(i, c0), torch.full_like(i, r)], 1))
+    rows = torch.cat(parts) if parts else torch.zeros(0, 4, dtype=torch.int32)
+    return to_device(rows.contiguous(), device)
+
+
+def own_group_merge(store, query: torch.Tensor, key: torch.Tensor, rows: torch.Tensor, block_table: torch.Tensor,
+                    part: torch.Tensor, lse: torch.Tensor, output: torch.Tensor, softmax_scale: float) -> None:
+    """Own-group-exact part 2 (``echokv_prefill_own_group``): each row's own K group
+    with full-precision keys, merged with ``part`` / ``lse`` into ``output``."""
+    if rows.shape[0] == 0:
+        return
+    L = store.layout
+    _lib.require_device(query, key, rows, block_table, part, lse, output, store.pages)
+    hq = query.shape[1]
+    if query.stride(2) != 1:
+        query = query.contiguous()
+    if key.stride(2) != 1:
+        key = key.contiguous()
+    if part.dtype != torch.float32 or part.stride(2) != 1 or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("part must be float32 rows, lse float32 [T, Hq] contiguous")
+    out = _out_view(output, hq)
+    rows = rows.to(torch.int32).contiguous()
+    block_table = _bt(block_table)
+    res = _lib.residual(store.res_k)
+    _lib.call(
+        "echokv_prefill_own_group", _lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(store.block_res),
+        _lib.ptr(store.res_group), _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1),
+        _lib.dtype_code(query), hq, _lib.ptr(key), key.stride(0), key.stride(1), _lib.dtype_code(key),
+        _lib.ptr(rows), rows.shape[0], _lib.ptr(block_table), block_table.stride(0), _lib.ptr(part), part.stride(0),
+        part.stride(1), _lib.ptr(lse), _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out),
+        float(softmax_scale), _lib.stream(),
+    )
 
 
 def prefill_attention_fused(store, query: torch.Tensor, output: torch.Tensor, prefill, req_of,
-                            block_table: torch.Tensor, softmax_scale: float, tiles: torch.Tensor | None = None) -> None:
-    """The fused kernel (echokv_vllm/kernels/prefill.py:242-327) over ``tiles``."""
+                            block_table: torch.Tensor, softmax_scale: float, tiles: torch.Tensor | None = None,
+                            lse: torch.Tensor | None = None) -> None:
+    """The fused kernel (echokv_vllm/kernels/prefill.py:242-327) over ``tiles``; ``lse`` as
+    for ``prefill_attention_dense``."""
     if not prefill:
         return
     L = store.layout
@@ -235,5 +297,5 @@ def prefill_attention_fused(store, query: torch.Tensor, output: torch.Tensor, pr
         _lib.ptr(store.res_group), _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1),
         _lib.dtype_code(query), hq, _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out),
         _lib.ptr(tiles), tiles.shape[0], block_m(gqa), _lib.ptr(block_table), block_table.stride(0),
-        float(softmax_scale), _lib.stream(),
+        float(softmax_scale), int(lse is not None), _lib.ptr(lse), _lib.stream(),
     )

@@ -159,7 +159,10 @@ int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int
 
 /* Chunked-prefill attention over the tiered pages (MFMA tiles), bottom-right causal:
  * tiles [n_tiles, 5] int32 = (first query row, tokens, first query position, ctx,
- * block-table row); each tile holds <= tile_m query tokens.
+ * block-table row); each tile holds <= tile_m query tokens. own_group = 1 leaves
+ * each query's own K group out (a query at p sees keys < p & ~(k_group - 1); k_group
+ * a power of two); lse (nullable, float [query rows, num_q_heads]) receives each
+ * row's log2-domain log-sum-exp of the scaled scores (-inf: no visible key).
  * Replaces echokv_vllm/kernels/prefill.py:170-207 (prefill_attention: the fused kernel
  * prefill.py:242-327 and the dense dequant + flash-attention path prefill.py:133-167). */
 int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
@@ -168,7 +171,7 @@ int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* 
                    void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
                    const int32_t* tiles, int64_t n_tiles, int32_t tile_m,
                    const int32_t* block_table, int64_t bt_s0, float softmax_scale,
-                   echokv_stream_t stream);
+                   int32_t own_group, float* lse, echokv_stream_t stream);
 
 /* Long-chunk prefill in two passes (the dense path for chunks longer than the fused
  * kernel's): each 64-key tile of every context is dequantized once into `workspace`
@@ -177,6 +180,7 @@ int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* 
  * flash attention on MFMA reads it: qtiles [n_qtiles, 5] int32 = (first query row,
  * tokens <= tile_m = 256 / GQA, first query position, ctx, first workspace tile of
  * the request's context), bottom-right causal. Workspace reads stay below n_packs tiles.
+ * own_group / lse as for echokv_prefill.
  * Replaces echokv_vllm/kernels/prefill.py:133-167 (prefill_attention_dense:
  * dequant_dense prefill.py:90-115 + flash-attention varlen).
  * echokv_prefill_dense_workspace: the workspace bytes for n_packs tiles, or minus an
@@ -189,7 +193,27 @@ int echokv_prefill_dense(const echokv_layout* L, const uint8_t* pages, const int
                          const int32_t* packs, int64_t n_packs, const int32_t* qtiles, int64_t n_qtiles,
                          int32_t tile_m, const int32_t* block_table, int64_t bt_s0,
                          void* workspace, int64_t workspace_bytes, float softmax_scale,
-                         echokv_stream_t stream);
+                         int32_t own_group, float* lse, echokv_stream_t stream);
+
+/* Own-group-exact prefill, second part: each query attends to its own K group with
+ * full-precision keys -- this step's key rows (key, aligned with the query rows)
+ * at positions >= the chunk's first position, the cache before it -- and cached V,
+ * as decode saw the group while it was open; the result merges by log-sum-exp with
+ * part (fp32 [query rows, num_q_heads, D], strides p_s0 / p_s1) and lse, the output
+ * of echokv_prefill / echokv_prefill_dense with own_group = 1, into out.
+ * rows [n_rows, 4] int32 = (query row, position, chunk's first position, block-table
+ * row). k_group <= 64 (a power of two), head_size <= 128, GQA <= 16.
+ * No counterpart in the reference: its docs/ECHOKV_VLLM_PLUGIN.md:261-266 names this
+ * fix for preempted / re-chunked requests (prefill sees its own group quantized where
+ * decode saw it exact) and leaves it open. */
+int echokv_prefill_own_group(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
+                             const int64_t* res_group, const echokv_residual* res,
+                             const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype, int32_t num_q_heads,
+                             const void* key, int64_t k_s0, int64_t k_s1, int32_t k_dtype,
+                             const int32_t* rows, int64_t n_rows, const int32_t* block_table, int64_t bt_s0,
+                             const float* part, int64_t p_s0, int64_t p_s1, const float* lse,
+                             void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                             float softmax_scale, echokv_stream_t stream);
 
 /* Dense dequantization of prefill contexts: work [n, 4] int32 = (block-table row,
  * block index, dense row of the block's first token, ctx) -> K, V [*, H, D].

@@ -60,6 +60,38 @@ def prefill_attention(store, query, prefill, req_of, block_table, scale, vectori
     return out
 
 
+def prefill_own_group_exact(store, query, key, prefill, req_of, block_table, scale):
+    """Prefill with own-group-exact semantics (no counterpart in the reference code:
+    ``echokv_vllm`` docs/ECHOKV_VLLM_PLUGIN.md:261-266 describe it as the fix for
+    preempted / re-chunked requests): each query attends as decode did when it was
+    the newest token. Query ``p`` of a chunk starting at ``c0`` sees the cache
+    (``gather``) for keys before its own K group ``[p - p % kg, p]``, and within
+    that group the keys as decode saw them while the group was open: full
+    precision -- ``key`` rows of this chunk (aligned with the query rows) at
+    positions ``>= c0``, the cache before -- with cached V. The group's last
+    position is the exception: its write completed the group, which decode then
+    read back quantized, so that query sees the cache throughout. Float64."""
+    kg = store.L.kg
+    out = np.zeros(query.shape, np.float64)
+    for (qs, qe, ctx, _), r in zip(prefill, req_of):
+        nq = qe - qs
+        c0 = ctx - nq
+        pos = np.arange(ctx)
+        k, v = store.gather_vec(np.asarray(block_table[r], np.int64)[pos // store.L.bs], pos % store.L.bs)
+        for g0 in range((c0 // kg) * kg, ctx, kg):  # the own groups of the chunk's queries
+            lo, hi = max(g0, c0), min(g0 + kg - 1, ctx)  # open-group queries (and exact keys) in the chunk
+            if hi > lo:
+                kx = k[:hi].copy()
+                kx[lo:hi] = key[qs + lo - c0 : qs + hi - c0]
+                out[qs + lo - c0 : qs + hi - c0] = attend_causal(query[qs + lo - c0 : qs + hi - c0], kx, v[:hi],
+                                                                 scale)
+            last = g0 + kg - 1  # the group's closing query: the cache throughout
+            if c0 <= last < ctx:
+                out[qs + last - c0] = attend_causal(query[qs + last - c0 : qs + last - c0 + 1], k[: last + 1],
+                                                    v[: last + 1], scale)[0]
+    return out
+
+
 def attend_causal(q, k, v, scale):
     """``q [nq, Hq, D]`` over ``k, v [n, H, D]`` with the bottom-right causal limit
     (query i sees keys < n - nq + i + 1), float64, one matrix product per head."""

@@ -79,13 +79,29 @@ def test_store_entry_points_reject_bad_layouts(lib):
     assert rc != 0  # bits must be 2, 4 or 8
 
 
-def _prefill_dense(lib, L, hq=32, tile_m=64, n_packs=4, n_q=2, ws_bytes=None):
+def _prefill_dense(lib, L, hq=32, tile_m=64, n_packs=4, n_q=2, ws_bytes=None, own_group=0):
     res = _lib.Residual(C.c_void_p(16), 1, 2, 16 * 8 * 128, 8 * 128, 128)
     p = C.c_void_p(64)  # never dereferenced: every call below fails its checks first
     if ws_bytes is None:
         ws_bytes = lib.echokv_prefill_dense_workspace(C.byref(L), n_packs)
     return lib.echokv_prefill_dense(C.byref(L), p, p, p, C.byref(res), p, 4096, 128, 1, hq, p, 4096, 128, 1, p,
-                                    n_packs, p, n_q, tile_m, p, 64, p, ws_bytes, 0.088, None)
+                                    n_packs, p, n_q, tile_m, p, 64, p, ws_bytes, 0.088, own_group, None, None)
+
+
+def _own_group(lib, L, hq=32, n=2):
+    res = _lib.Residual(C.c_void_p(16), 1, 2, 16 * 8 * 128, 8 * 128, 128)
+    p = C.c_void_p(64)  # never dereferenced: every call below fails its checks first
+    return lib.echokv_prefill_own_group(C.byref(L), p, p, p, C.byref(res), p, 4096, 128, 1, hq, p, 1024, 128, 1,
+                                        p, n, p, 64, p, 4096, 128, p, p, 4096, 128, 1, 0.088, None)
+
+
+def test_own_group_prefill_argument_checks(lib):
+    L = _layout()
+    assert _prefill_dense(lib, L, own_group=2) == 1            # own_group is 0 or 1
+    assert _own_group(lib, _layout(head_size=256)) == 2        # head_size <= 128
+    assert _own_group(lib, L, hq=8 * 32) == 2                  # GQA <= 16
+    assert _own_group(lib, L, n=-1) == 1
+    assert _own_group(lib, L, n=0) == 0                        # nothing to do: no launch
 
 
 def test_prefill_dense_workspace_size_and_argument_checks(lib):

@@ -75,6 +75,7 @@ def test_defaults_and_budget_rules():
     assert [default_init_bits(m) for m in (2, 4, 6, 8)] == [2, 4, 4, 8]
     assert load_config({"ECHOKV_FROZEN": "1"}).controller.frozen
     assert load_config({"ECHOKV_MEM_BITS": ""}).mem_bits == 4  # empty = unset
+    assert not cfg.own_group_exact and load_config({"ECHOKV_OWN_GROUP_EXACT": "1"}).own_group_exact
 
 
 def test_environment_is_read(monkeypatch):
@@ -95,6 +96,7 @@ def test_environment_is_read(monkeypatch):
     ({"ECHOKV_TAU_SCALING": "log"}, "ECHOKV_TAU_SCALING"),
     ({"ECHOKV_CANARY_INTERVAL": "0"}, "ECHOKV_CANARY_INTERVAL"),
     ({"ECHOKV_KREF_WINDOW": "16"}, "ECHOKV_KREF_WINDOW"),  # below the default K group of 32
+    ({"ECHOKV_OWN_GROUP_EXACT": "1", "ECHOKV_K_GROUP": "128", "ECHOKV_KREF_WINDOW": "128"}, "ECHOKV_OWN_GROUP_EXACT"),
 ])
 def test_bad_values_raise_value_error_naming_the_variable(env, name):
     with pytest.raises(ValueError, match=name):
@@ -103,7 +105,7 @@ def test_bad_values_raise_value_error_naming_the_variable(env, name):
 
 def test_every_variable_has_one_row():
     envs = [s.env for s in SETTINGS]
-    assert len(envs) == len(set(envs)) == 14
+    assert len(envs) == len(set(envs)) == 15
 
 
 # ---- canary.py:19-56 -----------------------------------------------------------------

@@ -36,12 +36,13 @@ def oracle_of(impl):
                              st.res_group.cpu().numpy())
 
 
-@pytest.fixture
-def env(monkeypatch):
+@pytest.fixture(params=["plain", "own-group"])
+def env(monkeypatch, request):
     for k, v in {"ECHOKV_K_GROUP": "16", "ECHOKV_MEM_BITS": "8", "ECHOKV_CANARY_INTERVAL": "2",
-                 "ECHOKV_KREF_WINDOW": "32", "ECHOKV_RESIDUAL_SLOTS": "24"}.items():
+                 "ECHOKV_KREF_WINDOW": "32", "ECHOKV_RESIDUAL_SLOTS": "24",
+                 "ECHOKV_OWN_GROUP_EXACT": "1" if request.param == "own-group" else "0"}.items():
         monkeypatch.setenv(k, v)
-    yield
+    yield request.param == "own-group"
     _vllm.set_forward_metadata(None)
 
 
@@ -169,11 +170,15 @@ def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
     worst = 0.0
     for li, layer in enumerate(layers):
         ps = oracle_of(layer.impl)
-        ref = OA.prefill_attention(ps, q[li].float().cpu().numpy(), md.prefill, md.prefill_reqs, table_np,
-                                   D ** -0.5, vectorized=True)
+        if env:  # own-group-exact prefill: each query's own K group from this step's keys
+            ref = OA.prefill_own_group_exact(ps, q[li].float().cpu().numpy(), k[li].float().cpu().numpy(),
+                                             md.prefill, md.prefill_reqs, table_np, D ** -0.5)
+        else:
+            ref = OA.prefill_attention(ps, q[li].float().cpu().numpy(), md.prefill, md.prefill_reqs, table_np,
+                                       D ** -0.5, vectorized=True)
         worst = max(worst, maxdiff(outs[li].view(-1, HQ, D), ref))
         assert int(layer.impl.store.tag[table_np[1, 0]]) == layer.impl.controller.bits
-    print(f"[backend prefill] max err {worst:.3e}", flush=True)
+    print(f"[backend prefill{' own-group' if env else ''}] max err {worst:.3e}", flush=True)
     assert worst <= TOL
 
     lens = list(PROMPTS)
