@@ -164,3 +164,49 @@ def test_hip_own_group_off_leaves_prefill_unchanged(device, decode_time):
     plain = OA.prefill_attention(ps, q.astype(np.float32), [(0, N, N, 0)], [0], s.meta["table"], D ** -0.5,
                                  vectorized=True)
     assert maxdiff(out, plain) <= 2e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("own_group", [False, True], ids=["plain", "own-group"])
+def test_hip_prefix_cached_request_reads_the_shared_blocks(device, decode_time, own_group):
+    """Prefix caching: request B's block table starts with request A's three blocks
+    (48 tokens, written by A); B writes only its own tokens 48..99 into fresh
+    blocks, then prefills that chunk over the whole context. Its attention equals
+    the oracle's over the same pages, and equals what B gets had it written the
+    whole sequence itself (the shared prefix holds the same bytes)."""
+    from echokv_amd.kernels import prefill as pf
+    from gpu_util import gpu_store, maxdiff
+    from oracle import store as OS
+
+    ref, k, v, q = decode_time
+    nb = -(-N // BS)
+    s = script([48, N - 48])
+    s.num_blocks = 2 * nb + 2
+    store, *_ = gpu_store(s, device)
+    table_a = np.arange(nb)
+    table_b = np.concatenate([table_a[:3], nb + np.arange(nb - 3)])  # shares A's first three blocks
+    pos = np.arange(48)
+    store.write(torch.from_numpy(k[:48]).to(device), torch.from_numpy(v[:48]).to(device),
+                torch.from_numpy(table_a[pos // BS] * BS + pos % BS).to(device), 4)
+    pos = np.arange(48, N)
+    kb = torch.from_numpy(k[48:]).to(device)
+    store.write(kb, torch.from_numpy(v[48:]).to(device), torch.from_numpy(table_b[pos // BS] * BS + pos % BS).to(device),
+                4)
+    table = torch.from_numpy(np.stack([table_a, table_b])).to(device, torch.int32)
+    out = torch.zeros(N - 48, HQ, D, device=device)
+    prefill = [(0, N - 48, N, 0)]
+    pf.prefill_attention(store, torch.from_numpy(q[48:]).to(device), out, prefill, [1], table, D ** -0.5,
+                         own_group_key=kb if own_group else None)
+    torch.cuda.synchronize()
+    L = store.layout
+    ps = OS.PageStore.over(OS.Layout(L.num_kv_heads, L.head_size, L.block_size, L.mem_bits, L.k_group, L.v_group),
+                           store.pages.cpu().numpy(), store.res_k.float().cpu().numpy(),
+                           store.block_res.cpu().numpy(), store.res_group.cpu().numpy())
+    tb = np.stack([table_a, table_b])
+    if own_group:
+        oracle = OA.prefill_own_group_exact(ps, q[48:].astype(np.float32), k[48:].astype(np.float32), prefill, [1],
+                                            tb, D ** -0.5)
+        assert maxdiff(out, ref[48:]) <= 2e-3  # and what decode saw, token by token
+    else:
+        oracle = OA.prefill_attention(ps, q[48:].astype(np.float32), prefill, [1], tb, D ** -0.5, vectorized=True)
+    assert maxdiff(out, oracle) <= 2e-3
