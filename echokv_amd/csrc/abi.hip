@@ -159,7 +159,6 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   if (L->k_group < 16) return ECHOKV_ESHAPE;
   if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
   const int gqa = num_q_heads / L->num_kv_heads;
-  if (gqa > 16) return ECHOKV_ESHAPE;
   if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
   if (num_seqs < 0 || num_splits <= 0 || blocks_per_split <= 0 || !res_ok(res)) return ECHOKV_EINVAL;
   if (tier != 2 && tier != 4 && tier != 8) return ECHOKV_EINVAL;
@@ -215,12 +214,23 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   a.out_dtype = out_dtype;
   a.ranges = 0;
   if (!(flags & ECHOKV_DECODE_BATCH_INVARIANT) && ek::decode_ranges(a, a.ranges) != hipSuccess) return ECHOKV_ELAUNCH;
-  hipError_t e = ek::launch_decode(a, num_seqs, (hipStream_t)stream);
-  if (e != hipSuccess) return ECHOKV_ELAUNCH;
-  if (a.ranges > 0) return launched(ek::launch_merge_balanced(a, (hipStream_t)stream));
-  ek::MergeArgs m{acc, ml, seq_lens, q_rows, out, o_s0, o_s1, out_dtype, num_q_heads, L->head_size,
-                  L->block_size, num_splits, blocks_per_split, num_seqs * num_q_heads};
-  return launched(ek::launch_merge(m, num_seqs, (hipStream_t)stream));
+  // A wave's MFMA columns hold 16 query heads: a larger GQA runs in passes of 16
+  // query heads per KV head (each pass reads the cache again; their rows are disjoint).
+  for (int g0 = 0; g0 < gqa; g0 += 16) {
+    a.g0 = g0;
+    a.gs = gqa - g0 < 16 ? gqa - g0 : 16;
+    if (ek::launch_decode(a, num_seqs, (hipStream_t)stream) != hipSuccess) return ECHOKV_ELAUNCH;
+    hipError_t e;
+    if (a.ranges > 0) {
+      e = ek::launch_merge_balanced(a, (hipStream_t)stream);
+    } else {
+      ek::MergeArgs m{acc, ml, seq_lens, q_rows, out, o_s0, o_s1, out_dtype, num_q_heads, L->head_size,
+                      L->block_size, num_splits, blocks_per_split, num_seqs * num_q_heads, gqa, a.g0, a.gs};
+      e = ek::launch_merge(m, num_seqs, (hipStream_t)stream);
+    }
+    if (e != hipSuccess) return ECHOKV_ELAUNCH;
+  }
+  return ECHOKV_OK;
 }
 
 }  // namespace

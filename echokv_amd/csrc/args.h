@@ -146,6 +146,7 @@ struct DecodeArgs {
   const void* q;
   long q_s0, q_s1;
   int q_dtype, hq, gqa;
+  int g0, gs;  // this pass's query heads of each KV head: [g0, g0 + gs), gs <= 16
   const int64_t* q_rows;
   const int32_t* bt;
   long bt_s0;
@@ -179,6 +180,7 @@ struct MergeArgs {
   long o_s0, o_s1;
   int out_dtype, hq, D, BS, num_splits, bps;
   long rows;  // num_seqs * hq
+  int gqa, g0, gs;  // rows of query heads g0 .. g0 + gs - 1 of each KV head only
 };
 
 struct CanaryArgs {

@@ -967,8 +967,8 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
 
   W w;
   {
-    const bool qv = live && n < a.gqa;
-    const long qb = q_row * a.q_s0 + (long)(h * a.gqa + (qv ? n : 0)) * a.q_s1 + c * W::CPL;
+    const bool qv = live && n < a.gs;
+    const long qb = q_row * a.q_s0 + (long)(h * a.gqa + a.g0 + (qv ? n : 0)) * a.q_s1 + c * W::CPL;
     float xq[W::CPL];
     // Scores are scaled inside the exponent (exp2(s * x - m)); the max is taken
     // on unscaled scores, which needs the scale positive: a negative one flips
@@ -1083,8 +1083,8 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   }
 
   const float l = rows_sum(w.l_lane);
-  if (live && n < a.gqa) {
-    const long qh = (long)h * a.gqa + n;
+  if (live && n < a.gs) {
+    const long qh = (long)h * a.gqa + a.g0 + n;
     if (sink.direct) {  // lane (c, n): channels (4c + i) * CPM + j of query head qh
       const float inv = 1.0f / l;
       const long o = q_row * a.o_s0 + qh * a.o_s1;
@@ -1256,6 +1256,7 @@ __global__ __launch_bounds__(256) void merge_balanced_kernel(DecodeArgs a) {
   if (row >= a.num_seqs * a.hq) return;
   const long seq = row / a.hq;
   const int head = (int)(row % a.hq);
+  if (head % a.gqa < a.g0 || head % a.gqa >= a.g0 + a.gs) return;  // another pass's query heads
   const int nb = seq_blocks(a, seq);
   if (nb == 0) return;
   long first = 0;
@@ -1401,6 +1402,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   if (row >= a.rows) return;
   const long seq = row / a.hq;
   const int head = (int)(row % a.hq);
+  if (head % a.gqa < a.g0 || head % a.gqa >= a.g0 + a.gs) return;  // another pass's query heads
   const int seq_len = (int)a.lens[seq];
   if (seq_len <= 0) return;
   const int n_blocks = (seq_len + a.BS - 1) / a.BS;

@@ -67,6 +67,26 @@ def test_decode_matches_oracle(device, case_stores, i, bps, qdt, inv):
         assert err <= TOL, f"{s.name} gqa={gqa} bps={bps}: max err {err}"
 
 
+@pytest.mark.parametrize("gqa", [17, 32])
+@pytest.mark.parametrize("inv", [False, True], ids=["balanced", "split"])
+def test_decode_gqa_above_16_matches_oracle(device, case_stores, gqa, inv):
+    """GQA beyond one MFMA column block (16 query heads per KV head) runs in passes
+    of 16 query heads; every query head's row against the oracle."""
+    for i in (0, 3):
+        s, sim, store = case_stores[i]
+        print(f"[decode] {s.name} gqa={gqa}", flush=True)
+        table = t(s.meta["table"], device, torch.int32)
+        lens = t(s.meta["lens"], device)
+        rng = np.random.default_rng(gqa)
+        q = rng.standard_normal((len(s.meta["lens"]), gqa * s.h, s.d), dtype=np.float32)
+        qt = t(q, device, torch.float16)
+        ref = OA.decode_attention(sim.ps, qt.float().cpu().numpy(), s.meta["table"], s.meta["lens"], s.d ** -0.5)
+        got = dec.decode_attention(store, qt, table, lens, s.d ** -0.5, blocks_per_split=2, batch_invariant=inv)
+        torch.cuda.synchronize()
+        err = maxdiff(got, ref)
+        assert err <= TOL, f"{s.name} gqa={gqa}: max err {err}"
+
+
 @pytest.mark.parametrize("scale", [-0.088, 0.0, 0.9])
 def test_decode_softmax_scale_sign_and_zero(device, case_stores, scale):
     """The kernels take the max on unscaled scores and scale inside the
