@@ -293,7 +293,8 @@ def run(args) -> dict:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(),
-            "kernel": "decode_kernel<128, 4> + merge_kernel (one INT4 layer-step, graph replay over the 16 INT4 layers)",
+            "kernel": ("decode_kernel<128, 4> + merge_kernel" if inv else "decode_balanced_kernel<128, 4> + merge_balanced_kernel")
+                      + " (one INT4 layer-step, graph replay over the 16 INT4 layers)",
             "alg_bytes_per_launch": int(per_layer_bytes),
         },
     }
