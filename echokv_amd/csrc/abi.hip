@@ -103,9 +103,18 @@ int echokv_write_step(const echokv_layout* L, uint8_t* pages, const void* key, i
   if (n_rows < 0 || fin_grid < 0 || tok_s0 < n_rows || !res_ok(res)) return ECHOKV_EINVAL;
   if (n_rows + fin_grid == 0) return ECHOKV_OK;
   if (!pages || !key || !fin_count || (n_rows && (!value || !tok)) || (fin_grid && !fin)) return ECHOKV_EINVAL;
+  // Fin rows stage their group in LDS when key and residual share a dtype, every
+  // four-channel run is aligned for one vector load, and the group fits the LDS.
+  int staged = -1;
+  if (kv_dtype == res->dtype && ek::step_staged_lds(L->k_group, kv_dtype) <= ek::kStepStagedMaxLds) {
+    const uintptr_t al = kv_dtype == ECHOKV_F32 ? 16 : 8;
+    if ((uintptr_t)key % al == 0 && (uintptr_t)res->ptr % al == 0 && k_s0 % 4 == 0 && k_s1 % 4 == 0 &&
+        res->s0 % 4 == 0 && res->s1 % 4 == 0 && res->s2 % 4 == 0)
+      staged = kv_dtype;
+  }
   ek::StepArgs a{ek::WriteTokArgs{to_lay(L), pages, key, k_s0, k_s1, value, v_s0, v_s1, kv_dtype, tok, tok_s0,
                                   to_res(res), kref, kref_s0, kref_s1},
-                 fin, fin_count, fin_grid, n_rows};
+                 fin, fin_count, fin_grid, n_rows, staged};
   return launched(ek::launch_write_step(a, (hipStream_t)stream));
 }
 

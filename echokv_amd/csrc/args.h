@@ -49,7 +49,8 @@ struct FinArgs {
   Res res;
 };
 
-// A fused step: token rows plus fin rows (fin: [>= fin_grid, 3 + KG]).
+// A fused step: token rows plus fin rows (fin: [>= fin_grid, 3 + KG], every row
+// below fin_grid is read; rows at or past *fin_count do nothing).
 constexpr int kMaxDeferred = 256;  // k_group bound of the fused step (a slot's group has < k_group rows in a step)
 struct StepArgs {
   WriteTokArgs w;
@@ -57,7 +58,15 @@ struct StepArgs {
   const int64_t* fin_count;
   long fin_grid;
   long n_rows;
+  int staged;  // dtype of key and residual when fin rows stage their group in LDS, else -1
 };
+
+// Dynamic LDS of a staged fused step, and the largest the launch takes without
+// raising the kernel's limit.
+inline size_t step_staged_lds(int k_group, int dtype) {
+  return (size_t)k_group * kThreads * (dtype == ECHOKV_F32 ? 16 : 8);
+}
+constexpr size_t kStepStagedMaxLds = 64 * 1024;
 
 // The keys a prefill query at position p sees are those < og_limit(p): p + 1
 // (bottom-right causal), or with own_group on (og_mask = ~(k_group - 1)) the keys

@@ -120,12 +120,18 @@ __device__ __forceinline__ long row_base(const uint8_t* pages, const Lay& L, lon
 // A block's 16 header bytes, read once: [0] tag, [4:16] pool chunk ids.
 struct Hdr {
   uint32_t tag;
-  int32_t id[3];
+  int32_t id0, id1, id2;  // pool chunk ids of chunks 1..3 (fields, not an array: no stack copy)
+  // Chunk j's id (j in 0..2) by masks: a select chain over the fields lets the
+  // compiler turn the header into a stack array indexed at run time.
+  __device__ __forceinline__ int32_t id(int j) const {
+    const int32_t m0 = -(int32_t)(j == 0), m1 = -(int32_t)(j == 1), m2 = -(int32_t)(j >= 2);
+    return (id0 & m0) | (id1 & m1) | (id2 & m2);
+  }
 };
 
 __device__ __forceinline__ Hdr load_hdr(const uint8_t* pages, const Lay& L, long blk) {
   const uint4 h = *(const uint4*)(pages + blk * L.stride);
-  return Hdr{h.x & 0xffu, {(int32_t)h.y, (int32_t)h.z, (int32_t)h.w}};
+  return Hdr{h.x & 0xffu, (int32_t)h.y, (int32_t)h.z, (int32_t)h.w};
 }
 
 // row_base from a header already in registers.
@@ -134,7 +140,7 @@ __device__ __forceinline__ long row_base_h(const Lay& L, long blk, const Hdr& hd
   const int j = off / tpc;
   long cb = blk * L.stride + L.o_data;
   if (j > 0) {
-    const int id = j == 1 ? hd.id[0] : (j == 2 ? hd.id[1] : hd.id[2]);
+    const int id = hd.id(j - 1);
     const long page = id / L.KC, slot = id % L.KC;
     if (id < 0 || page >= L.nb) return -1;
     cb = page * L.stride + L.o_data + slot * L.cb;

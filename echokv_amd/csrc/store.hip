@@ -15,9 +15,12 @@ namespace ek {
 // write_tokens (echokv_vllm/kernels/write.py:29-36, 172-229)
 // ---------------------------------------------------------------------------
 
-// Token row t; res_here: this workgroup stores the row's K to the residual (a
-// fused step leaves that store to the workgroup finalizing the slot's old group).
-__device__ __forceinline__ void write_token_row(const WriteTokArgs& a, long t, bool res_here) {
+// Token row t. res_here() says whether this workgroup stores the row's K to the
+// residual (a fused step leaves that store to the workgroup finalizing the slot's
+// old group); every thread calls it once, after the row's first loads are issued,
+// so a caller may run a workgroup-wide vote in it.
+template <typename ResHere>
+__device__ __forceinline__ void write_token_row(const WriteTokArgs& a, long t, ResHere res_here) {
   const Lay& L = a.L;
   const long slot = a.tok[t];
   if (slot < 0) return;
@@ -33,6 +36,7 @@ __device__ __forceinline__ void write_token_row(const WriteTokArgs& a, long t, b
   const int quads = L.D / 4;
   const int items = L.H * quads;
   const int G = L.D / L.VG;
+  bool rh = true;
   for (int base = 0; base < items; base += kThreads) {
     const int i = base + (int)threadIdx.x;
     const bool act = i < items;
@@ -51,6 +55,7 @@ __device__ __forceinline__ void write_token_row(const WriteTokArgs& a, long t, b
         km16[e] = *f16p(a.pages, blk * L.stride + L.o_km + 2 * (se + e));
       }
     }
+    if (base == 0) rh = res_here();  // uniform: every thread runs the first pass
     const int bits = tier_of(hd.tag);
     const long rb = row_base_h(L, blk, hd, off, bits);
     const int side = L.H * L.D * bits / 8;
@@ -73,7 +78,7 @@ __device__ __forceinline__ void write_token_row(const WriteTokArgs& a, long t, b
     store_codes4(a.pages + rb + side + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
 
     // K: residual (open group), codes under the sealed stats, K_ref ring.
-    if (res_here && rslot >= 0 && rslot < a.res.rows)
+    if (rh && rslot >= 0 && rslot < a.res.rows)
       st_n<4>(a.res.ptr, a.res.dtype, rslot * a.res.s0 + (long)(off % L.KG) * a.res.s1 + h * a.res.s2 + 4 * c, k);
     if (sealed != 0) {
       uint32_t kq[4];
@@ -88,7 +93,9 @@ __device__ __forceinline__ void write_token_row(const WriteTokArgs& a, long t, b
   }
 }
 
-__global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) { write_token_row(a, blockIdx.x, true); }
+__global__ __launch_bounds__(kThreads) void write_tokens_kernel(WriteTokArgs a) {
+  write_token_row(a, blockIdx.x, [] { return true; });
+}
 
 // ---------------------------------------------------------------------------
 // K-group quantization shared by finalize_k, seal and store_blocks: the group's
@@ -210,7 +217,7 @@ __device__ __forceinline__ void finalize_group(const FinArgs a, const int64_t* r
   cb[0] = blk * L.stride + L.o_data;
 #pragma unroll
   for (int j = 1; j < 4; ++j) {
-    const int id = hd.id[j - 1];
+    const int id = hd.id(j - 1);
     const uint32_t page = (uint32_t)id / (uint32_t)L.KC, slot = (uint32_t)id % (uint32_t)L.KC;
     cb[j] = (id < 0 || (long)page >= L.nb) ? -1L : (long)page * L.stride + L.o_data + (long)slot * L.cb;
   }
@@ -287,51 +294,258 @@ __global__ __launch_bounds__(kThreads) void finalize_k_kernel(FinArgs a) {
   finalize_row(a, f, nullptr, nullptr);
 }
 
-// One step's writes in one launch (the pair finalize_k, write_tokens). Workgroups
-// [0, fin_grid) take fin rows (masked by the device count), the rest token rows.
-// The pair's order matters only where a token's K goes to a residual slot that a
-// fin row of the step releases (the slot's old group completes now and is read
-// from it): both sides see that from the plan itself -- fin row f's slot
-// fin[f][2] equals the token's residual slot -- and that one store moves to the
-// fin row's workgroup, after its reads; nothing waits on another workgroup.
-__global__ __launch_bounds__(kThreads) void write_step_kernel(StepArgs s) {
+// ---------------------------------------------------------------------------
+// One step's writes in one launch (the pair finalize_k, write_tokens).
+//
+// Workgroups [0, fin_grid) take fin rows (rows at or past the device count do
+// nothing), the rest token rows. The pair's order matters only where a token's K
+// goes to a residual slot that a fin row of the step releases (the slot's old
+// group completes now and is read from it): both sides see that from the plan
+// itself -- fin row f's slot fin[f][2] equals the token's residual slot -- and
+// that one store moves to the fin row's workgroup, after its reads; nothing waits
+// on another workgroup.
+//
+// At decode shape a workgroup's time is a chain of dependent memory round trips
+// (2-3 us each once the previous kernel has cycled the caches) plus instruction
+// fetch, which starts cold every launch. So each workgroup issues every load that
+// depends only on its row in a first round trip (fin rows f < fin_grid are all in
+// the buffer; the count only says which are real), everything that depends on
+// those in a second, and runs its per-token work as short loops: a fin row stages
+// its group's values in LDS rather than in unrolled registers.
+// ---------------------------------------------------------------------------
+
+// Four consecutive channels of a 16-bit (uint2) or f32 (uint4) source, as stored.
+template <int DT> struct Raw4 { using V = uint2; };
+template <> struct Raw4<ECHOKV_F32> { using V = uint4; };
+
+template <int DT>
+__device__ __forceinline__ void raw4_to_f(const typename Raw4<DT>::V& r, float x[4]) {
+  if constexpr (DT == ECHOKV_F32) {
+    x[0] = __uint_as_float(r.x);
+    x[1] = __uint_as_float(r.y);
+    x[2] = __uint_as_float(r.z);
+    x[3] = __uint_as_float(r.w);
+  } else {
+    const uint32_t wd[2] = {r.x, r.y};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t b = (uint16_t)(wd[e >> 1] >> (16 * (e & 1)));
+      if constexpr (DT == ECHOKV_F16) x[e] = (float)__builtin_bit_cast(_Float16, b);
+      else x[e] = bf16_to_f32(b);
+    }
+  }
+}
+
+constexpr int kStepScan = 8;  // token rows per thread whose loads one scan pass issues together
+
+// Token rows of the step whose residual slot is rs (their K goes to the slot this
+// fin row releases). The caller loaded row threadIdx.x's (slot, residual slot).
+__device__ __forceinline__ void collect_deferred(const WriteTokArgs& a, long n_rows, long rs, long tslot, long tres,
+                                                 Deferred& def) {
+  auto add = [&](long t, long slot) {
+    const int i = atomicAdd(&def.n, 1);  // LDS counter: at most k_group - 1 rows take a slot in a step
+    if (i < kMaxDeferred) {
+      def.t[i] = t;
+      def.row[i] = (int)((slot % a.L.BS) % a.L.KG);
+    }
+  };
+  if (tslot >= 0 && tres == rs) add(threadIdx.x, tslot);
+  for (long t0 = kThreads + threadIdx.x; t0 < n_rows; t0 += (long)kThreads * kStepScan) {
+    long sl[kStepScan], re[kStepScan];
+#pragma unroll
+    for (int k = 0; k < kStepScan; ++k) {
+      const long t = t0 + (long)k * kThreads;
+      sl[k] = t < n_rows ? a.tok[t] : -1;
+      re[k] = t < n_rows ? a.tok[a.tok_s0 + t] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kStepScan; ++k)
+      if (sl[k] >= 0 && re[k] == rs) add(t0 + (long)k * kThreads, sl[k]);
+  }
+}
+
+// Round trip 1 of a fin row: its residual slot, the device count and the step's
+// token slots, then the deferred rows. Returns false when the row is past the count.
+__device__ __forceinline__ bool fin_prologue(const StepArgs& s, long f, Deferred& def, int64_t* grow) {
   const WriteTokArgs& a = s.w;
-  const int w = 3 + a.L.KG;
+  const int64_t* row = s.fin + f * (3 + a.L.KG);
   const long count = *s.fin_count;
-  if ((long)blockIdx.x < s.fin_grid) {
-    const long f = blockIdx.x;
-    if (f >= count) return;
-    const long rs = s.fin[f * w + 2];
-    __shared__ Deferred def;
-    if (threadIdx.x == 0) def.n = 0;
-    __syncthreads();
-    if (rs >= 0 && rs < a.res.rows) {
-      for (long t = threadIdx.x; t < s.n_rows; t += kThreads) {
-        const long slot = a.tok[t];
-        if (a.tok[a.tok_s0 + t] == rs && slot >= 0) {
-          const int i = atomicAdd(&def.n, 1);  // LDS counter: at most k_group - 1 rows take a slot in a step
-          if (i < kMaxDeferred) {
-            def.t[i] = t;
-            def.row[i] = (int)((slot % a.L.BS) % a.L.KG);
+  const long rs = row[2];
+  if (grow && (int)threadIdx.x < a.L.KG) grow[threadIdx.x] = row[3 + threadIdx.x];
+  const bool mine = (long)threadIdx.x < s.n_rows;
+  const long tslot = mine ? a.tok[threadIdx.x] : -1;
+  const long tres = mine ? a.tok[a.tok_s0 + threadIdx.x] : -1;
+  if (threadIdx.x == 0) def.n = 0;
+  __syncthreads();
+  if (f >= count) return false;
+  if (rs >= 0 && rs < a.res.rows) collect_deferred(a, s.n_rows, rs, tslot, tres, def);
+  __syncthreads();
+  if (def.n > kMaxDeferred) def.n = kMaxDeferred;  // not reached: the host checks k_group <= kMaxDeferred
+  return true;
+}
+
+// Fin row f with key and residual of dtype DT: the group's values go through LDS
+// (xs: [k_group][kThreads], each thread reads back only what it wrote).
+template <int DT>
+__device__ __forceinline__ void fin_staged(const StepArgs& s, long f, typename Raw4<DT>::V* xs, const Deferred& def,
+                                           const int64_t* grow) {
+  using V = typename Raw4<DT>::V;
+  constexpr long esz = DT == ECHOKV_F32 ? 4 : 2;
+  const WriteTokArgs& a = s.w;
+  const Lay& L = a.L;
+  const int KG = L.KG;
+  const int64_t* row = s.fin + f * (3 + KG);
+  const long blk = row[0];
+  const int grp = (int)row[1];
+  const long rs_raw = row[2];
+  const long rs = rs_raw < 0 ? 0 : rs_raw;  // -1: every token of the group is in this step's key
+  const bool ok = blk >= 0 && blk < L.nb && grp >= 0 && grp < L.BS / KG && rs < a.res.rows;
+  const int n_def = def.n;
+  const int quads = L.D / 4;
+  const Hdr hd = load_hdr(a.pages, L, ok ? blk : 0);  // block 0 stands in for a bad row (nothing is stored)
+  const char* key = (const char*)a.key;
+  const char* res = (const char*)a.res.ptr;
+  for (int i = threadIdx.x; i < L.H * quads; i += kThreads) {
+    const int h = i / quads, c = i % quads;
+    // Round trip 2: the group's values, and the first deferred rows' keys.
+    float kd[2][4];
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+      if (d < n_def) ld_n<4>(a.key, a.kv_dtype, def.t[d] * a.k_s0 + h * a.k_s1 + 4 * c, kd[d]);
+    if (ok) {
+      float mn[4], mx[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        mn[e] = __builtin_inff();
+        mx[e] = -__builtin_inff();
+      }
+      for (int p0 = 0; p0 < KG; p0 += 16) {
+        V v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int p = p0 + u;
+          if (p < KG) {
+            const long r = grow[p];
+            const char* src = r >= 0 ? key + esz * (r * a.k_s0 + h * a.k_s1 + 4 * c)
+                                     : res + esz * (rs * a.res.s0 + (long)p * a.res.s1 + h * a.res.s2 + 4 * c);
+            v[u] = *(const V*)src;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int p = p0 + u;
+          if (p < KG) {
+            xs[p * kThreads + threadIdx.x] = v[u];
+            float x[4];
+            raw4_to_f<DT>(v[u], x);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              mn[e] = fminf(mn[e], x[e]);
+              mx[e] = fmaxf(mx[e], x[e]);
+            }
           }
         }
       }
+      const int bits = tier_of(hd.tag);
+      float sc[4], mi[4];
+      const long se = ((long)grp * L.H + h) * L.D + 4 * c;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        _Float16 s16, m16;
+        group_stats(mn[e], mx[e], bits, s16, m16, sc[e], mi[e]);
+        *f16p(a.pages, blk * L.stride + L.o_ks + 2 * (se + e)) = s16;
+        *f16p(a.pages, blk * L.stride + L.o_km + 2 * (se + e)) = m16;
+      }
+      // Chunk j of the block: its own page's data for j = 0, pool chunk id[j - 1]
+      // otherwise (-1: out of range, nothing stored there).
+      long cb[4];
+      cb[0] = blk * L.stride + L.o_data;
+#pragma unroll
+      for (int j = 1; j < 4; ++j) {
+        const int id = hd.id(j - 1);
+        const uint32_t page = (uint32_t)id / (uint32_t)L.KC, slot = (uint32_t)id % (uint32_t)L.KC;
+        cb[j] = (id < 0 || (long)page >= L.nb) ? -1L : (long)page * L.stride + L.o_data + (long)slot * L.cb;
+      }
+      const int tpc = 2 * L.BS / bits;  // tokens per chunk
+      const long rowb = 2L * L.H * L.D * bits / 8;
+      const long within = (long)h * (L.D * bits / 8) + c * (bits / 2);
+      int j = (grp * KG) / tpc, w = (grp * KG) % tpc;
+#pragma unroll 4
+      for (int p = 0; p < KG; ++p) {
+        const long base = j == 0 ? cb[0] : (j == 1 ? cb[1] : (j == 2 ? cb[2] : cb[3]));
+        if (base >= 0) {
+          float x[4];
+          raw4_to_f<DT>(xs[p * kThreads + threadIdx.x], x);
+          uint32_t q[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) q[e] = quant_code(x[e], mi[e], sc[e], bits);
+          store_codes4(a.pages + base + w * rowb + within, pack4(q, bits), bits);
+        }
+        if (++w == tpc) {
+          w = 0;
+          ++j;
+        }
+      }
     }
-    __syncthreads();
-    if (def.n > kMaxDeferred) def.n = kMaxDeferred;  // not reached: the host checks k_group <= kMaxDeferred
-    const FinArgs fa{a.L, a.pages, a.key, a.k_s0, a.k_s1, a.kv_dtype, s.fin, s.fin_count, a.res};
-    finalize_row(fa, f, &a, &def);
+    // Residual K of the deferred rows: this thread has read these words above.
+    for (int d = 0; d < n_def; ++d) {
+      float k[4];
+      if (d < 2) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) k[e] = d == 0 ? kd[0][e] : kd[1][e];
+      } else {
+        ld_n<4>(a.key, a.kv_dtype, def.t[d] * a.k_s0 + h * a.k_s1 + 4 * c, k);
+      }
+      st_n<4>(a.res.ptr, a.res.dtype, rs_raw * a.res.s0 + (long)def.row[d] * a.res.s1 + h * a.res.s2 + 4 * c, k);
+    }
+  }
+}
+
+// Token row t of a fused step: round trip 1 takes the row's plan and values, the
+// device count and the fin rows' residual slots; the residual vote runs with the
+// row's second round trip (page header, sealed stats) in flight.
+__device__ __forceinline__ void step_token_row(const StepArgs& s, long t) {
+  const WriteTokArgs& a = s.w;
+  const int w = 3 + a.L.KG;
+  const long count = *s.fin_count;
+  const long rslot = a.tok[a.tok_s0 + t];
+  const long r0 = (long)threadIdx.x < s.fin_grid ? s.fin[threadIdx.x * w + 2] : -1;
+  auto res_here = [&]() {
+    bool hit = false;
+    if (rslot >= 0) {
+      hit = (long)threadIdx.x < count && r0 == rslot;
+      for (long f = threadIdx.x + kThreads; f < s.fin_grid; f += kThreads) {
+        const long rf = s.fin[f * w + 2];
+        hit = hit || (f < count && rf == rslot);
+      }
+    }
+    return !__syncthreads_or(hit);
+  };
+  write_token_row(a, t, res_here);
+}
+
+__global__ __launch_bounds__(kThreads) void write_step_kernel(StepArgs s) {
+  extern __shared__ uint4 step_lds[];  // fin_staged's group values (dynamic: k_group * kThreads * 8 or 16 bytes)
+  __shared__ Deferred def;
+  __shared__ int64_t grow[kMaxDeferred];  // the fin row's token row per position
+  if ((long)blockIdx.x < s.fin_grid) {
+    const long f = blockIdx.x;
+    const bool staged = s.staged >= 0;
+    if (!fin_prologue(s, f, def, staged ? grow : nullptr)) return;
+    if (s.staged == ECHOKV_F16) {
+      fin_staged<ECHOKV_F16>(s, f, (uint2*)step_lds, def, grow);
+    } else if (s.staged == ECHOKV_BF16) {
+      fin_staged<ECHOKV_BF16>(s, f, (uint2*)step_lds, def, grow);
+    } else if (s.staged == ECHOKV_F32) {
+      fin_staged<ECHOKV_F32>(s, f, step_lds, def, grow);
+    } else {
+      const WriteTokArgs& a = s.w;
+      const FinArgs fa{a.L, a.pages, a.key, a.k_s0, a.k_s1, a.kv_dtype, s.fin, s.fin_count, a.res};
+      finalize_row(fa, f, &a, &def);
+    }
     return;
   }
-  const long t = (long)blockIdx.x - s.fin_grid;
-  const long rslot = a.tok[a.tok_s0 + t];
-  bool hit = false;
-  if (rslot >= 0) {  // fin rows past the device count are never read (a graph's buffer may hold fewer)
-    const long nf = count < s.fin_grid ? count : s.fin_grid;
-    for (long f = threadIdx.x; f < nf; f += kThreads) hit = hit || s.fin[f * w + 2] == rslot;
-  }
-  const bool deferred = __syncthreads_or(hit);
-  write_token_row(a, t, !deferred);
+  step_token_row(s, (long)blockIdx.x - s.fin_grid);
 }
 
 // ---------------------------------------------------------------------------
@@ -605,7 +819,8 @@ hipError_t launch_finalize_k(const FinArgs& a, long rows, hipStream_t s) {
   return hipGetLastError();
 }
 hipError_t launch_write_step(const StepArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(write_step_kernel, dim3((unsigned)(a.fin_grid + a.n_rows)), dim3(kThreads), 0, s, a);
+  const size_t lds = a.staged < 0 ? 0 : step_staged_lds(a.w.L.KG, a.staged);
+  hipLaunchKernelGGL(write_step_kernel, dim3((unsigned)(a.fin_grid + a.n_rows)), dim3(kThreads), lds, s, a);
   return hipGetLastError();
 }
 hipError_t launch_seal(const SealArgs& a, long n, hipStream_t s) {

@@ -72,8 +72,9 @@ def write_step(store, key: torch.Tensor, value: torch.Tensor, meta, kref: torch.
     ``full_grid`` gives the finalize part one workgroup per token row, masked on
     the device by ``meta.fin_count`` (a captured graph does not know the count)."""
     n_fin = meta.n_rows if full_grid else meta.n_fin
-    if meta.fin.shape[0] == 0:  # no rows staged: the device count is 0 too
-        n_fin = 0
+    # The kernel reads every fin row below its grid (the device count masks them),
+    # and the staged rows cover the count: the grid stops at the rows there are.
+    n_fin = min(n_fin, meta.fin.shape[0])
     if n_fin + meta.n_rows == 0:
         return
     if store.layout.k_group > FUSED_MAX_K_GROUP:

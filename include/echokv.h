@@ -82,7 +82,8 @@ int echokv_finalize_k(const echokv_layout* L, uint8_t* pages,
                       const echokv_residual* res, echokv_stream_t stream);
 
 /* One step's writes in one launch: echokv_finalize_k's fin rows (workgroups
- * [0, fin_grid), rows >= *fin_count skipped) and echokv_write_tokens' token rows
+ * [0, fin_grid); fin holds at least fin_grid rows, all of them read, and rows
+ * >= *fin_count do nothing) and echokv_write_tokens' token rows
  * (n_rows of them), with the same arguments and results as the finalize-then-write
  * pair. A token whose residual slot is released by a fin row of the same step
  * has its residual K stored by that fin row's workgroup after it has read the
