@@ -18,7 +18,8 @@ against the 2e-3 budget, so the margin is visible in the log.
 * cfg4 shape: GQA 8 (Hq 64), one 32k-token sequence: default splits, a split of
   more than 64 blocks (the chunk loop), more than 64 splits (the two-pass merge);
   the canary at Hq 64.
-* more than 64 sequences (the chunked work-item scan), V groups of 16 and 64,
+* more than 64 sequences (the chunked work-item scan; short sequences, so the
+  balanced schedule's ranges cover several sequences each), V groups of 16 and 64,
   head size 64, and a layer view whose pages span more than 4 GiB (64-bit page
   addressing, as in a layer view of a pool interleaved across layers).
 """
@@ -263,6 +264,12 @@ def test_more_than_64_sequences_with_padding_rows(device):
     check("150 sequences", out[live], ref)
     check("150 sequences, split schedule", split[live], ref)
     assert (out[[3, 100]] == 7.0).all() and (split[[3, 100]] == 7.0).all()
+    # A workspace of 6 splits: the balanced schedule's ranges fill it.
+    tight = torch.full((150, 32, 128), 7.0, device=device)
+    dec.decode_attention(store, q, torch.from_numpy(table).to(device, torch.int32), torch.from_numpy(run).to(device),
+                         128 ** -0.5, out=tight, num_splits=6)
+    check("150 sequences, 6-split workspace", tight[live], ref)
+    assert (tight[[3, 100]] == 7.0).all()
 
 
 @pytest.mark.parametrize("d,vg", [(128, 16), (128, 64), (64, 32), (64, 16)])
