@@ -337,30 +337,50 @@ __device__ __forceinline__ void s_block(const Wave<D, QLO>& w, const uint32_t* k
 // S^T of a tile whose keys are the block's open K group, read from the
 // full-precision residual (row = token % KG) and split into fp16 hi + lo
 // (fp16 / bf16 keys are exact in fp16: lo = 0 is skipped). Lane (c, n): token
-// t0 + n, channels [c * D/4, (c+1) * D/4), eight at a time.
-template <int D, bool QLO>
+// t0 + n, channels [c * D/4, (c+1) * D/4), eight at a time. The residual's dtype
+// is a template parameter, so every row load issues before the first MFMA waits.
+template <int D, bool QLO, int RDT>
 __device__ __forceinline__ void s_from_residual(const Wave<D, QLO>& w, const DecodeArgs& a, long rslot, int t0, int h,
                                                 int lane, f4_t& sh, f4_t& sl) {
-  constexpr int CPL = D / 4;
+  constexpr int CPL = D / 4, NJ = D / 32;
+  // Rows loaded together: f32 rows take twice the registers, and hi + lo halves.
+  constexpr int STEP = RDT == ECHOKV_F32 ? 2 : NJ;
   const int c = lane >> 4, n = lane & 15;
   const long r0 = rslot * a.res.s0 + (long)((t0 + n) & (a.L.KG - 1)) * a.res.s1 + h * a.res.s2 + c * CPL;
-  const bool res_lo = a.res.dtype == ECHOKV_F32;
 #pragma unroll
-  for (int j = 0; j < D / 32; ++j) {
-    float xr[8];
-    ld_n<8>(a.res.ptr, a.res.dtype, r0 + 8 * j, xr);
-    h8_t kh, kl;
+  for (int j0 = 0; j0 < NJ; j0 += STEP) {
+    h8_t kh[STEP], kl[STEP];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      kh[e] = (_Float16)xr[e];
-      kl[e] = (_Float16)(xr[e] - (float)kh[e]);
+    for (int u = 0; u < STEP; ++u) {
+      const long e0 = r0 + 8 * (j0 + u);
+      if constexpr (RDT == ECHOKV_F16) {
+        const _Float16* src = (const _Float16*)a.res.ptr + e0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kh[u][e] = src[e];
+      } else if constexpr (RDT == ECHOKV_BF16) {
+        const uint16_t* src = (const uint16_t*)a.res.ptr + e0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kh[u][e] = (_Float16)bf16_to_f32(src[e]);
+      } else {
+        const float* src = (const float*)a.res.ptr + e0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float v = src[e];
+          kh[u][e] = (_Float16)v;
+          kl[u][e] = (_Float16)(v - (float)kh[u][e]);
+        }
+      }
     }
-    const h8_t qh = w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2], w.qn[4 * j + 3]);
-    sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh, sh, 0, 0, 0);
-    if (res_lo) sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh, sl, 0, 0, 0);
-    if constexpr (QLO) {
-      const h8_t ql = w2h8(w.ql[4 * j], w.ql[4 * j + 1], w.ql[4 * j + 2], w.ql[4 * j + 3]);
-      sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql, sl, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < STEP; ++u) {
+      const int j = j0 + u;
+      const h8_t qh = w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2], w.qn[4 * j + 3]);
+      sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[u], qh, sh, 0, 0, 0);
+      if constexpr (RDT == ECHOKV_F32) sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl[u], qh, sl, 0, 0, 0);
+      if constexpr (QLO) {
+        const h8_t ql = w2h8(w.ql[4 * j], w.ql[4 * j + 1], w.ql[4 * j + 2], w.ql[4 * j + 3]);
+        sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[u], ql, sl, 0, 0, 0);
+      }
     }
   }
 }
@@ -439,6 +459,8 @@ __device__ __forceinline__ void load_as_bytes(const uint8_t* p, int bits, uint32
 // One 16-token tile [t0, t0 + 16) of block `blk` stored at `bits` (any tier):
 // codes are widened to bytes and go through the 8-bit math. tokens >= n_valid
 // are masked; in_res: the tile is the block's open K group (K from the residual).
+// The block header is read once and each part's loads issue together: the tile
+// is a few memory round trips, not one per row.
 template <int D, bool QLO>
 __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs& a, long blk, int t0, int n_valid,
                                          long rslot, bool in_res, int h, int lane, int bits, float* x, h4_t* va) {
@@ -449,18 +471,20 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
   const uint8_t* pages = a.pages;
   const long side = (long)L.H * D * bits / 8;
   const long headb = (long)h * (D * bits / 8);
+  const Hdr hd = load_hdr(pages, L, blk);
 
   // ---- S^T = K Q'^T (+ bias) -------------------------------------------
   f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
   if (in_res) {
-    s_from_residual<D, QLO>(w, a, rslot, t0, h, lane, sh, sl);
+    if (a.res.dtype == ECHOKV_F16) s_from_residual<D, QLO, ECHOKV_F16>(w, a, rslot, t0, h, lane, sh, sl);
+    else if (a.res.dtype == ECHOKV_BF16) s_from_residual<D, QLO, ECHOKV_BF16>(w, a, rslot, t0, h, lane, sh, sl);
+    else s_from_residual<D, QLO, ECHOKV_F32>(w, a, rslot, t0, h, lane, sh, sl);
   } else {
     const long e0 = ((long)(t0 / L.KG) * L.H + h) * D + c * CPL;
-    const long rb = row_base(pages, L, blk, t0 + n, bits);
+    const long rb = row_base_h(L, blk, hd, t0 + n, bits);
     uint32_t kw[CPL / 4];
-    if (rb >= 0) {
-      load_as_bytes<CPL>(pages + rb + headb + (long)c * (CPL * bits / 8), bits, kw);
-    } else {
+    load_as_bytes<CPL>(pages + (rb >= 0 ? rb + headb + (long)c * (CPL * bits / 8) : blk * L.stride), bits, kw);
+    if (rb < 0) {
 #pragma unroll
       for (int i = 0; i < CPL / 4; ++i) kw[i] = 0;
     }
@@ -484,23 +508,37 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
   const int G = D / L.VG;
   const int g = (n * CPM) / L.VG;
   _Float16 sv[4], mv[4];
+  // The four rows at a compile-time width (one branch on the tier, not one per
+  // row), so their loads issue together.
+  auto load_v = [&](auto width) {
+    constexpr int BB = decltype(width)::value;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int tv = t0 + 4 * c + i;
-    const long rb = row_base(pages, L, blk, tv, bits);
-    const bool ok = tv < n_valid && rb >= 0;
-    if (ok) {
-      load_as_bytes<CPM>(pages + rb + side + headb + (long)n * (CPM * bits / 8), bits, vw[i]);
-      const long e = ((long)tv * L.H + h) * G + g;
+    for (int i = 0; i < 4; ++i) {
+      const int tv = t0 + 4 * c + i;
+      const long rb = row_base_h(L, blk, hd, tv, BB);
+      // Every lane loads (a row without a chunk reads its page's first bytes
+      // instead), and the masked rows are zeroed after: no branch per row, so
+      // the rows' loads issue back to back.
+      const long vb = rb >= 0 ? rb + side + headb + (long)n * (CPM * BB / 8) : blk * L.stride;
+      load_as_bytes<CPM>(pages + vb, BB, vw[i]);
+      const long e = ((long)tv * L.H + h) * G + g;  // tv < block size: inside the page's stats
       sv[i] = *f16p(pages, blk * L.stride + L.o_vs + 2 * e);
       mv[i] = *f16p(pages, blk * L.stride + L.o_vm + 2 * e);
-    } else {
-#pragma unroll
-      for (int k = 0; k < VW; ++k) vw[i][k] = 0;
-      sv[i] = (_Float16)0.f;
-      mv[i] = (_Float16)0.f;
     }
-  }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tv = t0 + 4 * c + i;
+      if (tv >= n_valid || row_base_h(L, blk, hd, tv, BB) < 0) {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) vw[i][k] = 0;
+        sv[i] = (_Float16)0.f;
+        mv[i] = (_Float16)0.f;
+      }
+    }
+  };
+  if (bits == 8) load_v(std::integral_constant<int, 8>{});
+  else if (bits == 4) load_v(std::integral_constant<int, 4>{});
+  else load_v(std::integral_constant<int, 2>{});
   vshift<8, VW>(vw, vsh);
   const h2_t s01 = {sv[0], sv[1]}, s23 = {sv[2], sv[3]};
   const h2_t m01 = {mv[0], mv[1]}, m23 = {mv[2], mv[3]};
