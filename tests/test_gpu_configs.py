@@ -274,25 +274,32 @@ def test_more_than_64_sequences_with_padding_rows(device):
 
 @pytest.mark.parametrize("d,vg", [(128, 16), (128, 64), (64, 32), (64, 16)])
 @pytest.mark.parametrize("bits", [8, 4, 2])
-def test_v_group_and_head_size_variants(device, d, vg, bits):
+@pytest.mark.parametrize("h", [4, 8])
+def test_v_group_and_head_size_variants(device, d, vg, bits, h):
+    """Four KV heads are one decode head group, eight are two (their workgroups
+    read neighbouring slices of the same token rows)."""
     lens = np.array([1, 17, 300, 64, 1000])
-    store, table = build_layer(device, lens, bits, h=4, d=d, vg=vg, seed=6, outliers=0.02)
+    store, table = build_layer(device, lens, bits, h=h, d=d, vg=vg, seed=6, outliers=0.02)
     ps = oracle_view(store)
     table_d = torch.from_numpy(table).to(device, torch.int32)
     gen = torch.Generator(device=device)
     gen.manual_seed(66)
-    q = torch.randn(5, 16, d, device=device, generator=gen).half()
+    q = torch.randn(5, 4 * h, d, device=device, generator=gen).half()
     got = dec.decode_attention(store, q, table_d, torch.from_numpy(lens).to(device), d ** -0.5)
     ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, d ** -0.5, vectorized=True)
-    check(f"decode D{d} VG{vg} int{bits}", got, ref)
+    check(f"decode H{h} D{d} VG{vg} int{bits}", got, ref)
+    got = dec.decode_attention(store, q, table_d, torch.from_numpy(lens).to(device), d ** -0.5, batch_invariant=True)
+    check(f"decode H{h} D{d} VG{vg} int{bits} split schedule", got, ref)
+    if h == 8:
+        return  # the prefill paths take the same head loop at any head count
     for path, chunk in (("dense", 100), ("fused", 30)):
         prefill, row = [], 0
         for n in lens.tolist():
             nq = min(chunk, n)
             prefill.append((row, row + nq, n, 0))
             row += nq
-        qp = torch.randn(row, 16, d, device=device, generator=gen).half()
-        out = torch.zeros(row, 16, d, device=device)
+        qp = torch.randn(row, 4 * h, d, device=device, generator=gen).half()
+        out = torch.zeros(row, 4 * h, d, device=device)
         fn = pf.prefill_attention_dense if path == "dense" else pf.prefill_attention_fused
         fn(store, qp, out, prefill, list(range(5)), table_d, d ** -0.5)
         torch.cuda.synchronize()
