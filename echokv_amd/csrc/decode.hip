@@ -1312,6 +1312,52 @@ __global__ __launch_bounds__(256) void merge_balanced_kernel(DecodeArgs a) {
   const bool rf_second = first > range_begin(rf, R, T);
   auto slot_of = [&](long q) { return 2 * q + (q == rf && rf_second ? 1 : 0); };
   const long n = rl - rf + 1;
+  if (n <= 16) {
+    // Up to 16 pieces: their (max, sum) pairs and partial rows are requested in
+    // one round trip (which pieces exist follows from the ranges alone); the
+    // weights are applied once the pairs are in.
+    const int pi = lane & 15;
+    const long qi = rf + pi;
+    const bool mine = lane < 16 && pi < n && range_begin(qi, R, T) < range_begin(qi + 1, R, T);
+    float mq = -__builtin_inff(), lq = 0.f;
+    if (mine) {
+      const long pr = slot_of(qi) * a.hq + head;
+      mq = a.ml[pr * 2];
+      lq = a.ml[pr * 2 + 1];
+    }
+    const uint64_t live = __builtin_amdgcn_ballot_w64(mine);  // piece u exists: bit u
+    float x[16][C];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const long q = rf + u;
+#pragma unroll
+      for (int e = 0; e < C; ++e) x[u][e] = 0.f;
+      if ((live >> u) & 1) {  // wave-uniform
+        const float* src = a.acc + (slot_of(q) * a.hq + head) * D + C * lane;
+#pragma unroll
+        for (int e = 0; e < C; ++e) x[u][e] = src[e];
+      }
+    }
+    float m = mq;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const float w = mine ? __builtin_amdgcn_exp2f(mq - m) : 0.f;
+    float den = w * lq;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+    float o[C] = {};
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const float wu = __shfl(w, u, 64);
+#pragma unroll
+      for (int e = 0; e < C; ++e) o[e] += x[u][e] * wu;
+    }
+#pragma unroll
+    for (int e = 0; e < C; ++e) o[e] /= den;
+    const long o_row = a.q_rows ? a.q_rows[seq] : seq;
+    st_n<C>(a.out, a.out_dtype, o_row * a.o_s0 + head * a.o_s1 + C * lane, o);
+    return;
+  }
   float m = -__builtin_inff();
   for (long g = 0; g < n; g += 64) {
     const long q = rf + g + lane;
