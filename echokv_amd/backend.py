@@ -56,8 +56,10 @@ from echokv_amd.kernels import prefill as pf
 from echokv_amd.tiered_cache import TieredKVCache, TieredLayout
 from echokv_amd.write_plan import SharedState, WriteMeta
 
-# Head sizes the HIP kernels are built for.
+# Head sizes the MFMA kernels are built for; others up to MAX_HEAD_SIZE take the
+# fp32 decode kernel (prefill through decode rows).
 KERNEL_HEAD_SIZES = (64, 128)
+MAX_HEAD_SIZE = 256
 # Upper bound on decode splits per sequence (a fixed grid, so a graph replays it).
 MAX_DECODE_SPLITS = dec.MAX_SPLITS
 
@@ -88,7 +90,7 @@ class EchoKVAttentionBackend(AttentionBackend):
 
     @classmethod
     def supports_head_size(cls, head_size: int) -> bool:
-        return head_size in KERNEL_HEAD_SIZES and head_size % load_config().v_group == 0
+        return head_size % 4 == 0 and head_size % load_config().v_group == 0 and head_size <= MAX_HEAD_SIZE
 
     @classmethod
     def supports_attn_type(cls, attn_type: str) -> bool:
@@ -364,7 +366,7 @@ class EchoKVMetadataBuilder(AttentionMetadataBuilder):
 
         dev = self.device
         prefill_tiles = prefill_dense = None
-        if prefill and self.impls:
+        if prefill and self.impls and pf.kernels_take(self.impls[0].head_size, self.gqa):
             if not pf.use_dense(prefill, self.impls[0].head_size):
                 prefill_tiles = pf.build_tiles(prefill, prefill_reqs, self.gqa, dev)
             else:

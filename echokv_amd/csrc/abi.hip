@@ -162,10 +162,14 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
                int32_t num_splits, int32_t blocks_per_split, int32_t tier, int32_t flags, float* acc, float* ml,
                bool static_scratch, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;
-  if (L->head_size != 64 && L->head_size != 128) return ECHOKV_ESHAPE;
-  if (L->v_group % (L->head_size / 16)) return ECHOKV_ESHAPE;
-  // A 16-token tile must lie in one K group (one k_scale / k_min row per tile).
-  if (L->k_group < 16) return ECHOKV_ESHAPE;
+  // The MFMA kernels: D 64 or 128 with at least D/16 channels per V group, 16-token
+  // tiles inside one K group (one k_scale / k_min row per tile), power-of-two block
+  // size and K group, <= 4 chunks per page. Any other layout takes decode_any.
+  const bool pow2 = !(L->block_size & (L->block_size - 1)) && !(L->k_group & (L->k_group - 1));
+  const bool mfma = (L->head_size == 64 || L->head_size == 128) && L->v_group % (L->head_size / 16) == 0 &&
+                    L->k_group >= 16 && pow2 && L->chunks_per_page <= 4 &&
+                    L->num_blocks * L->chunks_per_page < (1LL << 24);
+  if (!mfma && L->head_size > ek::kMaxAnyD) return ECHOKV_ESHAPE;
   if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
   const int gqa = num_q_heads / L->num_kv_heads;
   if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
@@ -197,14 +201,14 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   a.bps = blocks_per_split;
   a.num_seqs = num_seqs;
   a.tier = tier;
-  if ((L->block_size & (L->block_size - 1)) || (L->k_group & (L->k_group - 1)) || L->chunks_per_page > 4)
-    return ECHOKV_ESHAPE;
-  a.bs_shift = __builtin_ctz((unsigned)L->block_size);
-  a.kg_shift = __builtin_ctz((unsigned)L->k_group);
+  a.bs_shift = mfma ? __builtin_ctz((unsigned)L->block_size) : 0;
+  a.kg_shift = mfma ? __builtin_ctz((unsigned)L->k_group) : 0;
   a.vg_shift = __builtin_ctz((unsigned)L->v_group);
   // ceil(2^32 / KC) is exact for chunk ids < 2^24 (fractions of id / KC are multiples of 1 / KC >= 1/4).
-  a.kc_mul = L->chunks_per_page == 1 ? 0u : (uint32_t)((0x100000000ull + L->chunks_per_page - 1) / L->chunks_per_page);
-  if (L->num_blocks * L->chunks_per_page >= (1LL << 24)) return ECHOKV_ESHAPE;
+  a.kc_mul = !mfma || L->chunks_per_page == 1
+                 ? 0u
+                 : (uint32_t)((0x100000000ull + L->chunks_per_page - 1) / L->chunks_per_page);
+  if (!mfma && num_seqs > INT32_MAX / L->num_kv_heads / num_splits) return ECHOKV_ESHAPE;  // one workgroup each
   if (static_scratch) {
     // acc [S, Hq, splits, D] then ml [S, Hq, splits, 2], float32, in the static array.
     if (num_seqs > (1LL << 31) / num_q_heads / num_splits) return ECHOKV_ETOOBIG;
@@ -222,20 +226,23 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   a.o_s1 = o_s1;
   a.out_dtype = out_dtype;
   a.ranges = 0;
-  if (!(flags & ECHOKV_DECODE_BATCH_INVARIANT) && ek::decode_ranges(a, a.ranges) != hipSuccess) return ECHOKV_ELAUNCH;
+  if (mfma && !(flags & ECHOKV_DECODE_BATCH_INVARIANT) && ek::decode_ranges(a, a.ranges) != hipSuccess)
+    return ECHOKV_ELAUNCH;
   // A wave's MFMA columns hold 16 query heads: a larger GQA runs in passes of 16
   // query heads per KV head (each pass reads the cache again; their rows are disjoint).
   for (int g0 = 0; g0 < gqa; g0 += 16) {
     a.g0 = g0;
     a.gs = gqa - g0 < 16 ? gqa - g0 : 16;
-    if (ek::launch_decode(a, num_seqs, (hipStream_t)stream) != hipSuccess) return ECHOKV_ELAUNCH;
+    const hipError_t d = mfma ? ek::launch_decode(a, num_seqs, (hipStream_t)stream)
+                              : ek::launch_decode_any(a, (hipStream_t)stream);
+    if (d != hipSuccess) return ECHOKV_ELAUNCH;
     hipError_t e;
     if (a.ranges > 0) {
       e = ek::launch_merge_balanced(a, (hipStream_t)stream);
     } else {
       ek::MergeArgs m{acc, ml, seq_lens, q_rows, out, o_s0, o_s1, out_dtype, num_q_heads, L->head_size,
                       L->block_size, num_splits, blocks_per_split, num_seqs * num_q_heads, gqa, a.g0, a.gs};
-      e = ek::launch_merge(m, num_seqs, (hipStream_t)stream);
+      e = mfma ? ek::launch_merge(m, num_seqs, (hipStream_t)stream) : ek::launch_merge_any(m, (hipStream_t)stream);
     }
     if (e != hipSuccess) return ECHOKV_ELAUNCH;
   }

@@ -286,6 +286,11 @@ hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s);
 hipError_t decode_ranges(const DecodeArgs& a, long& ranges);
 hipError_t launch_merge_balanced(const DecodeArgs& a, hipStream_t s);
 hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s);
+// Decode for the layouts the MFMA kernels do not take (decode_any.hip): split
+// schedule only, head size a multiple of 4 up to kMaxAnyD.
+constexpr int kMaxAnyD = 256;
+hipError_t launch_decode_any(const DecodeArgs& a, hipStream_t s);
+hipError_t launch_merge_any(const MergeArgs& a, hipStream_t s);
 hipError_t launch_canary(const CanaryArgs& a, int num_layers, hipStream_t s);
 size_t canary_lds_bytes(int d, int nbits, int rows);  // one canary workgroup's LDS
 hipError_t launch_prefill(const PrefillArgs& a, long n_tiles, hipStream_t s);

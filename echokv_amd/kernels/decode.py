@@ -4,7 +4,10 @@ Interface of ``echokv_vllm/kernels/decode.py:44-92`` (``decode_attention``).
 The work runs in two HIP kernels (``echokv_amd/csrc/decode.hip``): a split-KV
 MFMA kernel -- one workgroup per (sequence, split), one wave per KV head,
 each block's tier read from its page header -- and a log-sum-exp merge that
-writes each sequence's output row. A sequence is cut into at most
+writes each sequence's output row. Layouts those kernels are not built for
+(head sizes other than 64 / 128 up to 256, K groups under 16, block sizes or K
+groups that are not powers of two, more than 4 chunks per page) take an fp32
+kernel with the same split schedule (``echokv_amd/csrc/decode_any.hip``). A sequence is cut into at most
 ``num_splits`` splits of ``max(blocks_per_split, ceil(blocks / num_splits))``
 blocks, a function of its own length, so its result does not depend on the
 rest of the batch.
@@ -67,8 +70,6 @@ def decode_attention(
     ``batch_invariant`` splits each sequence by its own length instead.
     """
     L = store.layout
-    if L.k_group < 16:
-        raise ValueError(f"decode reads one K group per 16-token tile: k_group must be >= 16, got {L.k_group}")
     dev = query.device
     _lib.require_device(query, block_table, seq_lens, store.pages)
     s = seq_lens.shape[0]

@@ -18,6 +18,11 @@ every 64-key tile of each context is dequantized once into a workspace, then
 a flash-attention kernel with ``256 // GQA``-token query tiles streams it
 through LDS. ``dequant_dense`` keeps the reference's dense-dequantization
 entry point (``[total_ctx, H, D]`` K/V).
+
+Both kernels are built for head sizes 64 and 128 (and at most ``ROWS`` query
+heads per KV head). Any other layout (the reference's PyTorch path) attends
+through decode rows: query ``i`` of a chunk is one decode row over its context's
+first ``ctx - nq + i + 1`` keys (``prefill_attention_rows``).
 """
 
 from __future__ import annotations
@@ -33,6 +38,7 @@ ROWS = 128  # query rows (tokens x GQA heads) per workgroup of the fused kernel
 FUSED_MAX_CHUNK = 64  # the fused kernel only when every chunk is this short
 DENSE_ROWS = 256  # query rows per workgroup of the two-pass path
 DENSE_KEYS = 64  # keys per workspace tile
+ROWS_WORKSPACE_BYTES = 256 << 20  # split workspace of one slice of decode rows
 
 
 def gqa_pad(gqa: int) -> int:
@@ -147,6 +153,48 @@ def _out_view(output: torch.Tensor, hq: int) -> torch.Tensor:
     return out
 
 
+def kernels_take(head_size: int, gqa: int) -> bool:
+    """Whether the prefill kernels serve this layout (else ``prefill_attention_rows``)."""
+    return head_size in (64, 128) and gqa <= ROWS
+
+
+def build_rows(prefill, req_of, device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(query row, block-table row, context length) int64 ``[T]`` each: query ``i`` of an
+    ``nq``-token chunk over ``ctx`` keys sees the first ``ctx - nq + i + 1``."""
+    rows = torch.empty(3, sum(qe - qs for qs, qe, *_ in prefill), dtype=torch.int64)
+    at = 0
+    for (qs, qe, ctx, *_), r in zip(prefill, req_of):
+        nq = qe - qs
+        rows[0, at:at + nq] = torch.arange(qs, qe)
+        rows[1, at:at + nq] = r
+        rows[2, at:at + nq] = torch.arange(ctx - nq + 1, ctx + 1)
+        at += nq
+    rows = to_device(rows, device)
+    return rows[0], rows[1], rows[2]
+
+
+def prefill_attention_rows(store, query: torch.Tensor, output: torch.Tensor, prefill, req_of,
+                           block_table: torch.Tensor, softmax_scale: float) -> None:
+    """Prefill for layouts the prefill kernels do not take: every query token is a
+    decode row (``echokv_decode``, split schedule) over its causal context -- the
+    attention of the reference's gather + bottom-right causal SDPA
+    (echokv_vllm/kernels/prefill.py:210-236). Rows go in slices whose split
+    workspace stays under ``ROWS_WORKSPACE_BYTES``."""
+    from echokv_amd.kernels import decode as dec
+
+    if not prefill:
+        return
+    q_rows, bt_rows, lens = build_rows(prefill, req_of, query.device)
+    hq, d = query.shape[1], query.shape[2]
+    out = _out_view(output, hq)
+    max_ctx = max(ctx for _, _, ctx, *_ in prefill)
+    splits = dec.default_splits(block_table, store.layout.block_size, dec.BLOCKS_PER_SPLIT, max_ctx)
+    step = max(1, ROWS_WORKSPACE_BYTES // (hq * splits * (d + 2) * 4))
+    for i in range(0, q_rows.shape[0], step):
+        dec.decode_attention(store, query, block_table, lens[i:i + step], softmax_scale, q_rows=q_rows[i:i + step],
+                             bt_rows=bt_rows[i:i + step], out=out, num_splits=splits, batch_invariant=True)
+
+
 def use_dense(prefill, head_size: int) -> bool:
     """The two-pass path serves a batch with any chunk longer than FUSED_MAX_CHUNK."""
     return head_size in (64, 128) and any(qe - qs > FUSED_MAX_CHUNK for qs, qe, *_ in prefill)
@@ -211,6 +259,11 @@ def prefill_attention(store, query: torch.Tensor, output: torch.Tensor, prefill,
     the context as usual. ``own_group_rows`` (``own_group_rows(prefill, req_of)``)
     may be built once per step."""
     if not prefill:
+        return
+    if not kernels_take(store.layout.head_size, query.shape[1] // store.layout.num_kv_heads):
+        if own_group_key is not None:
+            raise ValueError("own-group-exact prefill needs head size 64 or 128 and at most 128 query heads per KV head")
+        prefill_attention_rows(store, query, output, prefill, req_of, block_table, softmax_scale)
         return
     part, lse = output, None
     if own_group_key is not None:

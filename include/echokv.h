@@ -129,7 +129,10 @@ int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* b
  * length, so a sequence's result does not depend on the rest of the batch. tier
  * (2, 4 or 8) selects the kernel specialised for the layer's tier; blocks stored at
  * another tier, and each block's open K group, are still read correctly on a slower
- * path.
+ * path. Layouts: head_size 64 or 128 with v_group >= head_size / 16, k_group >= 16,
+ * power-of-two block_size and k_group and <= 4 chunks per page run on the MFMA
+ * kernels; any other layout (head_size up to 256) on an fp32 kernel with the split
+ * schedule (flags and tier then select nothing).
  * Replaces echokv_vllm/kernels/decode.py:44-92 (decode_attention) with its kernels
  * decode.py:135-224 (_decode_kernel) and decode.py:227-262 (_merge_kernel). */
 int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,

@@ -56,11 +56,18 @@ def _decode(lib, L, tier=4, splits=4, seqs=1, flags=0):
                              0.088, splits, 16, tier, flags, p, p, p, 4096, 128, 1, None)
 
 
+def _layout_of(head_size=128, block_size=16, k_group=16, v_group=32):
+    lay = TieredLayout(8, head_size, block_size, 8, k_group, v_group)
+    return lay.abi(100, lay.page_bytes)
+
+
 def test_decode_rejects_bad_arguments_before_launching(lib):
-    assert _decode(lib, _layout(head_size=96)) == 2          # D must be 64 or 128
+    assert _decode(lib, _layout_of(head_size=512)) == 2     # above the fp32 kernel's 256 channels
+    assert _decode(lib, _layout(head_size=96)) == 2          # chunk bytes do not match the head size
     assert _decode(lib, _layout(block_size=24)) == 2         # block not a multiple of 16
-    assert _decode(lib, _layout(block_size=48, k_group=16)) == 2  # decode needs a power-of-2 block
-    assert _decode(lib, _layout(k_group=8)) == 2             # a 16-token tile spans two K groups
+    # Layouts the MFMA kernels are not built for pass the checks (the fp32 kernel takes them).
+    for L in (_layout_of(head_size=96), _layout_of(head_size=256), _layout_of(block_size=48), _layout_of(k_group=8)):
+        assert _decode(lib, L, seqs=0) == 0
     assert _decode(lib, _layout(), tier=3) != 0
     assert _decode(lib, _layout(), splits=0) != 0
     assert _decode(lib, _layout(), seqs=-1) != 0
@@ -118,20 +125,15 @@ def test_prefill_dense_workspace_size_and_argument_checks(lib):
 
 
 def test_python_guards_refuse_before_any_device_work():
-    """decode refuses K groups shorter than its 16-token tile; finalize_k refuses a
-    fin table whose rows are not packed at 3 + k_group int64 (the kernel's stride)."""
+    """finalize_k refuses a fin table whose rows are not packed at 3 + k_group int64
+    (the kernel's stride)."""
     from types import SimpleNamespace
 
     import torch
 
-    from echokv_amd.kernels.decode import decode_attention
     from echokv_amd.kernels.write import finalize_k
     from echokv_amd.write_plan import WriteMeta
 
-    store = SimpleNamespace(layout=TieredLayout(8, 128, 16, 8, 8, 32))
-    q = torch.zeros(1, 32, 128)
-    with pytest.raises(ValueError, match="k_group must be >= 16"):
-        decode_attention(store, q, torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.long), 0.1)
     store = SimpleNamespace(layout=TieredLayout(8, 128, 16, 8, 16, 32))
     wide = torch.zeros(2, 40, dtype=torch.long)
     meta = WriteMeta(tok=torch.zeros(4, 1, dtype=torch.long), fin=wide[:, :19], fin_count=torch.ones(1, dtype=torch.long),

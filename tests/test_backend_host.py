@@ -169,7 +169,9 @@ def test_backend_answers(monkeypatch):
     assert B.supports_block_size(64) and not B.supports_block_size(16) and B.supports_block_size(None)
     monkeypatch.setenv("ECHOKV_K_GROUP", "16")
     assert B.supports_block_size(16) and B.get_supported_kernel_block_sizes() == [MultipleOf(16)]
-    assert B.supports_head_size(128) and B.supports_head_size(64) and not B.supports_head_size(96)
+    # The reference's rule (a multiple of 4 and of the V group), up to 256 channels.
+    assert B.supports_head_size(128) and B.supports_head_size(64) and B.supports_head_size(96)
+    assert B.supports_head_size(256) and not B.supports_head_size(80) and not B.supports_head_size(512)
     assert B.supports_attn_type("decoder") and not B.supports_attn_type("encoder")
     assert B.get_impl_cls() is EchoKVAttentionImpl and B.get_builder_cls() is EchoKVMetadataBuilder
     assert EchoKVMetadataBuilder.get_cudagraph_support(None, Spec()) == AttentionCGSupport.UNIFORM_SINGLE_TOKEN_DECODE

@@ -308,6 +308,42 @@ def test_v_group_and_head_size_variants(device, d, vg, bits, h):
         check(f"prefill {path} D{d} VG{vg} int{bits}", out, ref)
 
 
+@pytest.mark.parametrize("d,bs,kg,vg,h,gqa", [(96, 16, 16, 32, 4, 4), (256, 16, 16, 32, 4, 4), (128, 16, 8, 32, 4, 4),
+                                               (128, 48, 16, 32, 4, 4), (128, 16, 16, 4, 4, 4), (80, 32, 32, 16, 4, 2),
+                                               (96, 16, 16, 32, 2, 20)])
+@pytest.mark.parametrize("bits", [8, 4, 2])
+def test_layouts_outside_the_mfma_kernels(device, d, bs, kg, vg, h, gqa, bits):
+    """Head sizes other than 64 / 128 (up to 256), K groups under 16, block sizes
+    that are not powers of two and V groups under D/16 take the fp32 decode kernel
+    (the reference's PyTorch path serves them there), GQA 20 in two passes of query
+    heads; prefill attends through decode rows. Both equal the oracle."""
+    lens = np.array([1, 17, 300, 64, 1000])
+    store, table = build_layer(device, lens, bits, h=h, d=d, bs=bs, kg=kg, vg=vg, seed=8, outliers=0.02)
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    lens_d = torch.from_numpy(lens).to(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(88)
+    label = f"D{d} BS{bs} KG{kg} VG{vg} H{h} GQA{gqa} int{bits}"
+    q = torch.randn(5, gqa * h, d, device=device, generator=gen).half()
+    ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, d ** -0.5, vectorized=True)
+    for inv in (False, True):
+        got = dec.decode_attention(store, q, table_d, lens_d, d ** -0.5, batch_invariant=inv, num_splits=3)
+        check(f"decode {label}" + (" split schedule" if inv else ""), got, ref)
+    prefill, row = [], 0
+    for n in lens.tolist():
+        nq = min(100, n)
+        prefill.append((row, row + nq, n, 0))
+        row += nq
+    qp = torch.randn(row, gqa * h, d, device=device, generator=gen).half()
+    out = torch.zeros(row, gqa * h, d, device=device)
+    pf.prefill_attention(store, qp, out, prefill, list(range(5)), table_d, d ** -0.5)
+    torch.cuda.synchronize()
+    ref = OA.prefill_attention(ps, qp.float().cpu().numpy(), prefill, list(range(5)), table, d ** -0.5,
+                               vectorized=True)
+    check(f"prefill {label}", out, ref)
+
+
 @pytest.mark.parametrize("bits", [2, 4, 8])
 def test_decode_over_a_layer_view_spanning_more_than_4_gib(device, bits):
     """One layer's view of a pool interleaved across 32 layers (page stride = 32
