@@ -21,7 +21,12 @@ inline int prefill_tile_tokens(int gqa) { return kPrefillRows / gqa; }
 constexpr int kDenseKeys = 64;
 constexpr int kDenseWaves = 8;
 inline int dense_tile_tokens(int gqa) { return 32 * kDenseWaves / gqa; }
-inline long dense_tile_bytes(int D) { return (long)kDenseKeys * D * 6; }
+// A tile holds K as fp16 hi + fp8 lo (3 bytes per channel) and V^T as fp16, padded to
+// whole rounds of the attention kernel's 1 KiB-per-wave DMAs.
+inline long dense_tile_bytes(int D) {
+  const long raw = (long)kDenseKeys * D * 5, round = 1024L * kDenseWaves;
+  return (raw + round - 1) / round * round;
+}
 
 struct WriteTokArgs {
   Lay L;

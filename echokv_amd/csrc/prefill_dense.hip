@@ -5,18 +5,23 @@
 // Pass 1, pack_kernel: one workgroup per (64-key tile of a request's context,
 // KV head) dequantizes the keys once and writes the tile in the layout the
 // attention pass reads:
-//   K rows   [64 keys][D fp16 hi | D fp16 lo]   (hi + lo = the fp32 value to ~2^-22)
+//   K rows   [64 keys][D fp16 hi | D fp8 lo]    (lo = e4m3 of (x - hi) * 2^11: hi + lo
+//                                                is the fp32 value to ~2^-15)
 //   V^T rows [D][64 keys fp16]                  (keys of each 16-key step stored
 //                                                in the MFMA operand order below)
-// Keys past the context and unreadable blocks are zeros.
+// then padding to whole DMA rounds. Keys past the context and unreadable blocks
+// are zeros.
 //
 // Pass 2, flash_kernel: one workgroup (8 waves) per (query tile, KV head). A
 // query tile holds up to 256 / GQA tokens; its rows are (token, GQA head)
 // pairs, 32 per wave. Workspace tiles stream through a three-slot LDS ring by
 // LDS DMA (global_load_lds_dwordx4, 6 per wave per tile), the next tile in
 // flight while the current one is consumed. Per wave and tile:
-//   S^T[key, row] = K Q^T    v_mfma_f32_32x32x16_f16 on K hi and K lo (and Q lo
-//                            for float32 queries), Q held in registers
+//   S^T[key, row] = K Q^T    v_mfma_f32_32x32x16_f16 on K hi (and Q lo for
+//                            float32 queries), Q held in registers; K lo with
+//                            Q as e4m3 on v_mfma_scale_f32_32x32x64_f8f6f4 (its
+//                            scale operand takes the 2^11 back out) into the
+//                            same accumulator: a quarter of the hi pass's cycles
 //   online softmax per row   (the lane holds one row; its other half-wave holds
 //                            the same row's other keys), max moved lazily
 //   O^T[d, row] += V^T P^T   v_mfma_f32_32x32x16_f16, P^T straight from the S^T
@@ -24,8 +29,9 @@
 // with the bottom-right causal limit key <= query position.
 //
 // LDS reads are conflict-free through XOR swizzles applied by the DMA address
-// (the workspace itself stays linear): 16-byte slot s of K row k sits at slot
-// s ^ (k & 15) of its half-row, slot s of V^T row d at s ^ ((d >> 1) & 7).
+// (the workspace itself stays linear): 16-byte slot s of K row k's hi part sits
+// at slot s ^ (k & (D/8 - 1)) of that part, of its lo part at s ^ (k & (D/16 - 1)),
+// slot s of V^T row d at s ^ ((d >> 1) & 7).
 #include "args.h"
 
 namespace ek {
@@ -33,17 +39,27 @@ namespace ek {
 namespace {
 
 typedef float f16v_t __attribute__((ext_vector_type(16)));
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
+// K lo is stored as e4m3 of (x - hi) * 2^kLoShift; |x - hi| <= 2^-11 |x|, so the
+// stored value stays within |x| (e4m3 holds up to 448; larger ones saturate).
+constexpr int kLoShift = 11;
+constexpr float kLoMax = 448.f;
 
 constexpr int kDenseRing = 3;  // workspace tiles in the LDS ring
 
 template <int D>
 struct Ws {
-  static constexpr int KROW = 4 * D;          // bytes per key row (hi then lo)
+  static constexpr int KHI = 2 * D;            // bytes of a key row's hi part (its lo part: D)
+  static constexpr int KROW = 3 * D;           // bytes per key row (hi then lo)
   static constexpr int K_BYTES = kDenseKeys * KROW;
   static constexpr int VROW = 2 * kDenseKeys;  // bytes per V^T row
   static constexpr int V_BYTES = D * VROW;
-  static constexpr int BYTES = K_BYTES + V_BYTES;
-  static constexpr int KSW = D / 8 - 1;       // K swizzle mask (16-byte slots per half-row - 1)
+  static constexpr int ROUND = 1024 * kDenseWaves;
+  static constexpr int BYTES = (K_BYTES + V_BYTES + ROUND - 1) / ROUND * ROUND;  // = dense_tile_bytes(D)
+  static constexpr int KSWH = D / 8 - 1;       // swizzle masks: 16-byte slots of the hi / lo part - 1
+  static constexpr int KSWL = D / 16 - 1;
 };
 
 // Stored position of key k (0..63) in its V^T row: inside each 16-key step,
@@ -180,18 +196,26 @@ __global__ __launch_bounds__(256) void pack_kernel(PackArgs a) {
     }
   }
   uint8_t* tile = a.ws + ((long)blockIdx.x * L.H + h) * W::BYTES;
-  uint8_t* krow = tile + key * W::KROW + 2 * cq * CPT;
+  uint8_t* krow = tile + key * W::KROW;
 #pragma unroll
-  for (int v8 = 0; v8 < CPT / 8; ++v8) {
-    h8_t hi, lo;
+  for (int v16 = 0; v16 < CPT / 16; ++v16) {
+    h8_t hi[2];
+    v4i_t lo;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = kx[8 * v8 + e];
-      hi[e] = (_Float16)x;
-      lo[e] = (_Float16)(x - (float)hi[e]);
+    for (int e = 0; e < 16; e += 2) {
+      const float x0 = kx[16 * v16 + e], x1 = kx[16 * v16 + e + 1];
+      const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+      hi[e >> 3][e & 7] = h0;
+      hi[e >> 3][(e & 7) + 1] = h1;
+      const float l0 = fminf(fmaxf(__builtin_ldexpf(x0 - (float)h0, kLoShift), -kLoMax), kLoMax);
+      const float l1 = fminf(fmaxf(__builtin_ldexpf(x1 - (float)h1, kLoShift), -kLoMax), kLoMax);
+      const int pair = __builtin_amdgcn_cvt_pk_fp8_f32(l0, l1, 0, false) & 0xffff;
+      if (e & 2) lo[e >> 2] |= pair << 16;
+      else lo[e >> 2] = pair;
     }
-    *(h8_t*)(krow + 16 * v8) = hi;
-    *(h8_t*)(krow + 2 * D + 16 * v8) = lo;
+    *(h8_t*)(krow + 2 * (cq * CPT + 16 * v16)) = hi[0];
+    *(h8_t*)(krow + 2 * (cq * CPT + 16 * v16) + 16) = hi[1];
+    *(v4i_t*)(krow + W::KHI + cq * CPT + 16 * v16) = lo;
   }
   const int vp = vpos(key);
 #pragma unroll
@@ -212,7 +236,8 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
   static_assert(NBUF == 2 || NBUF == 3, "two or three ring slots");
   constexpr int NDMA = W::BYTES / 1024 / kDenseWaves;
   static_assert(W::BYTES % (1024 * kDenseWaves) == 0, "tile must split into whole DMA rounds");
-  constexpr int KGROUPS = NS / 2;          // 8-fragment K groups per 64-key tile
+  constexpr int NLO = D / 64;   // 64-channel chunks of K lo
+  constexpr int KGROUPS = NS / 2;          // K fragment groups per 64-key tile (= 2 * NLO)
   static_assert(2 * NDB <= 8, "V^T fragments of two steps fit one group");
   constexpr float kInf = __builtin_inff();
   extern __shared__ __attribute__((aligned(1024))) uint8_t ring[];
@@ -260,12 +285,14 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
     const int p = 1024 * (NDMA * wave + i) + 16 * lane;
     if (p < W::K_BYTES) {
       const int k = p / W::KROW, rb = p % W::KROW;
-      const int half = rb / (2 * D), slot = (rb % (2 * D)) / 16;
-      doff[i] = k * W::KROW + half * 2 * D + 16 * (slot ^ (k & W::KSW));
-    } else {
+      doff[i] = rb < W::KHI ? k * W::KROW + 16 * ((rb / 16) ^ (k & W::KSWH))
+                            : k * W::KROW + W::KHI + 16 * (((rb - W::KHI) / 16) ^ (k & W::KSWL));
+    } else if (p < W::K_BYTES + W::V_BYTES) {
       const int q = p - W::K_BYTES;
       const int d = q / W::VROW, slot = (q % W::VROW) / 16;
       doff[i] = W::K_BYTES + d * W::VROW + 16 * (slot ^ ((d >> 1) & 7));
+    } else {
+      doff[i] = p;  // padding
     }
   }
   const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)ring);
@@ -281,12 +308,35 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
   for (int i = 0; i < NBUF - 1; ++i)
     if (i < n_kt) issue(i);
 
-  // Query fragments (B operand of S^T): row r, channels 16 s + 8 hh .. +8.
+  // Query fragments (B operand of S^T): row r, channels 16 s + 8 hh .. +8 as fp16;
+  // for K lo, channels 64 c + 32 hh .. +32 as e4m3.
   h8_t qf[NS], ql[QLO ? NS : 1];
+  v8i_t qe[NLO];
   {
     const int tok = rv ? r / gqa : 0;
     const int qh = h * gqa + (rv ? r % gqa : 0);
     const long qb = (q_row0 + tok) * a.q_s0 + (long)qh * a.q_s1 + 8 * hh;
+#pragma unroll
+    for (int c = 0; c < NLO; ++c) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float x[8];
+        if (rv) {
+          ld_n<8>(a.q, a.q_dtype, qb - 8 * hh + 64 * c + 32 * hh + 8 * u, x);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = fminf(fmaxf(x[e], -kLoMax), kLoMax);
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          const int lo2 = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w], x[4 * w + 1], 0, false) & 0xffff;
+          const int hi2 = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * w + 2], x[4 * w + 3], 0, false) & 0xffff;
+          qe[c][2 * u + w] = lo2 | (hi2 << 16);
+        }
+      }
+    }
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       float x[8];
@@ -312,20 +362,23 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
   f16v_t s[2];
   h8_t fr[2][8];
 
-  // S^T = K Q^T over two 32-key blocks. K fragments go in groups of 8 (hi and
-  // lo of two 16-channel steps for both blocks): the next group's LDS reads
-  // are in flight while the current group feeds the MFMAs, which alternate
-  // between the two blocks' accumulators (scheduling fences keep that order).
+  // S^T = K Q^T over two 32-key blocks. K fragments go in groups: hi of two
+  // 16-channel steps for both blocks (4 x 16 bytes) and lo of 64-channel chunk
+  // g / 2 for block g % 2 (32 bytes); the next group's LDS reads are in flight
+  // while the current group feeds the MFMAs, which alternate between the two
+  // blocks' accumulators (scheduling fences keep that order).
   auto kload = [&](const uint8_t* buf, int g, h8_t* dst) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int st = 2 * g + (i >> 1), kb = i & 1;
       const int k = 32 * kb + j;
-      const uint8_t* kr = buf + k * W::KROW;
-      const int slot = (2 * st + hh) ^ (k & W::KSW);
-      dst[2 * i] = *(const h8_t*)(kr + 16 * slot);
-      dst[2 * i + 1] = *(const h8_t*)(kr + 2 * D + 16 * slot);
+      dst[i] = *(const h8_t*)(buf + k * W::KROW + 16 * ((2 * st + hh) ^ (k & W::KSWH)));
     }
+    const int k = 32 * (g & 1) + j;
+    const uint8_t* lr = buf + k * W::KROW + W::KHI;
+    const int s0 = 4 * (g >> 1) + 2 * hh;
+    dst[4] = *(const h8_t*)(lr + 16 * (s0 ^ (k & W::KSWL)));
+    dst[5] = *(const h8_t*)(lr + 16 * ((s0 + 1) ^ (k & W::KSWL)));
   };
   auto qk = [&](const uint8_t* buf) {
     s[0] = f16v_t{};
@@ -339,13 +392,21 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int st = 2 * g + (i >> 1), kb = i & 1;
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * i], qf[st], s[kb], 0, 0, 0);
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], qf[st], s[kb], 0, 0, 0);
       }
+      {
+        const v4i_t x0 = __builtin_bit_cast(v4i_t, f[4]), x1 = __builtin_bit_cast(v4i_t, f[5]);
+        const v8i_t lo = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+        // e4m3 x e4m3; B's scale 2^(116 - 127) undoes the stored 2^11.
+        s[g & 1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(lo, qe[g >> 1], s[g & 1], 0, 0, 0, 127, 0,
+                                                                   127 - kLoShift);
+      }
+      if constexpr (QLO) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int st = 2 * g + (i >> 1), kb = i & 1;
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * i + 1], qf[st], s[kb], 0, 0, 0);
-        if constexpr (QLO) s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2 * i], ql[st], s[kb], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+          const int st = 2 * g + (i >> 1), kb = i & 1;
+          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], ql[st], s[kb], 0, 0, 0);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
