@@ -124,6 +124,7 @@ def run(args) -> dict:
 
     from echokv_amd._util import to_device
     from echokv_amd.kernels.decode import decode_attention
+    from echokv_amd.tiered_cache import HeaderWriter
     from echokv_amd.write_plan import stage_plan
 
     dev = torch.device("cuda:0")
@@ -146,6 +147,23 @@ def run(args) -> dict:
     int4 = [li for li in range(LAYERS) if tiers[li] == 4]
     scale = D ** -0.5
     inv = args.schedule == "split"
+    headers = HeaderWriter(stores)
+
+    def stage(plan, opened):
+        """The step's plan and every layer's new page headers in one upload; the
+        headers in one launch (the same blocks open in every layer)."""
+        batch = all(o is not None and np.array_equal(o[0], opened[0][0]) for o in opened)
+        meta, extra = stage_plan(plan, dev, (opened[0][0], np.concatenate([o[1] for o in opened])) if batch else None)
+        shared.apply_res_map(*extra[:4])
+        if batch:
+            headers.check(opened[0][0])
+            headers.write(extra[4], extra[5])
+        else:
+            for li, s in enumerate(stores):
+                if opened[li] is not None:
+                    s.write_headers(to_device(torch.from_numpy(opened[li][0]), dev),
+                                    to_device(torch.from_numpy(opened[li][1]), dev))
+        return meta
 
     def step(i):
         pos = ctx - 1 + i  # position of this step's new token
@@ -154,12 +172,9 @@ def run(args) -> dict:
         opened = [s.prepare(plan, int(t)) for s, t in zip(stores, tiers)]
         shared.commit(plan)
         lens = pos + 1
-        meta, extra = stage_plan(plan, dev, None)
-        shared.apply_res_map(*extra[:4])
+        meta = stage(plan, opened)
         lens_d = to_device(torch.from_numpy(lens), dev)  # pinned, non-blocking: the host keeps planning
         for li, s in enumerate(stores):
-            if opened[li] is not None:
-                s.write_headers(to_device(torch.from_numpy(opened[li][0]), dev), to_device(torch.from_numpy(opened[li][1]), dev))
             s.apply(meta, kn[li], vn[li], krefs[li])
             decode_attention(s, q[li], table_d, lens_d, scale, blocks_per_split=args.bps, out=out[li],
                              num_splits=num_splits, workspace=ws, tier=int(tiers[li]), batch_invariant=inv)
@@ -207,11 +222,7 @@ def run(args) -> dict:
         plan = shared.planner.plan(slots)
         opened = [s.prepare(plan, int(t)) for s, t in zip(stores, tiers)]
         shared.commit(plan)
-        meta, extra = stage_plan(plan, dev, None)
-        shared.apply_res_map(*extra[:4])
-        for li, s in enumerate(stores):
-            if opened[li] is not None:
-                s.write_headers(to_device(torch.from_numpy(opened[li][0]), dev), to_device(torch.from_numpy(opened[li][1]), dev))
+        meta = stage(plan, opened)
         tok_buf.copy_(meta.tok)
         if meta.n_fin:
             fin_buf[: meta.n_fin].copy_(meta.fin)

@@ -23,7 +23,7 @@ _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTS = (
     "echokv_error_string", "echokv_write_tokens", "echokv_finalize_k", "echokv_write_step", "echokv_seal_groups",
-    "echokv_gather",
+    "echokv_gather", "echokv_write_headers",
     "echokv_store_blocks", "echokv_decode", "echokv_decode_static", "echokv_prefill", "echokv_prefill_dense",
     "echokv_prefill_dense_workspace", "echokv_prefill_own_group",
     "echokv_dequant_dense", "echokv_canary_kl",
@@ -57,6 +57,7 @@ _SIGS = {
     "echokv_write_step": [LP, P, P, I64, I64, P, I64, I64, I32, P, I64, I64, P, P, I64, RP, P, I64, I64, P],
     "echokv_seal_groups": [LP, P, P, I64, RP, P],
     "echokv_gather": [LP, P, P, P, RP, P, P, I64, P, P, P],
+    "echokv_write_headers": [P, I32, I64, P, I64, P, P],
     "echokv_store_blocks": [LP, P, P, I64, P, P, I32, P],
     "echokv_decode": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, I32, P, P, P,
                       I64, I64, I32, P],

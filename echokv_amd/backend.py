@@ -53,7 +53,7 @@ from echokv_amd.controller import SUPPORTED_BITS, LayerController
 from echokv_amd.host_slots import host_lens_and_slots, is_dummy_step
 from echokv_amd.kernels import decode as dec
 from echokv_amd.kernels import prefill as pf
-from echokv_amd.tiered_cache import TieredKVCache, TieredLayout
+from echokv_amd.tiered_cache import HeaderWriter, TieredKVCache, TieredLayout
 from echokv_amd.write_plan import SharedState, WriteMeta
 
 # Head sizes the MFMA kernels are built for; others up to MAX_HEAD_SIZE take the
@@ -277,7 +277,8 @@ class EchoKVMetadataBuilder(AttentionMetadataBuilder):
         self.impls = [layer.impl for layer in self.layers]
         for impl, cache in zip(self.impls, caches):
             impl.bind(cache, self.shared)
-        tail = self.cap * (4 + 3 * len(self.impls)) + 64
+        self.headers = HeaderWriter([impl.store for impl in self.impls])
+        tail = self.cap * (5 + 2 * len(self.impls)) + 64
         self.image = StepImage(self.cap, cfg.canary_max_q, 3 + cfg.k_group, tail, self.device)
         impl0 = self.impls[0]
         dev = torch.device(self.device)
@@ -401,14 +402,15 @@ class EchoKVMetadataBuilder(AttentionMetadataBuilder):
                     opened.append(st.open_blocks(opens, impl.controller.bits, protect=plan.touched_np))
         shared.commit(plan)
         tail = [plan.res_map_block, plan.res_map_value, plan.res_group_slot, plan.res_group_value]
-        for blocks, headers in opened:
-            tail += [blocks, np.ascontiguousarray(headers).view(np.int64).reshape(-1)]
+        if opened:  # the same blocks in every layer: their ids once, then each layer's headers
+            self.headers.check(opens)
+            tail += [opens, np.concatenate([np.ascontiguousarray(h).view(np.int64).reshape(-1) for _, h in opened])]
         tok = np.stack([plan.tok_slot, plan.tok_res, plan.tok_sealed, plan.tok_kref])
         fin_count, canary_rows, dec_views, tok_d, fin_d, views = self.image.upload(
             plan.n_fin, canary, decode, tok, plan.fin, tail)
         shared.apply_res_map(*views[:4])
-        for impl, ids, hdr in zip(self.impls, views[4::2], views[5::2]):
-            impl.store.write_headers(ids, hdr.view(-1, 2).view(torch.uint8))
+        if opened:
+            self.headers.write(views[4], views[5])
         write = WriteMeta(tok=tok_d, fin=fin_d, fin_count=fin_count, n_rows=plan.n_rows, n_fin=plan.n_fin)
         return write, canary_rows, dec_views
 

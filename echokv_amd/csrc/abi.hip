@@ -139,6 +139,16 @@ int echokv_gather(const echokv_layout* L, const uint8_t* pages, const int64_t* b
   return launched(ek::launch_gather(a, n, (hipStream_t)stream));
 }
 
+int echokv_write_headers(const uint64_t* page_bases, int32_t n_layers, int64_t page_stride, const int64_t* ids,
+                         int64_t n, const uint8_t* headers, echokv_stream_t stream) {
+  if (n_layers < 0 || n < 0 || page_stride < 16 || page_stride % 4) return ECHOKV_EINVAL;
+  if (n_layers == 0 || n == 0) return ECHOKV_OK;
+  if ((int64_t)n_layers * n > INT32_MAX || ((uintptr_t)headers & 3)) return ECHOKV_EINVAL;
+  if (!page_bases || !ids || !headers) return ECHOKV_EINVAL;
+  return launched(ek::launch_write_headers(page_bases, page_stride, ids, (const uint32_t*)headers, n_layers, n,
+                                           (hipStream_t)stream));
+}
+
 int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* blocks, int64_t n, const float* k,
                         const float* v, int32_t bits, echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;

@@ -284,6 +284,8 @@ hipError_t launch_own_group(const OwnGroupArgs& a, long n, hipStream_t s);
 hipError_t launch_seal(const SealArgs& a, long n, hipStream_t s);
 hipError_t launch_store_blocks(const StoreBlkArgs& a, long n, hipStream_t s);
 hipError_t launch_gather(const GatherArgs& a, long n, hipStream_t s);
+hipError_t launch_write_headers(const uint64_t* page_bases, long page_stride, const int64_t* ids,
+                                const uint32_t* hdr, int n_layers, long n, hipStream_t s);
 hipError_t launch_dequant_dense(const DenseArgs& a, long n, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s);
 // Ranges of the balanced schedule for a batch on the current device: one per

@@ -823,6 +823,29 @@ hipError_t launch_write_step(const StepArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(write_step_kernel, dim3((unsigned)(a.fin_grid + a.n_rows)), dim3(kThreads), lds, s, a);
   return hipGetLastError();
 }
+// Page headers of a step's freshly opened blocks in every layer, one launch: layer
+// l's 16 header bytes of block ids[i] are hdr[l * n + i], at page_bases[l] +
+// ids[i] * page_stride. Four 32-bit stores (page bases need only 4-byte alignment).
+__global__ __launch_bounds__(kThreads) void write_headers_kernel(const uint64_t* page_bases, long page_stride,
+                                                                  const int64_t* ids, const uint32_t* hdr,
+                                                                  int n_layers, long n) {
+  const long i = (long)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n_layers * n) return;
+  const long l = i / n, b = i - l * n;
+  uint32_t* dst = (uint32_t*)(page_bases[l] + (uint64_t)(ids[b] * page_stride));
+  const uint32_t* src = hdr + 4 * i;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dst[e] = src[e];
+}
+
+hipError_t launch_write_headers(const uint64_t* page_bases, long page_stride, const int64_t* ids,
+                                const uint32_t* hdr, int n_layers, long n, hipStream_t s) {
+  const long total = n_layers * n;
+  hipLaunchKernelGGL(write_headers_kernel, dim3((unsigned)((total + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
+                     page_bases, page_stride, ids, hdr, n_layers, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_seal(const SealArgs& a, long n, hipStream_t s) {
   hipLaunchKernelGGL(seal_kernel, dim3((unsigned)n), dim3(kThreads), 0, s, a);
   return hipGetLastError();

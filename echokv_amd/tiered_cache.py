@@ -227,6 +227,36 @@ class ChunkPool:
         return opens
 
 
+class HeaderWriter:
+    """The page headers of a step's opened blocks in every layer of a cache group
+    (the same blocks open in every layer, each at its layer's tier), written by one
+    launch (``echokv_write_headers``) instead of one index write per layer."""
+
+    def __init__(self, stores) -> None:
+        self.stores = list(stores)
+        strides = {s.pages.stride(0) for s in self.stores}
+        if len(strides) != 1:
+            raise ValueError("the layers of one cache group must share the page stride")
+        self.stride = strides.pop()
+        self.num_blocks = min(s.pages.shape[0] for s in self.stores)
+        bases = torch.tensor([s.pages.data_ptr() for s in self.stores], dtype=torch.int64)
+        self.bases = to_device(bases, self.stores[0].device)
+
+    def check(self, ids: np.ndarray) -> None:
+        """Host check of the block ids before they go to the device."""
+        if ids.size and (ids.min() < 0 or ids.max() >= self.num_blocks):
+            raise ValueError(f"header block ids outside the {self.num_blocks} pages")
+
+    def write(self, ids: torch.Tensor, headers: torch.Tensor) -> None:
+        """``ids`` int64 ``[n]``; ``headers`` ``[n_layers * n * 16]`` bytes (any dtype view),
+        layer-major, both on the device."""
+        n = ids.numel()
+        if headers.numel() * headers.element_size() != len(self.stores) * n * 16:
+            raise ValueError("headers must hold 16 bytes per layer and block")
+        _lib.call("echokv_write_headers", _lib.ptr(self.bases), len(self.stores), self.stride, _lib.ptr(ids), n,
+                  _lib.ptr(headers), _lib.stream())
+
+
 class TieredKVCache:
     """One layer's tiered store over ``pages``: a uint8 ``[num_blocks, >= page_bytes]`` device view."""
 

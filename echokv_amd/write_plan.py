@@ -213,15 +213,19 @@ class WriteMeta:
 
 
 def stage_plan(plan: WritePlan, device, opened=None):
-    """``plan.stage`` (and ``opened`` headers) in one host-to-device copy: returns
-    ``(WriteMeta, (res blocks, res values, group slots, group values, opened ids, headers))``."""
+    """``plan.stage`` (and ``opened`` = (block ids, headers ``[rows, 16]`` uint8) -- one
+    layer's rows, or several layers' one after another) in one host-to-device copy:
+    returns ``(WriteMeta, (res blocks, res values, group slots, group values, opened
+    ids, headers))``."""
     t, f, w = plan.n_rows, plan.n_fin, 3 + plan.k_group
     image = plan.stage
-    n_open = 0
+    n_open = n_hdr = 0
     if opened is not None:
         ids = _host.as_i64(opened[0])
         n_open = ids.size
-        image = np.concatenate([image, ids, np.ascontiguousarray(opened[1]).view(np.int64).reshape(-1)])
+        hdr = np.ascontiguousarray(opened[1]).view(np.int64).reshape(-1)
+        n_hdr = hdr.size
+        image = np.concatenate([image, ids, hdr])
     dev = to_device(torch.from_numpy(image), device)
     o = 1 + 4 * t
     meta = WriteMeta(tok=dev[1:o].view(4, t), fin=dev[o : o + f * w].view(f, w), fin_count=dev[0:1], n_rows=t,
@@ -233,5 +237,5 @@ def stage_plan(plan: WritePlan, device, opened=None):
         o += n
     headers = (None, None)
     if opened is not None:
-        headers = (dev[o : o + n_open], dev[o + n_open : o + 3 * n_open].view(-1, 2).view(torch.uint8))
+        headers = (dev[o : o + n_open], dev[o + n_open : o + n_open + n_hdr].view(-1, 2).view(torch.uint8))
     return meta, (*maps, *headers)

@@ -103,6 +103,15 @@ int echokv_write_step(const echokv_layout* L, uint8_t* pages,
 int echokv_seal_groups(const echokv_layout* L, uint8_t* pages, const int64_t* ev, int64_t n,
                        const echokv_residual* res, echokv_stream_t stream);
 
+/* The page headers of a step's opened blocks in every layer of a cache group, one
+ * launch: layer l's header (16 bytes: tag, then the pool chunk ids) of block ids[i]
+ * is headers[(l * n + i) * 16 ..], written at page_bases[l] + ids[i] * page_stride
+ * (page_bases: device array of n_layers page-base addresses, 4-byte aligned; ids
+ * must name blocks of every layer). Replaces the per-layer header assignment of
+ * echokv_vllm/tiered_cache.py:258-307 (open_blocks / write_headers) for a whole step. */
+int echokv_write_headers(const uint64_t* page_bases, int32_t n_layers, int64_t page_stride, const int64_t* ids,
+                         int64_t n, const uint8_t* headers, echokv_stream_t stream);
+
 /* Dequantized K and V (float32 [n, H, D]) of tokens (blk[i], off[i]); never-opened
  * blocks read as zeros, a block's open K group reads the residual.
  * Replaces echokv_vllm/tiered_cache.py:451-478 (gather). */

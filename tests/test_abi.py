@@ -113,7 +113,8 @@ def test_own_group_prefill_argument_checks(lib):
 
 def test_prefill_dense_workspace_size_and_argument_checks(lib):
     L = _layout()
-    assert lib.echokv_prefill_dense_workspace(C.byref(L), 3) == 3 * 8 * 64 * 128 * 6
+    # 3 tiles x 8 KV heads x 64 keys x 128 channels x (K fp16 hi + K e4m3 lo + V fp16 = 5 bytes)
+    assert lib.echokv_prefill_dense_workspace(C.byref(L), 3) == 3 * 8 * 64 * 128 * 5
     assert lib.echokv_prefill_dense_workspace(C.byref(_layout(head_size=96)), 3) < 0
     assert lib.echokv_prefill_dense_workspace(C.byref(L), -1) < 0
     assert _prefill_dense(lib, _layout(head_size=96)) == 2   # D must be 64 or 128

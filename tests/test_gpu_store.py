@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import scripts as S
+from echokv_amd.tiered_cache import TieredKVCache, TieredLayout
 from gpu_util import gpu_replay, gpu_store
 from host_sim import golden
 
@@ -216,3 +217,29 @@ def test_fused_step_matches_finalize_then_write_and_oracle(device, monkeypatch):
     bad = np.flatnonzero((fused.pages.cpu().numpy() != sim.ps.pages).any(axis=1))
     assert bad.size == 0, f"pages {bad.tolist()} differ from the oracle"
     np.testing.assert_array_equal(fused.res_k[live].float().cpu().numpy(), sim.ps.res_k[live.cpu().numpy()])
+
+
+def test_batched_headers_equal_per_layer_writes(device):
+    """One echokv_write_headers launch writes every layer's opened-block headers
+    exactly where the per-layer index writes put them; other bytes stay as they were."""
+    from echokv_amd.tiered_cache import HeaderWriter
+
+    layout = TieredLayout(8, 128, 16, 8, 16, 32)
+    rng = np.random.default_rng(5)
+    stores = []
+    for _ in range(3):
+        pages = torch.from_numpy(rng.integers(0, 256, (40, layout.page_bytes), dtype=np.uint8)).to(device)
+        stores.append(TieredKVCache(layout, pages, residual_slots=4))
+    before = [s.pages.clone() for s in stores]
+    ids = np.array([3, 17, 0, 39], np.int64)
+    hdr = rng.integers(0, 256, (3, ids.size, 16), dtype=np.uint8)
+    hw = HeaderWriter(stores)
+    hw.check(ids)
+    hw.write(torch.from_numpy(ids).to(device), torch.from_numpy(hdr.reshape(-1)).to(device))
+    torch.cuda.synchronize()
+    for li, s in enumerate(stores):
+        want = before[li].clone()
+        want[torch.from_numpy(ids).to(device), :16] = torch.from_numpy(hdr[li]).to(device)
+        assert torch.equal(s.pages, want)
+    with pytest.raises(ValueError):
+        hw.check(np.array([40]))
