@@ -986,7 +986,20 @@ struct SpanSink {
   long part_row0;
   int part_stride;
   bool direct;
+  // Balanced schedule: blocks of the workgroup's range after this span, and the
+  // range's length (0: no priorities).
+  int rem_after, total;
 };
+
+// Wave priority from the share of the workgroup's range still ahead of it: the
+// co-resident workgroups of a CU start at different times, and the one with the
+// most left issues first, so they finish together instead of in start order.
+__device__ __forceinline__ void range_priority(int left, int total) {
+  if (4 * left > 3 * total) __builtin_amdgcn_s_setprio(3);
+  else if (4 * left > 2 * total) __builtin_amdgcn_s_setprio(2);
+  else if (4 * left > total) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+}
 
 // Blocks [b_start, b_end) of sequence `seq` for the KV heads of head group hg
 // (one wave per head).
@@ -1085,6 +1098,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
       wg_barrier();
       if (tt + R::NBUF - 1 < n_tiles) issue(tt + R::NBUF - 1);
       const int b = tt >> tpb_shift;
+      if (sink.total > 0 && (tt & 3) == 0) range_priority(b_end - c0 - b + sink.rem_after, sink.total);
       if (!((m_blk >> b) & 1)) continue;
       if (!piped(tt)) {
         rare = true;
@@ -1181,7 +1195,7 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   const int b_start = split * bps;
   const int b_end = b_start + bps < n_blocks ? b_start + bps : n_blocks;
   decode_span<D, BITS, QLO>(a, seq, b_start, b_end, (int)(item % n_hg), wv, lane, ring_lds, ring0,
-                            SpanSink{seq * a.hq * a.num_splits + split, a.num_splits, false});
+                            SpanSink{seq * a.hq * a.num_splits + split, a.num_splits, false, 0, 0});
 }
 
 // ---------------------------------------------------------------------------
@@ -1271,7 +1285,7 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
       const bool whole = pos == first && end == first + nb;
       const long slot = 2 * r + (pos == lo ? 0 : 1);
       decode_span<D, BITS, QLO>(a, seq, (int)(pos - first), (int)(end - first), hg, wv, lane, ring_lds, ring0,
-                                SpanSink{slot * a.hq, 1, whole});
+                                SpanSink{slot * a.hq, 1, whole, (int)(hi - end), (int)(hi - lo)});
     }
     pos = end;
     first += nb;
