@@ -457,11 +457,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], sl2, -ms));
-        s[kb][i] = p;
-        lsum += p;
-      }
+      for (int i = 0; i < 16; ++i) s[kb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], sl2, -ms));
     }
   };
   // O^T += V^T P^T, 16 keys per step; keys 32..63's fragments load while
@@ -480,6 +476,10 @@ __global__ __launch_bounds__(64 * kDenseWaves) void flash_kernel(FlashArgs a) {
         h8_t pb;
 #pragma unroll
         for (int e = 0; e < 8; ++e) pb[e] = (_Float16)s[kb][r0 + e];
+        // The row sum takes the fp16 weights the PV product uses (two per dot).
+        const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) lsum = __builtin_amdgcn_fdot2(h2_t{pb[e], pb[e + 1]}, one, lsum, false);
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
           acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[k2 * NDB + db], pb, acc[db], 0, 0, 0);
