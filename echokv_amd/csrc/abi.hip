@@ -292,10 +292,13 @@ int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* 
                    const int32_t* tiles, int64_t n_tiles, int32_t tile_m, const int32_t* block_table, int64_t bt_s0,
                    float softmax_scale, int32_t own_group, float* lse, echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;
-  if (L->head_size != 64 && L->head_size != 128) return ECHOKV_ESHAPE;
   if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
   const int gqa = num_q_heads / L->num_kv_heads;
-  if (gqa > ek::kPrefillRows || tile_m != ek::prefill_tile_tokens(gqa)) return ECHOKV_ESHAPE;
+  // The MFMA kernel: head size 64 or 128, at most kPrefillRows query rows per
+  // tile. Any other layout (head size up to kMaxAnyD) takes the fp32 kernel.
+  const bool mfma = (L->head_size == 64 || L->head_size == 128) && gqa <= ek::kPrefillRows;
+  if (!mfma && (L->head_size > ek::kMaxAnyD || own_group)) return ECHOKV_ESHAPE;
+  if (tile_m != (mfma ? ek::prefill_tile_tokens(gqa) : ek::any_tile_tokens(gqa))) return ECHOKV_ESHAPE;
   if (own_group != 0 && own_group != 1) return ECHOKV_EINVAL;
   if (own_group && (L->k_group & (L->k_group - 1))) return ECHOKV_ESHAPE;
   if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;
@@ -324,7 +327,16 @@ int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* 
   a.scale_log2 = softmax_scale * 1.4426950408889634f;
   a.og_mask = own_group ? ~(L->k_group - 1) : 0;
   a.lse = lse;
-  return launched(ek::launch_prefill(a, n_tiles, (hipStream_t)stream));
+  a.g0 = 0;
+  a.gs = gqa;
+  if (mfma) return launched(ek::launch_prefill(a, n_tiles, (hipStream_t)stream));
+  if (n_tiles > INT32_MAX / L->num_kv_heads) return ECHOKV_EINVAL;
+  for (int g0 = 0; g0 < gqa; g0 += 16) {  // passes of 16 query heads per KV head
+    a.g0 = g0;
+    a.gs = gqa - g0 < 16 ? gqa - g0 : 16;
+    if (ek::launch_prefill_any(a, n_tiles, (hipStream_t)stream) != hipSuccess) return ECHOKV_ELAUNCH;
+  }
+  return ECHOKV_OK;
 }
 
 int64_t echokv_prefill_dense_workspace(const echokv_layout* L, int64_t n_packs) {

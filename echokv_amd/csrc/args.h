@@ -227,6 +227,7 @@ struct PrefillArgs {
   float scale_log2;
   int og_mask;  // nonzero: a query at position p sees keys < (p & og_mask) (its own K group left out)
   float* lse;   // nullable: [rows, hq] log2-domain log-sum-exp of each query row's scores
+  int g0, gs;   // fp32 kernel (prefill_any): this pass's query heads of each KV head, gs <= 16
 };
 
 struct PackArgs {
@@ -298,6 +299,10 @@ hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s);
 constexpr int kMaxAnyD = 256;
 hipError_t launch_decode_any(const DecodeArgs& a, hipStream_t s);
 hipError_t launch_merge_any(const MergeArgs& a, hipStream_t s);
+// Prefill for those layouts: tiles of any_tile_tokens(gqa) query tokens, one
+// workgroup per (tile, KV head), each query's causal context streamed once per tile.
+inline int any_tile_tokens(int gqa) { return gqa >= 16 ? 1 : 16 / gqa; }
+hipError_t launch_prefill_any(const PrefillArgs& a, long n_tiles, hipStream_t s);
 hipError_t launch_canary(const CanaryArgs& a, int num_layers, hipStream_t s);
 size_t canary_lds_bytes(int d, int nbits, int rows);  // one canary workgroup's LDS
 hipError_t launch_prefill(const PrefillArgs& a, long n_tiles, hipStream_t s);

@@ -263,11 +263,199 @@ __global__ __launch_bounds__(256) void merge_any_kernel(MergeArgs a) {
     if (lane + 64 * e < D) st(a.out, a.out_dtype, o_row * a.o_s0 + head * a.o_s1 + lane + 64 * e, num[e] / den);
 }
 
+// Chunked prefill for the same layouts (echokv_vllm/kernels/prefill.py:210-236, the
+// reference's gather + bottom-right causal SDPA): one workgroup per (tile of
+// query tokens, KV head). Its columns are (token i, query head g) pairs, at most
+// 16; column (i, g) sees keys < q_pos0 + i + 1 of its request's context. The
+// keys stream once per tile in 64-key tiles exactly as in decode_any_kernel, and
+// each column's row is normalized and written at the end.
+__global__ __launch_bounds__(kAnyThreads) void prefill_any_kernel(PrefillArgs a) {
+  const Lay& L = a.L;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int h = (int)(blockIdx.x % L.H);
+  const int32_t* td = a.tiles + (long)(blockIdx.x / L.H) * 5;
+  const long q_row0 = td[0];
+  const int n_tok = td[1], q_pos0 = td[2], ctx = td[3];
+  const long bt_row = td[4];
+  const int gs = a.gs;
+  const int n_cols = n_tok * gs;  // <= 16 (the host sizes tiles so)
+  const long kv_end = q_pos0 + n_tok < ctx ? q_pos0 + n_tok : ctx;
+
+  __shared__ __align__(16) float qs[kAnyCols * kMaxAnyD];
+  __shared__ float ps[kAnyCols][kAnyTile];
+  __shared__ float alpha[kAnyCols];
+  __shared__ long rbs[kAnyTile], pbs[kAnyTile], kres[kAnyTile];
+  __shared__ int offs[kAnyTile], bits_s[kAnyTile];
+
+  const int D = L.D, quads = D / 4, G = D / L.VG;
+  const int qh0 = h * a.gqa + a.g0;
+  for (int i = tid; i < n_cols * D; i += kAnyThreads) {
+    const int c = i / D, d = i - c * D;
+    const int tok = c / gs, g = c - tok * gs;
+    qs[i] = ld(a.q, a.q_dtype, (q_row0 + tok) * a.q_s0 + (long)(qh0 + g) * a.q_s1 + d) * a.scale_log2;
+  }
+
+  float m_run[4], l_run[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m_run[i] = -__builtin_inff();
+    l_run[i] = 0.f;
+  }
+  const int NT = kAnyThreads / D;
+  const int r = tid / D, d = tid - r * D;
+  float o[kAnyCols];
+#pragma unroll
+  for (int c = 0; c < kAnyCols; ++c) o[c] = 0.f;
+
+  for (long t0 = 0; t0 < kv_end; t0 += kAnyTile) {
+    __syncthreads();
+    if (tid < kAnyTile) {
+      const long pos = t0 + tid;
+      long rb = -2, pb = 0, kr = -1;
+      int off = 0, bits = 2;
+      if (pos < kv_end) {
+        const long b = pos / L.BS;
+        off = (int)(pos - b * L.BS);
+        const long blk = a.bt[bt_row * a.bt_s0 + b];
+        if (blk >= 0 && blk < L.nb) {
+          pb = blk * L.stride;
+          bits = tier_of(a.pages[pb]);
+          rb = row_base(a.pages, L, blk, off, bits);
+          const long rs = a.block_res[blk];
+          if (rs >= 0 && rs < a.res.rows && a.res_group[rs] == off / L.KG)
+            kr = rs * a.res.s0 + (long)(off % L.KG) * a.res.s1 + (long)h * a.res.s2;
+        }
+      }
+      rbs[tid] = rb;
+      pbs[tid] = pb;
+      kres[tid] = kr;
+      offs[tid] = off;
+      bits_s[tid] = bits;
+    }
+    __syncthreads();
+
+    {
+      const int j = tid >> 2, p = tid & 3;
+      float s[kAnyCols];
+#pragma unroll
+      for (int c = 0; c < kAnyCols; ++c) s[c] = 0.f;
+      const long rb = rbs[j];
+      if (rb >= 0) {
+        const long kr = kres[j];
+        const int bits = bits_s[j];
+        const uint8_t* kp = a.pages + rb + (long)h * (D * bits / 8);
+        const long se = pbs[j] + 2 * (((long)(offs[j] / L.KG) * L.H + h) * D);
+        for (int q4 = p; q4 < quads; q4 += 4) {
+          float k[4];
+          if (kr >= 0) {
+            ld4(a.res.ptr, a.res.dtype, kr + 4 * q4, k);
+          } else {
+            const uint32_t kc = load_codes4(kp + q4 * (bits / 2), bits);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float ks = (float)*f16p(a.pages, se + L.o_ks + 2 * (4 * q4 + e));
+              const float km = (float)*f16p(a.pages, se + L.o_km + 2 * (4 * q4 + e));
+              k[e] = code_at(kc, e, bits) * ks + km;
+            }
+          }
+#pragma unroll
+          for (int c = 0; c < kAnyCols; ++c) {
+            if (c < n_cols) {
+              const float4 q = *(const float4*)&qs[c * D + 4 * q4];
+              s[c] += q.x * k[0] + q.y * k[1] + q.z * k[2] + q.w * k[3];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < kAnyCols; ++c) {
+        s[c] += __shfl_xor(s[c], 1, 64);
+        s[c] += __shfl_xor(s[c], 2, 64);
+      }
+      if (p == 0) {
+        const long pos = t0 + j;
+#pragma unroll
+        for (int c = 0; c < kAnyCols; ++c) {
+          if (c < n_cols) {
+            const long lim = q_pos0 + c / gs + 1;  // bottom-right causal: keys <= the query's position
+            ps[c][j] = (rb == -2 || pos >= lim) ? -__builtin_inff() : s[c];
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = wv + 4 * i;
+      if (c < n_cols) {
+        const float x = ps[c][lane];
+        const float m_new = fmaxf(m_run[i], wave_max(x));
+        const bool none = m_new == -__builtin_inff();
+        const float pr = none ? 0.f : __builtin_amdgcn_exp2f(x - m_new);
+        const float al = none ? 1.f : __builtin_amdgcn_exp2f(m_run[i] - m_new);
+        l_run[i] = l_run[i] * al + wave_sum(pr);
+        m_run[i] = m_new;
+        ps[c][lane] = pr;
+        if (lane == 0) alpha[c] = al;
+      }
+    }
+    __syncthreads();
+
+    if (r < NT) {
+#pragma unroll
+      for (int c = 0; c < kAnyCols; ++c)
+        if (c < n_cols) o[c] *= alpha[c];
+      for (int j = r; j < kAnyTile; j += NT) {
+        const long rb = rbs[j];
+        if (rb < 0) continue;
+        const int bits = bits_s[j];
+        const long vb = rb + (long)(L.H + h) * (D * bits / 8) + ((d * bits) >> 3);
+        const float code = (float)((a.pages[vb] >> ((d * bits) & 7)) & ((1u << bits) - 1u));
+        const long ve = ((long)offs[j] * L.H + h) * G + d / L.VG;
+        const float v = code * (float)*f16p(a.pages, pbs[j] + L.o_vs + 2 * ve) +
+                        (float)*f16p(a.pages, pbs[j] + L.o_vm + 2 * ve);
+#pragma unroll
+        for (int c = 0; c < kAnyCols; ++c)
+          if (c < n_cols) o[c] += ps[c][j] * v;
+      }
+    }
+  }
+
+  // Sum O's token shares, normalize, write each column's row.
+  __syncthreads();
+  if (r < NT) {
+#pragma unroll
+    for (int c = 0; c < kAnyCols; ++c)
+      if (c < n_cols) qs[(r * n_cols + c) * D + d] = o[c];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = wv + 4 * i;
+      if (c < n_cols) alpha[c] = l_run[i] > 0.f ? 1.f / l_run[i] : 0.f;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < n_cols * D; i += kAnyThreads) {
+    const int c = i / D, dd = i - c * D;
+    float x = 0.f;
+    for (int rr = 0; rr < NT; ++rr) x += qs[(rr * n_cols + c) * D + dd];
+    const int tok = c / gs, g = c - tok * gs;
+    st(a.out, a.out_dtype, (q_row0 + tok) * a.o_s0 + (long)(qh0 + g) * a.o_s1 + dd, x * alpha[c]);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_decode_any(const DecodeArgs& a, hipStream_t s) {
   const long wgs = a.num_seqs * a.L.H * a.num_splits;
   hipLaunchKernelGGL(decode_any_kernel, dim3((unsigned)wgs), dim3(kAnyThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_any(const PrefillArgs& a, long n_tiles, hipStream_t s) {
+  hipLaunchKernelGGL(prefill_any_kernel, dim3((unsigned)(n_tiles * a.L.H)), dim3(kAnyThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -20,9 +20,10 @@ through LDS. ``dequant_dense`` keeps the reference's dense-dequantization
 entry point (``[total_ctx, H, D]`` K/V).
 
 Both kernels are built for head sizes 64 and 128 (and at most ``ROWS`` query
-heads per KV head). Any other layout (the reference's PyTorch path) attends
-through decode rows: query ``i`` of a chunk is one decode row over its context's
-first ``ctx - nq + i + 1`` keys (``prefill_attention_rows``).
+heads per KV head). Any other layout (the reference's PyTorch path serves them)
+takes an fp32 kernel through the same entry point (``echokv_prefill``): tiles of
+``any_block_m(gqa)`` query tokens, so a workgroup's (token, query head) columns
+are at most 16, each tile streaming its causal context once.
 """
 
 from __future__ import annotations
@@ -38,7 +39,6 @@ ROWS = 128  # query rows (tokens x GQA heads) per workgroup of the fused kernel
 FUSED_MAX_CHUNK = 64  # the fused kernel only when every chunk is this short
 DENSE_ROWS = 256  # query rows per workgroup of the two-pass path
 DENSE_KEYS = 64  # keys per workspace tile
-ROWS_WORKSPACE_BYTES = 256 << 20  # split workspace of one slice of decode rows
 
 
 def gqa_pad(gqa: int) -> int:
@@ -50,12 +50,17 @@ def block_m(gqa: int) -> int:
     return max(1, ROWS // gqa)
 
 
-def build_tiles(prefill, req_of, gqa: int, device) -> torch.Tensor:
+def any_block_m(gqa: int) -> int:
+    """Query tokens per tile of the fp32 kernel (at most 16 (token, head) columns)."""
+    return 1 if gqa >= 16 else 16 // gqa
+
+
+def build_tiles(prefill, req_of, gqa: int, device, tokens: int | None = None) -> torch.Tensor:
     """Tile table ``[n, 5]`` int32: (q_row0, n_tokens, q_pos0, ctx, request).
 
     ``prefill`` holds (q_start, q_end, ctx, _) per prefill request, ``req_of``
-    the matching block-table row."""
-    bm = block_m(gqa)
+    the matching block-table row; ``tokens`` per tile, by default ``block_m(gqa)``."""
+    bm = tokens or block_m(gqa)
     rows = []
     for (qs, qe, ctx, *_), r in zip(prefill, req_of):
         nq = qe - qs
@@ -154,45 +159,8 @@ def _out_view(output: torch.Tensor, hq: int) -> torch.Tensor:
 
 
 def kernels_take(head_size: int, gqa: int) -> bool:
-    """Whether the prefill kernels serve this layout (else ``prefill_attention_rows``)."""
+    """Whether the MFMA prefill kernels serve this layout (else the fp32 kernel)."""
     return head_size in (64, 128) and gqa <= ROWS
-
-
-def build_rows(prefill, req_of, device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(query row, block-table row, context length) int64 ``[T]`` each: query ``i`` of an
-    ``nq``-token chunk over ``ctx`` keys sees the first ``ctx - nq + i + 1``."""
-    rows = torch.empty(3, sum(qe - qs for qs, qe, *_ in prefill), dtype=torch.int64)
-    at = 0
-    for (qs, qe, ctx, *_), r in zip(prefill, req_of):
-        nq = qe - qs
-        rows[0, at:at + nq] = torch.arange(qs, qe)
-        rows[1, at:at + nq] = r
-        rows[2, at:at + nq] = torch.arange(ctx - nq + 1, ctx + 1)
-        at += nq
-    rows = to_device(rows, device)
-    return rows[0], rows[1], rows[2]
-
-
-def prefill_attention_rows(store, query: torch.Tensor, output: torch.Tensor, prefill, req_of,
-                           block_table: torch.Tensor, softmax_scale: float) -> None:
-    """Prefill for layouts the prefill kernels do not take: every query token is a
-    decode row (``echokv_decode``, split schedule) over its causal context -- the
-    attention of the reference's gather + bottom-right causal SDPA
-    (echokv_vllm/kernels/prefill.py:210-236). Rows go in slices whose split
-    workspace stays under ``ROWS_WORKSPACE_BYTES``."""
-    from echokv_amd.kernels import decode as dec
-
-    if not prefill:
-        return
-    q_rows, bt_rows, lens = build_rows(prefill, req_of, query.device)
-    hq, d = query.shape[1], query.shape[2]
-    out = _out_view(output, hq)
-    max_ctx = max(ctx for _, _, ctx, *_ in prefill)
-    splits = dec.default_splits(block_table, store.layout.block_size, dec.BLOCKS_PER_SPLIT, max_ctx)
-    step = max(1, ROWS_WORKSPACE_BYTES // (hq * splits * (d + 2) * 4))
-    for i in range(0, q_rows.shape[0], step):
-        dec.decode_attention(store, query, block_table, lens[i:i + step], softmax_scale, q_rows=q_rows[i:i + step],
-                             bt_rows=bt_rows[i:i + step], out=out, num_splits=splits, batch_invariant=True)
 
 
 def use_dense(prefill, head_size: int) -> bool:
@@ -263,7 +231,7 @@ def prefill_attention(store, query: torch.Tensor, output: torch.Tensor, prefill,
     if not kernels_take(store.layout.head_size, query.shape[1] // store.layout.num_kv_heads):
         if own_group_key is not None:
             raise ValueError("own-group-exact prefill needs head size 64 or 128 and at most 128 query heads per KV head")
-        prefill_attention_rows(store, query, output, prefill, req_of, block_table, softmax_scale)
+        prefill_attention_fused(store, query, output, prefill, req_of, block_table, softmax_scale)
         return
     part, lse = output, None
     if own_group_key is not None:
@@ -328,15 +296,17 @@ def prefill_attention_fused(store, query: torch.Tensor, output: torch.Tensor, pr
                             block_table: torch.Tensor, softmax_scale: float, tiles: torch.Tensor | None = None,
                             lse: torch.Tensor | None = None) -> None:
     """The fused kernel (echokv_vllm/kernels/prefill.py:242-327) over ``tiles``; ``lse`` as
-    for ``prefill_attention_dense``."""
+    for ``prefill_attention_dense``. Layouts the MFMA kernel is not built for take the
+    fp32 kernel (tiles of ``any_block_m(gqa)`` tokens)."""
     if not prefill:
         return
     L = store.layout
     _lib.require_device(query, output, block_table, store.pages)
     hq = query.shape[1]
     gqa = hq // L.num_kv_heads
+    tile_m = block_m(gqa) if kernels_take(L.head_size, gqa) else any_block_m(gqa)
     if tiles is None:
-        tiles = build_tiles(prefill, req_of, gqa, query.device)
+        tiles = build_tiles(prefill, req_of, gqa, query.device, tokens=tile_m)
     if tiles.numel() == 0:
         return
     if query.stride(2) != 1:
@@ -349,6 +319,6 @@ def prefill_attention_fused(store, query: torch.Tensor, output: torch.Tensor, pr
         "echokv_prefill", _lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(store.block_res),
         _lib.ptr(store.res_group), _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1),
         _lib.dtype_code(query), hq, _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out),
-        _lib.ptr(tiles), tiles.shape[0], block_m(gqa), _lib.ptr(block_table), block_table.stride(0),
+        _lib.ptr(tiles), tiles.shape[0], tile_m, _lib.ptr(block_table), block_table.stride(0),
         float(softmax_scale), int(lse is not None), _lib.ptr(lse), _lib.stream(),
     )

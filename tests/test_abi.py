@@ -95,6 +95,24 @@ def _prefill_dense(lib, L, hq=32, tile_m=64, n_packs=4, n_q=2, ws_bytes=None, ow
                                     n_packs, p, n_q, tile_m, p, 64, p, ws_bytes, 0.088, own_group, None, None)
 
 
+def _prefill(lib, L, hq=32, tile_m=32, n_tiles=0, own_group=0):
+    res = _lib.Residual(C.c_void_p(16), 1, 2, 16 * 8 * 128, 8 * 128, 128)
+    p = C.c_void_p(64)  # never dereferenced: every call below fails its checks first or launches nothing
+    return lib.echokv_prefill(C.byref(L), p, p, p, C.byref(res), p, 4096, 128, 1, hq, p, 4096, 128, 1, p, n_tiles,
+                              tile_m, p, 64, 0.088, own_group, None, None)
+
+
+def test_prefill_tile_sizes_by_kernel(lib):
+    """MFMA tiles hold 128 / GQA tokens; other layouts (fp32 kernel) 16 / GQA, no own group."""
+    assert _prefill(lib, _layout_of(), tile_m=32) == 0                    # D 128, GQA 4: 128 / 4
+    assert _prefill(lib, _layout_of(), tile_m=4) == 2
+    assert _prefill(lib, _layout_of(head_size=96), tile_m=4) == 0         # fp32 kernel: 16 / 4
+    assert _prefill(lib, _layout_of(head_size=96), tile_m=32) == 2
+    assert _prefill(lib, _layout_of(head_size=96), tile_m=4, own_group=1) == 2
+    assert _prefill(lib, _layout_of(head_size=256), hq=8 * 20, tile_m=1) == 0  # GQA 20: one token per tile
+    assert _prefill(lib, _layout_of(head_size=512), tile_m=4) == 2
+
+
 def _own_group(lib, L, hq=32, n=2):
     res = _lib.Residual(C.c_void_p(16), 1, 2, 16 * 8 * 128, 8 * 128, 128)
     p = C.c_void_p(64)  # never dereferenced: every call below fails its checks first
