@@ -275,10 +275,14 @@ __global__ __launch_bounds__(kAnyThreads) void prefill_any_kernel(PrefillArgs a)
   const int h = (int)(blockIdx.x % L.H);
   const int32_t* td = a.tiles + (long)(blockIdx.x / L.H) * 5;
   const long q_row0 = td[0];
-  const int n_tok = td[1], q_pos0 = td[2], ctx = td[3];
+  const int q_pos0 = td[2], ctx = td[3];
   const long bt_row = td[4];
   const int gs = a.gs;
-  const int n_cols = n_tok * gs;  // <= 16 (the host sizes tiles so)
+  // The host sizes tiles to at most 16 columns; a larger tile is cut to its first
+  // 16 / gs tokens rather than overrun the LDS rows.
+  const int max_tok = kAnyCols / gs > 0 ? kAnyCols / gs : 1;
+  const int n_tok = td[1] < max_tok ? td[1] : max_tok;
+  const int n_cols = n_tok * gs;
   const long kv_end = q_pos0 + n_tok < ctx ? q_pos0 + n_tok : ctx;
 
   __shared__ __align__(16) float qs[kAnyCols * kMaxAnyD];
