@@ -437,6 +437,8 @@ class EchoKVAttentionImpl(AttentionImpl):
         self.num_kv_heads = num_kv_heads or num_heads
         self.kv_cache_dtype = kv_cache_dtype
         self.cfg = cfg = load_config()
+        if cfg.own_group_exact and not pf.kernels_take(head_size, self.num_heads // self.num_kv_heads):
+            raise NotImplementedError("ECHOKV_OWN_GROUP_EXACT needs head size 64 or 128 and GQA <= 128")
         self.controller = LayerController(cfg.controller)
         # Allocated at model construction so vLLM's memory profiler counts them: the
         # full-precision K of each block's open group (+1 spare row), the K_ref ring and

@@ -189,6 +189,14 @@ def test_impl_refuses_unsupported_features(kw, what):
         EchoKVAttentionImpl(32, 128, 0.088, 8, **kw)
 
 
+def test_own_group_exact_needs_the_mfma_prefill_layouts(monkeypatch):
+    monkeypatch.setenv("ECHOKV_OWN_GROUP_EXACT", "1")
+    monkeypatch.setenv("ECHOKV_K_GROUP", "16")
+    EchoKVAttentionImpl(32, 128, 0.088, 8)
+    with pytest.raises(NotImplementedError, match="OWN_GROUP_EXACT"):
+        EchoKVAttentionImpl(32, 96, 0.088, 8)
+
+
 def test_impl_buffers_follow_the_config(monkeypatch):
     monkeypatch.setenv("ECHOKV_K_GROUP", "16")
     monkeypatch.setenv("ECHOKV_RESIDUAL_SLOTS", "20")
