@@ -81,7 +81,7 @@ def build_state(dev, steps_total: int, seed: int = 1):
     ctx = rng.integers(512, 8193, S).astype(np.int64)
     tiers = rng.permutation(np.array([8] * 8 + [4] * 16 + [2] * 8))
     layout = TieredLayout(H, D, BS, MEM, KG, VG)
-    page = BS * TieredLayout.per_token_bytes(H, D, MEM, KG, VG)
+    page = layout.aligned_stride  # pages on 128-byte lines (see TieredLayout.alloc_pages)
     nbs = -(-(ctx + steps_total + 1) // BS)
     nb = int(nbs.sum()) + 16
     perm = rng.permutation(nb)
@@ -93,7 +93,7 @@ def build_state(dev, steps_total: int, seed: int = 1):
     shared = SharedState(nb, BS, KG, S + 16, kref_window=64, device=dev)
     stores, krefs = [], []
     for _ in range(LAYERS):
-        pages = torch.empty(nb, page, dtype=torch.uint8, device=dev)
+        pages = layout.alloc_pages(nb, dev)
         res = torch.zeros(S + 17, KG, H, D, dtype=torch.float16, device=dev)
         stores.append(TieredKVCache(layout, pages, residual=res, shared=shared))
         krefs.append(torch.zeros(64, H, D, device=dev))
@@ -342,12 +342,12 @@ def _prefill_pass(reps: int) -> dict:
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(3)
     layout = TieredLayout(H, D, BS, MEM, KG, VG)
-    page = BS * TieredLayout.per_token_bytes(H, D, MEM, KG, VG)
+    page = layout.aligned_stride  # pages on 128-byte lines (see TieredLayout.alloc_pages)
     nbs = PF_CTX // BS
     nb = PF_SEQS * nbs + 16
     table = rng.permutation(nb)[: PF_SEQS * nbs].reshape(PF_SEQS, nbs).astype(np.int64)
     shared = SharedState(nb, BS, KG, PF_SEQS + 16, kref_window=64, device=dev)
-    pages = torch.zeros(nb, page, dtype=torch.uint8, device=dev)
+    pages = layout.alloc_pages(nb, dev, zero=True)
     res = torch.zeros(PF_SEQS + 17, KG, H, D, dtype=torch.bfloat16, device=dev)
     store = TieredKVCache(layout, pages, residual=res, shared=shared)
     kref = torch.zeros(64, H, D, device=dev)
@@ -442,7 +442,7 @@ def run_cfg4(reps: int = 5) -> dict:
     rng = np.random.default_rng(3)
     tiers = rng.permutation(np.array([8] * 20 + [4] * 40 + [2] * 20))
     layout = TieredLayout(H, D, BS, MEM, KG, VG)
-    page = BS * TieredLayout.per_token_bytes(H, D, MEM, KG, VG)
+    page = layout.aligned_stride  # pages on 128-byte lines (see TieredLayout.alloc_pages)
     ctx = np.full(C4_S, C4_CTX, np.int64)
     nbs = -(-ctx // BS)
     nb = int(nbs.sum()) + 16
@@ -458,7 +458,7 @@ def run_cfg4(reps: int = 5) -> dict:
     print(f"[bench cfg4] planned {pre.size} slots, {time.time() - t_setup:.1f}s", file=sys.stderr, flush=True)
     stores, krefs = [], []
     for _ in range(C4_LAYERS):
-        pages = torch.empty(nb, page, dtype=torch.uint8, device=dev)
+        pages = layout.alloc_pages(nb, dev)
         res = torch.zeros(C4_S + 17, KG, H, D, dtype=torch.float16, device=dev)
         stores.append(TieredKVCache(layout, pages, residual=res, shared=shared))
         krefs.append(torch.zeros(64, H, D, device=dev))

