@@ -1017,6 +1017,10 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   const bool live = h < L.H;  // a wave past the last head still loads its share of every tile
 
   W w;
+  // The first chunk's block table row is requested with the query, so their
+  // round trips overlap; its page headers follow before the query is converted.
+  const int nb_first = b_end - b_start < 64 ? b_end - b_start : 64;
+  BlockLane bl;
   {
     const bool qv = live && n < a.gs;
     const long qb = q_row * a.q_s0 + (long)(h * a.gqa + a.g0 + (qv ? n : 0)) * a.q_s1 + c * W::CPL;
@@ -1033,6 +1037,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
 #pragma unroll
       for (int e = 0; e < W::CPL; ++e) xq[e] = 0.f;
     }
+    bl = load_block<BITS>(a, lane < nb_first ? (long)a.bt[bt_row * a.bt_s0 + b_start + lane] : -1L);
 #pragma unroll
     for (int i = 0; i < W::CPL / 2; ++i) {
       const float x0 = q_sign * xq[2 * i], x1 = q_sign * xq[2 * i + 1];
@@ -1055,7 +1060,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   const bool stats_ok = (D >> a.vg_shift) == 2 || (D >> a.vg_shift) == 4;
   for (int c0 = b_start; c0 < b_end; c0 += 64) {
     const int nb = b_end - c0 < 64 ? b_end - c0 : 64;
-    const BlockLane bl = load_block<BITS>(a, lane < nb ? (long)a.bt[bt_row * a.bt_s0 + c0 + lane] : -1L);
+    if (c0 != b_start) bl = load_block<BITS>(a, lane < nb ? (long)a.bt[bt_row * a.bt_s0 + c0 + lane] : -1L);
     const int last_tok = (c0 + nb) * L.BS < seq_len ? (c0 + nb) * L.BS : seq_len;
     const int n_tiles = (last_tok - c0 * L.BS + 15) >> 4;
 
