@@ -122,10 +122,10 @@ def build_state(dev, steps_total: int, seed: int = 1):
 def run(args) -> dict:
     import torch
 
-    from echokv_amd._util import to_device
     from echokv_amd.kernels.decode import decode_attention
+    from echokv_amd.step import StepDriver
     from echokv_amd.tiered_cache import HeaderWriter
-    from echokv_amd.write_plan import stage_plan
+    from echokv_amd.write_plan import WriteMeta
 
     dev = torch.device("cuda:0")
     t_setup = time.time()
@@ -148,36 +148,30 @@ def run(args) -> dict:
     scale = D ** -0.5
     inv = args.schedule == "split"
     headers = HeaderWriter(stores)
+    # The product's per-step host path: one native call plans the step for all 32
+    # layers (write plan, opened blocks and headers per layer) into one image, one
+    # copy uploads it, and the device effects are launched (StepDriver, as the
+    # vLLM backend's builder runs it).
+    driver = StepDriver(shared, stores, cap=S, canary_slots=8, device=dev)
+    tiers32 = tiers.astype(np.int32)
+    qsl = np.arange(S + 1, dtype=np.int32)
 
-    def stage(plan, opened):
-        """The step's plan and every layer's new page headers in one upload; the
-        headers in one launch (the same blocks open in every layer)."""
-        batch = all(o is not None and np.array_equal(o[0], opened[0][0]) for o in opened)
-        meta, extra = stage_plan(plan, dev, (opened[0][0], np.concatenate([o[1] for o in opened])) if batch else None)
-        shared.apply_res_map(*extra[:4])
-        if batch:
-            headers.check(opened[0][0])
-            headers.write(extra[4], extra[5])
-        else:
-            for li, s in enumerate(stores):
-                if opened[li] is not None:
-                    s.write_headers(to_device(torch.from_numpy(opened[li][0]), dev),
-                                    to_device(torch.from_numpy(opened[li][1]), dev))
-        return meta
+    def host_step(i):
+        pos = ctx - 1 + i  # position of this step's new token
+        slots = (table[np.arange(S), pos // BS] * BS + pos % BS).astype(np.int64)
+        up = driver.run(qsl, (pos + 1).astype(np.int32), slots, tiers32, False)
+        driver.apply(up, headers)
+        return up, pos + 1
 
     def step(i):
-        pos = ctx - 1 + i  # position of this step's new token
-        slots = table[np.arange(S), pos // BS] * BS + pos % BS
-        plan = shared.planner.plan(slots)
-        opened = [s.prepare(plan, int(t)) for s, t in zip(stores, tiers)]
-        shared.commit(plan)
-        lens = pos + 1
-        meta = stage(plan, opened)
-        lens_d = to_device(torch.from_numpy(lens), dev)  # pinned, non-blocking: the host keeps planning
+        up, lens = host_step(i)
+        meta = WriteMeta(tok=up.tok, fin=up.fin, fin_count=up.fin_count, n_rows=up.n_tokens, n_fin=up.n_fin)
+        rows, reqs, lens_d = up.decode
         for li, s in enumerate(stores):
             s.apply(meta, kn[li], vn[li], krefs[li])
-            decode_attention(s, q[li], table_d, lens_d, scale, blocks_per_split=args.bps, out=out[li],
-                             num_splits=num_splits, workspace=ws, tier=int(tiers[li]), batch_invariant=inv)
+            decode_attention(s, q[li], table_d, lens_d, scale, blocks_per_split=args.bps, q_rows=rows, bt_rows=reqs,
+                             out=out[li], num_splits=num_splits, workspace=ws, tier=int(tiers[li]),
+                             batch_invariant=inv)
         return lens
 
     # End to end, eager: the host plans every step; all 32 layers write and attend.
@@ -191,23 +185,22 @@ def run(args) -> dict:
     wall_eager = time.perf_counter() - t0
 
     # End to end, graph-replayed (as a serving engine runs decode): the host plans
-    # each step and copies the plan into fixed device buffers (rows = the batch,
-    # finalize over a full grid masked by the device count); one HIP graph then
-    # runs every layer's finalize, write, decode and merge.
-    from echokv_amd.write_plan import WriteMeta
-    tok_buf = torch.full((4, S), -1, dtype=torch.int64, device=dev)
-    fin_buf = torch.zeros(S, 3 + KG, dtype=torch.int64, device=dev)
-    cnt_buf = torch.zeros(1, dtype=torch.int64, device=dev)
-    lens_buf = torch.zeros(S, dtype=torch.int64, device=dev)
-    gmeta = WriteMeta(tok=tok_buf, fin=fin_buf, fin_count=cnt_buf, n_rows=S, n_fin=S)
+    # each step into the driver's fixed device buffers (rows = the batch, finalize
+    # over a full grid masked by the device count); one HIP graph then runs every
+    # layer's finalize, write, decode and merge.
+    g0 = args.warmup + args.steps
+    up, lens = host_step(g0)
+    gmeta = WriteMeta(tok=up.tok, fin=up.fin, fin_count=up.fin_count, n_rows=S, n_fin=up.fin.shape[0])
+    g_rows, g_reqs, g_lens = up.decode
 
     def all_layers():
         for li, s in enumerate(stores):
             s.apply(gmeta, kn[li], vn[li], krefs[li], capturing=True)
-            decode_attention(s, q[li], table_d, lens_buf, scale, blocks_per_split=args.bps, out=out[li],
-                             num_splits=num_splits, workspace=ws, tier=int(tiers[li]), batch_invariant=inv)
+            decode_attention(s, q[li], table_d, g_lens, scale, blocks_per_split=args.bps, q_rows=g_rows,
+                             bt_rows=g_reqs, out=out[li], num_splits=num_splits, workspace=ws, tier=int(tiers[li]),
+                             batch_invariant=inv)
 
-    all_layers()  # warm-up with nothing staged: no row written, every length 0
+    all_layers()  # step g0, eagerly (its plan is staged)
     torch.cuda.synchronize()
     step_graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(step_graph):
@@ -217,23 +210,13 @@ def run(args) -> dict:
 
     def gstep(i):
         t_host = time.perf_counter()
-        pos = ctx - 1 + i
-        slots = table[np.arange(S), pos // BS] * BS + pos % BS
-        plan = shared.planner.plan(slots)
-        opened = [s.prepare(plan, int(t)) for s, t in zip(stores, tiers)]
-        shared.commit(plan)
-        meta = stage(plan, opened)
-        tok_buf.copy_(meta.tok)
-        if meta.n_fin:
-            fin_buf[: meta.n_fin].copy_(meta.fin)
-        cnt_buf.copy_(meta.fin_count)
-        lens_buf.copy_(to_device(torch.from_numpy(pos + 1), dev))
+        up, lens = host_step(i)
+        assert up.tok.data_ptr() == gmeta.tok.data_ptr() and up.decode[2].data_ptr() == g_lens.data_ptr()
         host_s[0] += time.perf_counter() - t_host
         step_graph.replay()
-        return pos + 1
+        return lens
 
-    g0 = args.warmup + args.steps
-    for i in range(g0, g0 + 2):
+    for i in range(g0 + 1, g0 + 2):
         gstep(i)
     torch.cuda.synchronize()
     host_s[0] = 0.0
@@ -248,29 +231,31 @@ def run(args) -> dict:
     # graph so the events time GPU work only (no host launch gaps).
     lens_d = torch.from_numpy(lens).to(dev)
 
-    def int4_decode():
-        for li in int4:
-            decode_attention(stores[li], q[li], table_d, lens_d, scale, blocks_per_split=args.bps, out=out[li],
-                             num_splits=num_splits, workspace=ws, tier=4, batch_invariant=inv)
+    def time_int4(invariant: bool) -> float:
+        """ms per INT4 layer-step (decode + merge), graph-replayed over the 16 INT4 layers."""
+        def int4_decode():
+            for li in int4:
+                decode_attention(stores[li], q[li], table_d, lens_d, scale, blocks_per_split=args.bps, out=out[li],
+                                 num_splits=num_splits, workspace=ws, tier=4, batch_invariant=invariant)
 
-    int4_decode()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
         int4_decode()
-    for _ in range(3):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = args.reps
-    e0.record()
-    for _ in range(reps):
-        graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    int4_ms = e0.elapsed_time(e1)
-    n_launch = len(int4) * reps
-    avg_ms = int4_ms / n_launch
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            int4_decode()
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (len(int4) * args.reps)
+
+    avg_ms = time_int4(inv)
+    other_ms = time_int4(not inv)
     per_layer_bytes = alg_bytes(lens, 4)
     achieved = per_layer_bytes / (avg_ms * 1e-3) / 1e9
     res = {
@@ -298,6 +283,10 @@ def run(args) -> dict:
         "attn_write_step_eager_ms": round(wall_eager * 1e3 / args.steps, 3),
         "attn_write_step_eager_tok_s": round(S * args.steps / wall_eager, 1),
         "int4_decode_us_per_layer": round(avg_ms * 1e3, 2),
+        "schedule": args.schedule,
+        "other_schedule": {"schedule": "split" if not inv else "balanced",
+                           "int4_decode_us_per_layer": round(other_ms * 1e3, 2),
+                           "GBs": round(alg_bytes(lens, 4) / (other_ms * 1e-3) / 1e9, 1)},
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),

@@ -19,7 +19,8 @@ FILL, LAST, CUM = range(3)
 EXPORTS = (
     "ekh_planner_new", "ekh_planner_free", "ekh_plan", "ekh_commit", "ekh_planner_state", "ekh_residual_free_list",
     "ekh_sealed_mask", "ekh_block_array", "ekh_pool_new", "ekh_pool_free", "ekh_pool_open", "ekh_pool_seal_row",
-    "ekh_pool_counters", "ekh_pool_reset_counters", "ekh_pool_tags", "ekh_pool_free_list",
+    "ekh_pool_counters", "ekh_pool_reset_counters", "ekh_pool_tags", "ekh_pool_free_list", "ekh_pool_live",
+    "ekh_stepper_new", "ekh_stepper_free", "ekh_stepper_run", "ekh_host_slots",
 )
 
 
@@ -28,6 +29,26 @@ class PlanView(C.Structure):
                                          "n_grp_map", "stage_len")] + [
         ("stage", C.POINTER(C.c_int64)), ("evict", C.POINTER(C.c_int64)), ("open", C.POINTER(C.c_int64)),
         ("touched", C.POINTER(C.c_int64))]
+
+
+class Batch(C.Structure):
+    """``ekh_batch``: one step's batch (pointers to int32 query starts / lengths, int64 slots)."""
+
+    _fields_ = [("num_reqs", C.c_int64), ("num_tokens", C.c_int64), ("query_start", C.c_void_p),
+                ("seq_lens", C.c_void_p), ("slot_mapping", C.c_void_p)]
+
+
+_STEP_WORDS = ("step", "len", "o_canary", "o_dec", "o_tok", "o_fin", "o_res", "o_grp", "o_open", "o_hdr", "o_seal",
+               "rows_dec", "rows_tok", "rows_fin", "n_dec", "n_tokens", "n_fin", "n_res", "n_grp", "n_open",
+               "n_seal", "n_canary", "decode_only", "graph_rows")
+
+
+class StepView(C.Structure):
+    """``ekh_step_view``: where each part of a step image sits."""
+
+    _fields_ = [(n, C.c_int64) for n in _STEP_WORDS] + [
+        ("canary_ctx", C.c_double), ("n_prefill", C.c_int64), ("prefill", C.POINTER(C.c_int64)),
+        ("n_victims", C.c_int64), ("victims", C.POINTER(C.c_int64)), ("image", C.POINTER(C.c_int64))]
 
 
 P, I32, I64, PI64, PU8 = C.c_void_p, C.c_int32, C.c_int64, C.POINTER(C.c_int64), C.POINTER(C.c_uint8)
@@ -48,6 +69,11 @@ _SIGS = {
     "ekh_pool_reset_counters": ([P], None),
     "ekh_pool_tags": ([P], PI64),
     "ekh_pool_free_list": ([P, PI64, I64], I64),
+    "ekh_pool_live": ([P, PI64], None),
+    "ekh_stepper_new": ([P, C.POINTER(P), I32, I64, I32], P),
+    "ekh_stepper_free": ([P], None),
+    "ekh_stepper_run": ([P, C.POINTER(Batch), P, I32, P, I64, C.POINTER(StepView)], C.c_int),
+    "ekh_host_slots": ([C.POINTER(Batch), P, I64, I64, I64, P, I64, I32, P], C.c_int),
 }
 
 _lib = None

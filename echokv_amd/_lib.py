@@ -19,14 +19,14 @@ LIB_PATH = Path(__file__).resolve().parent / "libechokv.so"
 
 F32, F16, BF16 = 0, 1, 2
 DECODE_BATCH_INVARIANT = 1
-_DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 EXPORTS = (
     "echokv_error_string", "echokv_write_tokens", "echokv_finalize_k", "echokv_write_step", "echokv_seal_groups",
     "echokv_gather", "echokv_write_headers",
     "echokv_store_blocks", "echokv_decode", "echokv_decode_static", "echokv_prefill", "echokv_prefill_dense",
     "echokv_prefill_dense_workspace", "echokv_prefill_own_group",
-    "echokv_dequant_dense", "echokv_canary_kl",
+    "echokv_dequant_dense", "echokv_canary_kl", "echokv_decode_workspace_rows",
 )
 
 
@@ -93,6 +93,8 @@ def lib() -> C.CDLL:
             fn.restype = C.c_int
         l.echokv_prefill_dense_workspace.argtypes = [LP, I64]
         l.echokv_prefill_dense_workspace.restype = C.c_int64
+        l.echokv_decode_workspace_rows.argtypes = [LP, I32, I32, I64, I32, I32]
+        l.echokv_decode_workspace_rows.restype = C.c_int64
         _lib = l
     return _lib
 
@@ -106,7 +108,7 @@ def call(name: str, *args) -> None:
 
 def dtype_code(t: torch.Tensor) -> int:
     try:
-        return _DTYPES[t.dtype]
+        return DTYPES[t.dtype]
     except KeyError:
         raise RuntimeError(f"unsupported dtype {t.dtype}") from None
 

@@ -2,30 +2,33 @@
 
 Interface of ``echokv_vllm/backend.py:72-636``: ``EchoKVAttentionBackend``
 (``customize_spec``, block / head-size support, ``get_name() == "CUSTOM"``),
-``EchoKVMetadataBuilder`` (``build`` once per step for all layers) and
+``EchoKVMetadataBuilder`` (``build`` once per step for every layer) and
 ``EchoKVAttentionImpl`` (``bind``, ``do_kv_cache_update``, ``forward``). vLLM
-budgets the page as one opaque byte state per token (``customize_spec``), so
-its cache manager, memory profiler and block tables see exactly the bytes the
-tiered store uses.
+budgets the page as one opaque byte state per token (``customize_spec``), so its
+cache manager, memory profiler and block tables see exactly the bytes the tiered
+store uses.
 
-Per step the builder, on the host and once for every layer:
+How a step runs here:
 
-* plans the writes (native planner), seals evicted groups and opens blocks at
-  each layer's current tier, and uploads the step's metadata with one
-  non-blocking copy into a device image whose graph-visible parts sit at fixed
-  offsets, so a captured decode graph reads each step's values;
-* lays out the batch: one decode entry per single-token request (graph padding
-  included, length 0), the prefill chunks with their work lists and one shared
-  workspace;
-* runs the canary for every layer at once on the step after a fire (δ̂ for every
-  tier), and lets each layer's controller consume the previous fire's result, so
-  reading it never waits for the stream.
+* ``build`` makes every host decision of the step for all layers in one native
+  call (``StepDriver``, ``echokv_amd/step.py``): the batch layout, the write plan,
+  the blocks that open in each layer at that layer's tier, and the canary rows.
+  One host-to-device copy then carries the step's metadata; the few device
+  effects that must precede the layers' writes (residual-map and page-header
+  updates, and the rare seals and demotions) are launched right away.
+* The canary has its own clock (``CanaryClock``): a fire step stashes query rows,
+  the next build scores every layer at once and hands each controller the
+  previous fire's δ̂, which the GPU finished long ago, so reading it never waits.
+* ``do_kv_cache_update`` and ``forward`` only launch HIP kernels on device
+  metadata (``WriteMeta``, ``DecodeWork``, ``PrefillWork``), so a decode-only step
+  replays as one HIP graph.
 
-``do_kv_cache_update`` and ``forward`` then only launch HIP kernels on device
-metadata: the quantize-on-write of the step's K/V, chunked-prefill and decode
-attention over the tiered pages (each block read at its own tier), and the copy
-of the canary's query rows. There is no other path: without the HIP library the
-calls raise.
+The torch-profiler scopes are the reference's (``echokv.build``,
+``echokv.canary``, ``echokv.write``, ``echokv.prefill_attn``,
+``echokv.decode_attn``; inside ``echokv.write`` the store's ``echokv.write.k_finalize``
+and ``echokv.write.tokens``), so the reference's
+profiling harness reads the same report. There is no other path: without the HIP
+library every call raises.
 """
 
 from __future__ import annotations
@@ -36,9 +39,9 @@ from typing import ClassVar
 
 import numpy as np
 import torch
+from torch.profiler import record_function
 
 from echokv_amd import _vllm
-from echokv_amd._util import to_device
 from echokv_amd._vllm import (
     AttentionBackend,
     AttentionCGSupport,
@@ -48,16 +51,17 @@ from echokv_amd._vllm import (
     MultipleOf,
 )
 from echokv_amd.canary import canary_kl, ring_view
-from echokv_amd.config import load_config
+from echokv_amd.config import load_config, v_group_supported
 from echokv_amd.controller import SUPPORTED_BITS, LayerController
 from echokv_amd.host_slots import host_lens_and_slots, is_dummy_step
 from echokv_amd.kernels import decode as dec
 from echokv_amd.kernels import prefill as pf
+from echokv_amd.step import StepDriver
 from echokv_amd.tiered_cache import HeaderWriter, TieredKVCache, TieredLayout
 from echokv_amd.write_plan import SharedState, WriteMeta
 
 # Head sizes the MFMA kernels are built for; others up to MAX_HEAD_SIZE take the
-# fp32 decode kernel (prefill through decode rows).
+# fp32 kernels.
 KERNEL_HEAD_SIZES = (64, 128)
 MAX_HEAD_SIZE = 256
 # Upper bound on decode splits per sequence (a fixed grid, so a graph replays it).
@@ -90,7 +94,10 @@ class EchoKVAttentionBackend(AttentionBackend):
 
     @classmethod
     def supports_head_size(cls, head_size: int) -> bool:
-        return head_size % 4 == 0 and head_size % load_config().v_group == 0 and head_size <= MAX_HEAD_SIZE
+        """The reference's rule (a multiple of 4 and of the V group) up to 256
+        channels, for V groups the kernels store (``v_group_supported``)."""
+        vg = load_config().v_group
+        return head_size % 4 == 0 and head_size <= MAX_HEAD_SIZE and v_group_supported(vg, head_size)
 
     @classmethod
     def supports_attn_type(cls, attn_type: str) -> bool:
@@ -114,6 +121,45 @@ def block_multiple() -> int:
     return max(16, load_config().k_group)
 
 
+# ---- per-step device work --------------------------------------------------------
+
+@dataclass
+class DecodeWork:
+    """One decode entry per single-token request (graph padding: length 0)."""
+
+    rows: torch.Tensor  # query rows
+    reqs: torch.Tensor  # block-table rows
+    lens: torch.Tensor  # cache lengths, the new token included
+    num_splits: int  # split grid (fixed, so a graph replays it)
+    workspace: tuple | None  # (acc, ml) shared by every layer; None: the call allocates
+    batch_invariant: bool
+
+    def run(self, impl, query: torch.Tensor, block_table: torch.Tensor, out: torch.Tensor) -> None:
+        dec.decode_attention(impl.store, query, block_table, self.lens, impl.scale, q_rows=self.rows,
+                             bt_rows=self.reqs, out=out, num_splits=self.num_splits, workspace=self.workspace,
+                             tier=impl.decode_tier(), batch_invariant=self.batch_invariant)
+
+
+@dataclass
+class PrefillWork:
+    """The step's prefill chunks and the device tables of the path that runs them."""
+
+    entries: list  # (q_start, q_end, context, 0) per chunk
+    reqs: list  # block-table row of each chunk
+    tiles: torch.Tensor | None = None  # fused path (every chunk <= 64 tokens)
+    dense: tuple | None = None  # (DensePlan, workspace) of the two-pass path
+    own_group_rows: torch.Tensor | None = None  # own-group-exact prefill (ECHOKV_OWN_GROUP_EXACT=1)
+
+    def run(self, impl, query: torch.Tensor, key: torch.Tensor, block_table: torch.Tensor,
+            out: torch.Tensor) -> None:
+        og_key = None
+        if self.own_group_rows is not None:  # each query's own K group from this step's key rows
+            og_key = key.view(key.shape[0], impl.num_kv_heads, impl.head_size)
+        pf.prefill_attention(impl.store, query, out, self.entries, self.reqs, block_table, impl.scale,
+                             tiles=self.tiles, dense=self.dense, own_group_key=og_key,
+                             own_group_rows=self.own_group_rows)
+
+
 @dataclass
 class EchoKVMetadata:
     num_actual_tokens: int
@@ -123,98 +169,71 @@ class EchoKVMetadata:
     block_table: torch.Tensor
     slot_mapping: torch.Tensor
     write: WriteMeta | None  # None: no KV cache bound yet (memory profiling); attention is skipped
-    canary_rows: torch.Tensor | None  # [canary_max_q] query rows the canary reads
-    fire: bool  # this step's query rows feed the canary (scored at the next build)
-    decode_rows: torch.Tensor | None  # [nd] query rows of single-token requests
-    decode_reqs: torch.Tensor | None  # [nd] their block-table rows
-    decode_lens: torch.Tensor | None  # [nd] their cache lengths (0 = graph padding)
-    num_splits: int  # decode split grid (fixed, so graphs can replay it)
-    decode_workspace: tuple | None  # (acc, ml) shared by every layer's decode
-    prefill: list  # (q_start, q_end, ctx, 0) per prefill request
-    prefill_reqs: list  # block-table row of each prefill entry
-    prefill_tiles: torch.Tensor | None  # fused-kernel tiles (every chunk <= 64 tokens)
-    prefill_dense: object | None  # (DensePlan, workspace) of the two-pass path (longer chunks)
-    own_group_rows: torch.Tensor | None = None  # own-group-exact prefill rows (ECHOKV_OWN_GROUP_EXACT=1)
+    decode: DecodeWork | None = None
+    prefill: PrefillWork | None = None
+    canary_rows: torch.Tensor | None = None  # [canary_max_q] query rows the canary reads
+    fire: bool = False  # this step's query rows feed the canary (scored at the next build)
 
 
-class StepImage:
-    """One step's int64 metadata in one device buffer, uploaded with one copy.
+# ---- canary schedule ---------------------------------------------------------------
 
-    Segments at fixed offsets (capacity ``cap`` rows, so a graph captured at any
-    batch size up to ``cap`` reads the current step): ``[fin count | canary rows
-    (nq) | decode q rows, block-table rows, lengths (3 x cap) | tokens (4 x cap) |
-    fin rows (cap x w) | tail]``; the tail (residual map, page headers) is read by
-    the builder's own index writes, never by a graph. A larger step uses a fresh
-    buffer of its own size. Host images are pinned and reused round-robin once the
-    copy that read them has completed.
+class CanaryClock:
+    """When the canary fires and when its result reaches the controllers.
+
+    Every ``interval``-th real step arms the clock; the next step with a live
+    request fires: its newest query rows are stashed by ``forward``. The build
+    after a fire scores every layer from the stash (``echokv.canary``) and feeds
+    the controllers the fire before it, so reading δ̂ back never waits for the
+    GPU (the reference's schedule, ``echokv_vllm/backend.py:314-333,395-408``).
     """
 
-    RING = 4
+    def __init__(self, interval: int) -> None:
+        self.interval = interval
+        self.steps = 0
+        self.armed = False
+        self.stashed: tuple | None = None  # (rows, mean context) of the last fire, not yet scored
+        self.scored: tuple | None = None  # (δ̂ [layers, tiers] on the device, mean context), not yet fed
 
-    def __init__(self, cap: int, nq: int, w: int, tail: int, device) -> None:
-        self.cap, self.nq, self.w, self.tail = cap, nq, w, tail
-        self.device = torch.device(device)
-        self.o_can = 2
-        self.o_dec = self.o_can + nq + (nq & 1)
-        self.o_tok = self.o_dec + 3 * cap
-        self.o_fin = self.o_tok + 4 * cap
-        self.o_tail = self.o_fin + cap * w
-        self.size = self.o_tail + tail
-        self.dev = torch.zeros(self.size, dtype=torch.long, device=self.device)
-        pin = self.device.type == "cuda"
-        self.host = [torch.zeros(self.size, dtype=torch.long, pin_memory=pin) for _ in range(self.RING if pin else 1)]
-        self.done: list = [None] * len(self.host)
-        self.turn = 0
+    def tick(self, dummy: bool) -> bool:
+        """Count a step; whether this step should take canary rows."""
+        if not dummy:
+            self.steps += 1
+            if self.steps % self.interval == 0:
+                self.armed = True
+        return self.armed
 
-    def upload(self, n_fin: int, canary: np.ndarray, decode: tuple, tok: np.ndarray, fin: np.ndarray, tail: list):
-        """Views ``(fin_count, canary, (rows, reqs, lens), tok [4, t], fin, tail views)``."""
-        nd, t = decode[0].size, tok.shape[1]
-        tail_len = sum(a.size for a in tail)
-        fits = max(nd, t, n_fin) <= self.cap and tail_len <= self.tail
-        if fits:
-            cap, o_dec, o_tok, o_fin, o_tail = self.cap, self.o_dec, self.o_tok, self.o_fin, self.o_tail
-            fin_rows = cap  # a graph's finalize runs a full grid masked by the count
-            i = self.turn
-            if self.done[i] is not None:
-                self.done[i].synchronize()  # the copy that read this host image four steps ago
-            h = self.host[i].numpy()
-        else:  # a step too large for any graph: a buffer of its own size
-            cap = max(nd, t, n_fin, 1)
-            o_dec = self.o_dec
-            o_tok = o_dec + 3 * cap
-            o_fin = o_tok + 4 * cap
-            o_tail = o_fin + n_fin * self.w
-            fin_rows = n_fin
-            h = np.zeros(o_tail + tail_len, np.int64)
-        h[0] = n_fin
-        h[self.o_can : self.o_can + self.nq] = canary
-        for k in range(3):
-            h[o_dec + k * cap : o_dec + k * cap + nd] = decode[k]
-        for k in range(4):
-            h[o_tok + k * cap : o_tok + k * cap + t] = tok[k]
-        h[o_fin : o_fin + fin.size] = fin.reshape(-1)
-        o = o_tail
-        for a in tail:
-            h[o : o + a.size] = a.reshape(-1)
-            o += a.size
-        if fits:
-            dev = self.dev
-            dev[:o].copy_(self.host[i][:o], non_blocking=True)
-            if self.device.type == "cuda":
-                ev = self.done[i] or torch.cuda.Event()
-                ev.record()
-                self.done[i] = ev
-            self.turn = (self.turn + 1) % len(self.host)
-        else:
-            dev = to_device(torch.from_numpy(h), self.device)
-        views, o = [], o_tail
-        for a in tail:
-            views.append(dev[o : o + a.size])
-            o += a.size
-        return (dev[0:1], dev[self.o_can : self.o_can + self.nq],
-                tuple(dev[o_dec + k * cap : o_dec + k * cap + nd] for k in range(3)),
-                dev[o_tok : o_tok + 4 * cap].view(4, cap)[:, :t],
-                dev[o_fin : o_fin + fin_rows * self.w].view(fin_rows, self.w), views)
+    def fired(self, rows: int, ctx: float) -> None:
+        if rows:
+            self.armed = False
+            self.stashed = (rows, ctx)
+
+    def reset(self) -> None:
+        self.stashed = self.scored = None
+
+
+# ---- builder -------------------------------------------------------------------------
+
+class _Group:
+    """A cache group's layers once bound to their KV caches: stores, shared state,
+    the step driver, header writer and shared canary workspace."""
+
+    def __init__(self, builder, layers: list, caches: list) -> None:
+        cfg = builder.cfg
+        self.impls = [layer.impl for layer in layers]
+        self.shared = SharedState(caches[0].shape[0], builder.kv_cache_spec.block_size, cfg.k_group,
+                                  builder.residual_slots, cfg.kref_window, builder.device)
+        for impl, cache in zip(self.impls, caches):
+            impl.bind(cache, self.shared)
+        self.stores = [impl.store for impl in self.impls]
+        self.driver = StepDriver(self.shared, self.stores, builder.cap, cfg.canary_max_q, builder.device)
+        self.headers = HeaderWriter(self.stores)
+        impl0 = self.impls[0]
+        self.canary_ws = torch.empty(len(self.impls) * impl0.num_kv_heads * len(SUPPORTED_BITS),
+                                     device=impl0.store.device)
+        self.cache_ptr = caches[0].data_ptr()
+
+    def tiers(self) -> np.ndarray:
+        return np.fromiter((impl.controller.bits for impl in self.impls), np.int32, len(self.impls))
 
 
 class EchoKVMetadataBuilder(AttentionMetadataBuilder):
@@ -232,190 +251,139 @@ class EchoKVMetadataBuilder(AttentionMetadataBuilder):
     def __init__(self, kv_cache_spec, layer_names, vllm_config, device) -> None:
         super().__init__(kv_cache_spec, layer_names, vllm_config, device)
         self.cfg = load_config()
-        self.num_heads = _vllm.num_attention_heads(vllm_config, layer_names)
-        self.gqa = self.num_heads // kv_cache_spec.num_kv_heads
+        self.gqa = _vllm.num_attention_heads(vllm_config, layer_names) // kv_cache_spec.num_kv_heads
         # Exact host sequence lengths are not available under async speculative decoding.
         self.host_slots = getattr(vllm_config, "speculative_config", None) is None
         self.check_host_slots = os.environ.get("ECHOKV_CHECK_HOST_SLOTS", "0") == "1"
         self.host_slot_steps = 0
-        bs = kv_cache_spec.block_size
-        max_blocks = -(-vllm_config.model_config.max_model_len // bs)
-        self.num_splits = max(1, min(-(-max_blocks // dec.BLOCKS_PER_SPLIT), MAX_DECODE_SPLITS))
+        self.num_splits = decode_splits(vllm_config.model_config.max_model_len, kv_cache_spec.block_size)
         self.residual_slots = residual_slots(self.cfg, vllm_config)
-        comp = getattr(vllm_config, "compilation_config", None)
-        self.cap = getattr(comp, "max_cudagraph_capture_size", None) or 512
-        self.layers: list | None = None  # set by _attach (vLLM) or bind_layers (standalone)
-        self.impls: list = []
-        self._cache_ptr: int | None = None
-        self.shared: SharedState | None = None
-        self.image: StepImage | None = None
-        self.workspace: tuple | None = None
-        self.step = 0
-        self.fire_pending = False
-        self.measured: tuple | None = None  # (rows, mean context) stashed at the last fire
-        self.pending: tuple | None = None  # the last δ̂ [layers, tiers] (device), not yet consumed
+        self.cap = graph_capacity(vllm_config)
+        self.layers: list | None = None  # bind_layers (standalone drivers) or vLLM's layers
+        self.group: _Group | None = None
+        self.canary = CanaryClock(self.cfg.canary_interval)
 
-    # -- binding ----------------------------------------------------------------
+    @property
+    def shared(self) -> SharedState | None:
+        return None if self.group is None else self.group.shared
+
     def bind_layers(self, layers: list) -> None:
         """The attention layers of this group (objects with ``kv_cache`` and ``impl``)."""
         self.layers = list(layers)
-        self._cache_ptr = None
+        self.group = None
 
-    def _attach(self) -> bool:
-        """Bind every layer's impl to its KV cache and the shared state (once per cache)."""
+    def _bound(self) -> _Group | None:
+        """The group over the layers' current caches; None while vLLM profiles memory
+        (no KV cache yet). Rebinds when vLLM hands the layers new caches."""
         if self.layers is None:
             self.layers = _vllm.attention_layers(self.vllm_config, self.layer_names)
-        first = getattr(self.layers[0], "kv_cache", None) if self.layers else None
-        if first is not None and self._cache_ptr is not None and first.data_ptr() == self._cache_ptr:
-            return True
         caches = [getattr(layer, "kv_cache", None) for layer in self.layers]
         if not caches or any(c is None or c.numel() == 0 for c in caches):
-            return False  # memory profiling: no KV cache yet
-        cfg = self.cfg
-        self.shared = SharedState(caches[0].shape[0], self.kv_cache_spec.block_size, cfg.k_group, self.residual_slots,
-                                  cfg.kref_window, self.device)
-        self.impls = [layer.impl for layer in self.layers]
-        for impl, cache in zip(self.impls, caches):
-            impl.bind(cache, self.shared)
-        self.headers = HeaderWriter([impl.store for impl in self.impls])
-        tail = self.cap * (5 + 2 * len(self.impls)) + 64
-        self.image = StepImage(self.cap, cfg.canary_max_q, 3 + cfg.k_group, tail, self.device)
-        impl0 = self.impls[0]
-        dev = torch.device(self.device)
-        self.workspace = (torch.empty(self.cap, impl0.num_heads, self.num_splits, impl0.head_size, device=dev),
-                          torch.empty(self.cap, impl0.num_heads, self.num_splits, 2, device=dev))
-        self.canary_ws = torch.empty(len(self.impls) * impl0.num_kv_heads * len(SUPPORTED_BITS), device=dev)
-        self._cache_ptr = caches[0].data_ptr()
-        self.measured = self.pending = None
-        return True
+            return None
+        if self.group is None or self.group.cache_ptr != caches[0].data_ptr():
+            self.group = _Group(self, self.layers, caches)
+            self.canary.reset()
+        return self.group
 
-    # -- canary -----------------------------------------------------------------
-    def _run_canary(self) -> None:
-        """δ̂ for every layer from the query rows stashed on the fire step; the
-        controllers consume the previous fire's δ̂ (long finished on the GPU)."""
-        nq, ctx_mean = self.measured
-        self.measured = None
-        if self.pending is not None:
-            deltas, prev_ctx = self.pending
-            self.pending = None
-            for impl, d in zip(self.impls, deltas.tolist()):
-                impl.controller.observe(dict(zip(SUPPORTED_BITS, d)), prev_ctx)
-        pl = self.shared.planner
-        if pl.kref_fill < self.cfg.k_group:
-            return
-        kref = ring_view(torch.stack([i.kref_buf for i in self.impls]), pl.kref_pos, pl.kref_fill, dim=1)
-        q = torch.stack([i.stash[:nq] for i in self.impls])
-        deltas = canary_kl(q, kref, SUPPORTED_BITS, self.cfg.k_group, self.impls[0].scale, workspace=self.canary_ws)
-        self.pending = (_vllm.tp_mean(deltas), ctx_mean)
-
-    # -- build ------------------------------------------------------------------
+    # -- the step ---------------------------------------------------------------
     def build(self, common_prefix_len: int, common_attn_metadata, fast_build: bool = False) -> EchoKVMetadata:
-        cm = common_attn_metadata
+        with record_function("echokv.build"):
+            return self._build(common_attn_metadata)
+
+    def _mapping(self, cm, dummy: bool):
+        """The step's (lengths, slots) on the host: derived from host copies when vLLM
+        exposes them, else read back from the device (a wait: dummy steps only)."""
+        bs = self.kv_cache_spec.block_size
+        n, t = cm.num_reqs, cm.num_actual_tokens
+        host = host_lens_and_slots(cm, bs) if self.host_slots else None
+        if host is not None:
+            self.host_slot_steps += 1
+            if not self.check_host_slots:
+                return host
+        elif self.check_host_slots and self.host_slots and not dummy:
+            raise AssertionError("ECHOKV_CHECK_HOST_SLOTS=1 but the host slot mapping is unavailable")
+        dev = (cm.seq_lens[:n].cpu().long(), cm.slot_mapping[:t].cpu().long())
+        if host is not None and not (torch.equal(host[0], dev[0]) and torch.equal(host[1], dev[1])):
+            raise AssertionError("EchoKV host slot mapping differs from vLLM's")
+        return dev
+
+    def _build(self, cm) -> EchoKVMetadata:
         if getattr(cm, "causal", True) is not True:
             raise NotImplementedError("EchoKV supports causal decoder attention only")
         n, t = cm.num_reqs, cm.num_actual_tokens
-        bs = self.kv_cache_spec.block_size
         dummy = is_dummy_step(cm)
-        host = host_lens_and_slots(cm, bs) if self.host_slots else None
-        if host is not None:
-            lens_cpu, slots_cpu = host
-            self.host_slot_steps += 1
-        if host is None and self.check_host_slots and self.host_slots and not dummy:
-            raise AssertionError("ECHOKV_CHECK_HOST_SLOTS=1 but the host slot mapping is unavailable")
-        if host is None or self.check_host_slots:
-            # Device-to-host copies wait for the stream: only dummy steps and checks take them.
-            dev_lens, dev_slots = cm.seq_lens[:n].cpu().long(), cm.slot_mapping[:t].cpu().long()
-            if host is not None and not (torch.equal(lens_cpu, dev_lens) and torch.equal(slots_cpu, dev_slots)):
-                raise AssertionError("EchoKV host slot mapping differs from vLLM's")
-            lens_cpu, slots_cpu = dev_lens, dev_slots
+        lens, slots = self._mapping(cm, dummy)
+        md = EchoKVMetadata(num_actual_tokens=t, num_reqs=n, query_start_loc_cpu=cm.query_start_loc_cpu[: n + 1],
+                            seq_lens_cpu=lens, block_table=cm.block_table_tensor, slot_mapping=cm.slot_mapping,
+                            write=None)
+        group = self._bound()
+        if group is None:
+            return md
+        if self.canary.stashed is not None:
+            self._score_canary(group)  # before this step's writes move the K_ref ring
+        fire = self.canary.tick(dummy)
+        qsl = np.ascontiguousarray(cm.query_start_loc_cpu[: n + 1].numpy(), dtype=np.int32)
+        up = group.driver.run(qsl, np.ascontiguousarray(lens.numpy(), dtype=np.int32),
+                              np.ascontiguousarray(slots.numpy(), dtype=np.int64), group.tiers(), fire)
+        self.canary.fired(up.n_canary, up.canary_ctx)
+        group.driver.apply(up, group.headers)
+        md.write = WriteMeta(tok=up.tok, fin=up.fin, fin_count=up.fin_count, n_rows=up.n_tokens, n_fin=up.n_fin)
+        md.canary_rows = up.canary_rows
+        md.fire = up.n_canary > 0
+        if up.decode is not None:
+            n_dec = up.decode[0].numel()
+            md.decode = DecodeWork(*up.decode, num_splits=self.num_splits,
+                                   workspace=group.impls[0].decode_workspace(n_dec, self.num_splits, self.cap),
+                                   batch_invariant=self.cfg.batch_invariant)
+        if up.prefill:
+            md.prefill = self._prefill_work(group, up.prefill)
+        return md
 
-        # The batch, vectorized over requests.
-        qsl = cm.query_start_loc_cpu[: n + 1].numpy().astype(np.int64)
-        lens = lens_cpu.numpy().astype(np.int64)
-        qlen = np.diff(qsl)
-        live = (qlen > 0) & (lens > 0)
-        last_rows, last_ctx = (qsl[1:] - 1)[live], lens[live]
-        if (qlen <= 1).all():
-            d_idx = np.arange(n)  # decode-only, as graphs replay it: padding requests too (length 0)
-        else:
-            d_idx = np.flatnonzero(live & (qlen == 1))
-        d_lens = np.where(qlen[d_idx] == 1, lens[d_idx], 0)
-        d_rows = np.minimum(qsl[:-1][d_idx], max(t - 1, 0))
-        pre = np.flatnonzero(live & (qlen > 1))
-        prefill = [(int(qsl[r]), int(qsl[r + 1]), int(lens[r]), 0) for r in pre.tolist()]
-        prefill_reqs = pre.tolist()
-
-        write = canary_rows = None
-        fire = False
-        dec_views = (None, None, None)
-        if self._attach():
-            if self.measured is not None:
-                self._run_canary()  # before this step's plan moves the K_ref ring
-            if not dummy:
-                self.step += 1
-                if self.step % self.cfg.canary_interval == 0:
-                    self.fire_pending = True
-            nq = self.cfg.canary_max_q
-            canary = np.zeros(nq, np.int64)
-            if self.fire_pending and last_rows.size:
-                self.fire_pending = False
-                fire = True
-                k = min(nq, last_rows.size)
-                canary[:k] = last_rows[:k]
-                self.measured = (k, float(last_ctx[:k].mean()))
-            write, canary_rows, dec_views = self._plan(slots_cpu, canary, (d_rows, d_idx, d_lens))
-
+    def _prefill_work(self, group: _Group, chunks: list) -> PrefillWork:
+        entries = [(qs, qe, ctx, 0) for qs, qe, ctx, _ in chunks]
+        work = PrefillWork(entries=entries, reqs=[r for *_, r in chunks])
+        impl0 = group.impls[0]
         dev = self.device
-        prefill_tiles = prefill_dense = None
-        if prefill and self.impls and pf.kernels_take(self.impls[0].head_size, self.gqa):
-            if not pf.use_dense(prefill, self.impls[0].head_size):
-                prefill_tiles = pf.build_tiles(prefill, prefill_reqs, self.gqa, dev)
+        if pf.kernels_take(impl0.head_size, self.gqa):
+            if not pf.use_dense(entries, impl0.head_size):
+                work.tiles = pf.build_tiles(entries, work.reqs, self.gqa, dev)
             else:
-                plan = pf.build_dense_plan(prefill, prefill_reqs, self.gqa, dev)
-                nbytes = pf.dense_workspace_bytes(self.impls[0].store, plan.packs.shape[0])
-                prefill_dense = (plan, torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev))
-        og_rows = pf.build_own_group_rows(prefill, prefill_reqs, dev) if prefill and self.cfg.own_group_exact else None
-        return EchoKVMetadata(
-            num_actual_tokens=t, num_reqs=n, query_start_loc_cpu=cm.query_start_loc_cpu[: n + 1].cpu(),
-            seq_lens_cpu=lens_cpu, block_table=cm.block_table_tensor, slot_mapping=cm.slot_mapping, write=write,
-            canary_rows=canary_rows, fire=fire, decode_rows=dec_views[0] if d_idx.size else None,
-            decode_reqs=dec_views[1] if d_idx.size else None, decode_lens=dec_views[2] if d_idx.size else None,
-            num_splits=self.num_splits,
-            decode_workspace=self.workspace if d_idx.size and d_idx.size <= self.cap else None,
-            prefill=prefill, prefill_reqs=prefill_reqs, prefill_tiles=prefill_tiles, prefill_dense=prefill_dense,
-            own_group_rows=og_rows)
+                plan = pf.build_dense_plan(entries, work.reqs, self.gqa, dev)
+                nbytes = pf.dense_workspace_bytes(impl0.store, plan.packs.shape[0])
+                work.dense = (plan, torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev))
+        if self.cfg.own_group_exact:
+            work.own_group_rows = pf.build_own_group_rows(entries, work.reqs, dev)
+        return work
 
-    def _plan(self, slots_cpu: torch.Tensor, canary: np.ndarray, decode: tuple):
-        """Host side of the step's writes for every layer, then one upload."""
-        shared = self.shared
-        plan = shared.planner.plan(slots_cpu)
-        # Which blocks open is the same in every layer (offset-0 writes and writes into
-        # never-opened blocks); the tier each opens at is the layer's own.
-        opens = self.impls[0].store.pool.fresh_opens(plan)
-        opened = []
-        if opens.size or plan.evictions:
-            for impl in self.impls:
-                st = impl.store
-                for ev in plan.evictions:  # rare; before the slot is reused below
-                    st._seal(ev)
-                if opens.size:
-                    opened.append(st.open_blocks(opens, impl.controller.bits, protect=plan.touched_np))
-        shared.commit(plan)
-        tail = [plan.res_map_block, plan.res_map_value, plan.res_group_slot, plan.res_group_value]
-        if opened:  # the same blocks in every layer: their ids once, then each layer's headers
-            self.headers.check(opens)
-            tail += [opens, np.concatenate([np.ascontiguousarray(h).view(np.int64).reshape(-1) for _, h in opened])]
-        tok = np.stack([plan.tok_slot, plan.tok_res, plan.tok_sealed, plan.tok_kref])
-        fin_count, canary_rows, dec_views, tok_d, fin_d, views = self.image.upload(
-            plan.n_fin, canary, decode, tok, plan.fin, tail)
-        shared.apply_res_map(*views[:4])
-        if opened:
-            self.headers.write(views[4], views[5])
-        write = WriteMeta(tok=tok_d, fin=fin_d, fin_count=fin_count, n_rows=plan.n_rows, n_fin=plan.n_fin)
-        return write, canary_rows, dec_views
+    def _score_canary(self, group: _Group) -> None:
+        """δ̂ for every layer from the rows stashed on the fire step; the controllers
+        take the fire before it."""
+        rows, ctx = self.canary.stashed
+        self.canary.stashed = None
+        if self.canary.scored is not None:
+            deltas, prev_ctx = self.canary.scored
+            self.canary.scored = None
+            for impl, d in zip(group.impls, deltas.tolist()):
+                impl.controller.observe(dict(zip(SUPPORTED_BITS, d)), prev_ctx)
+        planner = group.shared.planner
+        if planner.kref_fill < self.cfg.k_group:
+            return
+        with record_function("echokv.canary"):
+            kref = ring_view(torch.stack([i.kref_buf for i in group.impls]), planner.kref_pos, planner.kref_fill,
+                             dim=1)
+            q = torch.stack([i.stash[:rows] for i in group.impls])
+            deltas = canary_kl(q, kref, SUPPORTED_BITS, self.cfg.k_group, group.impls[0].scale,
+                               workspace=group.canary_ws)
+            self.canary.scored = (_vllm.tp_mean(deltas), ctx)
 
+
+# ---- implementation ----------------------------------------------------------------
 
 class EchoKVAttentionImpl(AttentionImpl):
+    # Decode workspaces shared by every layer of the process, by shape: layers run
+    # one after another on one stream.
+    _workspaces: ClassVar[dict] = {}
+
     def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int | None = None,
                  alibi_slopes: list[float] | None = None, sliding_window: int | None = None,
                  kv_cache_dtype: str = "auto", logits_soft_cap: float | None = None,
@@ -441,70 +409,111 @@ class EchoKVAttentionImpl(AttentionImpl):
             raise NotImplementedError("ECHOKV_OWN_GROUP_EXACT needs head size 64 or 128 and GQA <= 128")
         self.controller = LayerController(cfg.controller)
         # Allocated at model construction so vLLM's memory profiler counts them: the
-        # full-precision K of each block's open group (+1 spare row), the K_ref ring and
-        # the canary's stashed query rows.
+        # full-precision K of each block's open group (+1 spare row), the K_ref ring,
+        # the canary's stashed query rows and the decode workspaces.
         dt = model_dtype()
         self.residual = torch.zeros(residual_slots(cfg) + 1, cfg.k_group, self.num_kv_heads, head_size, dtype=dt)
         self.kref_buf = torch.zeros(cfg.kref_window, self.num_kv_heads, head_size, dtype=torch.float32)
         self.stash = torch.zeros(cfg.canary_max_q, num_heads, head_size, dtype=dt)
+        self._reserve_workspace(dt)
         self.store: TieredKVCache | None = None
         self.forward_calls = 0  # eager forwards; graph replays do not enter Python
+
+    # -- buffers -------------------------------------------------------------------
+    def _reserve_workspace(self, q_dtype: torch.dtype):
+        """The decode workspace rows a graph-sized step needs, reserved now when a GPU is
+        current (vLLM builds layers on the device) and shared by all layers."""
+        vc = _vllm.current_vllm_config()
+        if vc is None or not torch.cuda.is_available():
+            return None
+        cap = graph_capacity(vc)
+        bs = getattr(getattr(vc, "cache_config", None), "block_size", None) or block_multiple()
+        splits = decode_splits(vc.model_config.max_model_len, bs)
+        layout = TieredLayout(self.num_kv_heads, self.head_size, bs, self.cfg.mem_bits, self.cfg.k_group,
+                              self.cfg.v_group)
+        from echokv_amd import _lib
+
+        flags = _lib.DECODE_BATCH_INVARIANT if self.cfg.batch_invariant else 0
+        rows = _lib.lib().echokv_decode_workspace_rows(_lib.byref(layout.abi(1, layout.page_bytes)), self.num_heads,
+                                                       _lib.DTYPES[q_dtype], cap, splits, flags)
+        if rows > 0:
+            self._workspace(int(rows), torch.device("cuda", torch.cuda.current_device()))
+
+    def _workspace(self, rows: int, device) -> tuple:
+        """The process's shared workspace for this head shape, allocated once: a captured
+        graph keeps its address, so it is never replaced by a larger one."""
+        key = (str(device), self.num_heads, self.head_size)
+        if key not in self._workspaces:
+            self._workspaces[key] = (
+                torch.empty(rows, self.num_heads, self.head_size, dtype=torch.float32, device=device),
+                torch.empty(rows, self.num_heads, 2, dtype=torch.float32, device=device))
+        return self._workspaces[key]
+
+    def decode_workspace(self, n_dec: int, num_splits: int, cap: int) -> tuple | None:
+        """``(acc, ml)`` for a decode of ``n_dec`` entries, or None (an eager step larger
+        than any graph: the call allocates its own)."""
+        store = self.store
+        flags = 1 if self.cfg.batch_invariant else 0
+        rows = dec.workspace_rows(store, self.num_heads, self.stash.dtype, n_dec, num_splits, flags)
+        full = dec.workspace_rows(store, self.num_heads, self.stash.dtype, max(cap, n_dec), num_splits, flags)
+        acc, ml = self._workspace(full, store.device)  # sized for the graph capacity on first use
+        return (acc, ml) if acc.shape[0] >= rows else None
+
+    def decode_tier(self) -> int:
+        """The tier whose specialised decode kernel runs: the layer's current tier."""
+        return self.controller.bits
 
     def bind(self, kv_cache: torch.Tensor, shared: SharedState) -> None:
         """Wrap ``kv_cache`` (this layer's view of vLLM's pool, ``[blocks, 1, block, bytes]``)."""
         raw = kv_cache.view(torch.uint8)
-        if raw.dim() != 4:
-            raise RuntimeError(f"unexpected EchoKV cache view shape={tuple(raw.shape)}")
-        num_blocks, slots, block_size, row = raw.shape
-        if slots != 1 or raw.stride(3) != 1 or raw.stride(2) != row:
-            raise RuntimeError(f"unexpected EchoKV cache view shape={tuple(raw.shape)} stride={raw.stride()}")
-        pages = torch.as_strided(raw, (num_blocks, block_size * row), (raw.stride(0), 1))
+        shape = tuple(raw.shape)
+        if raw.dim() != 4 or shape[1] != 1 or raw.stride(3) != 1 or raw.stride(2) != shape[3]:
+            raise RuntimeError(f"unexpected EchoKV cache view shape={shape} stride={raw.stride()}")
+        num_blocks, _, block_size, row = shape
+        pages = raw.as_strided((num_blocks, block_size * row), (raw.stride(0), 1))
         layout = TieredLayout(self.num_kv_heads, self.head_size, block_size, self.cfg.mem_bits, self.cfg.k_group,
                               self.cfg.v_group)
         dev = pages.device
-        self.residual = self.residual.to(dev)
-        self.kref_buf = self.kref_buf.to(dev)
-        self.stash = self.stash.to(dev)
+        self.residual, self.kref_buf, self.stash = (t.to(dev) for t in (self.residual, self.kref_buf, self.stash))
         self.store = TieredKVCache(layout, pages, residual=self.residual, shared=shared)
 
-    # -- write path --------------------------------------------------------------
-    def do_kv_cache_update(self, layer, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
-                           slot_mapping: torch.Tensor) -> None:
+    # -- per layer and step -------------------------------------------------------
+    @staticmethod
+    def _step_metadata(layer):
+        """This layer's metadata of the step (vLLM's forward context or a driver's)."""
         md = _vllm.forward_metadata()
-        if isinstance(md, list):  # speculative decoding: [0] is the base model
+        if isinstance(md, list):  # speculative decoding: the base model's metadata comes first
             md = md[0]
         if isinstance(md, dict):
             md = md[layer.layer_name]
+        return md
+
+    def do_kv_cache_update(self, layer, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
+                           slot_mapping: torch.Tensor) -> None:
+        md = self._step_metadata(layer)
         if md is None or md.write is None:
             return
-        self.store.apply(md.write, key, value, self.kref_buf, capturing=_capturing(key))
+        with record_function("echokv.write"):
+            self.store.apply(md.write, key, value, self.kref_buf, capturing=_capturing(key))
 
-    # -- read path ---------------------------------------------------------------
     def forward(self, layer, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
                 attn_metadata: EchoKVMetadata, output: torch.Tensor, output_scale: torch.Tensor | None = None,
                 output_block_scale: torch.Tensor | None = None) -> torch.Tensor:
         if output_scale is not None or output_block_scale is not None:
             raise NotImplementedError("fused output quantization is not supported by EchoKV")
         md = attn_metadata
-        if md is None or md.write is None:  # profiling / warm-up run
+        if md is None or md.write is None:  # memory profiling / warm-up
             return output
         self.forward_calls += 1
-        store = self.store
         out = output.view(output.shape[0], -1, query.shape[-1])
-        if md.prefill:
-            og_key = None
-            if md.own_group_rows is not None:  # own-group-exact: this step's key rows, aligned with the queries
-                og_key = key.view(key.shape[0], self.num_kv_heads, self.head_size)
-            pf.prefill_attention(store, query, out, md.prefill, md.prefill_reqs, md.block_table, self.scale,
-                                 tiles=md.prefill_tiles, dense=md.prefill_dense, own_group_key=og_key,
-                                 own_group_rows=md.own_group_rows)
-        if md.decode_rows is not None:
-            # Query / block-table rows by index, output rows written in place.
-            dec.decode_attention(store, query, md.block_table, md.decode_lens, self.scale, q_rows=md.decode_rows,
-                                 bt_rows=md.decode_reqs, out=out, num_splits=md.num_splits,
-                                 workspace=md.decode_workspace, tier=self.controller.bits)
-        # The canary's query rows (scored at the next build). A graph captures the
-        # copy unconditionally: its rows are valid either way.
+        if md.prefill is not None:
+            with record_function("echokv.prefill_attn"):
+                md.prefill.run(self, query, key, md.block_table, out)
+        if md.decode is not None:
+            with record_function("echokv.decode_attn"):
+                md.decode.run(self, query, md.block_table, out)
+        # Stash the canary's query rows (scored at the next build); a graph records the
+        # copy on every step, its rows being valid either way.
         if md.fire or _capturing(query):
             torch.index_select(query, 0, md.canary_rows, out=self.stash)
         return output
@@ -512,6 +521,19 @@ class EchoKVAttentionImpl(AttentionImpl):
 
 def _capturing(t: torch.Tensor) -> bool:
     return t.is_cuda and torch.cuda.is_current_stream_capturing()
+
+
+def decode_splits(max_model_len: int, block_size: int) -> int:
+    """The split grid of a decode: enough splits of ``BLOCKS_PER_SPLIT`` blocks for the
+    longest sequence, at most ``MAX_DECODE_SPLITS``."""
+    max_blocks = -(-max_model_len // block_size)
+    return max(1, min(-(-max_blocks // dec.BLOCKS_PER_SPLIT), MAX_DECODE_SPLITS))
+
+
+def graph_capacity(vllm_config) -> int:
+    """The largest batch a captured graph replays (vLLM's capture sizes), 512 by default."""
+    comp = getattr(vllm_config, "compilation_config", None)
+    return getattr(comp, "max_cudagraph_capture_size", None) or 512
 
 
 def residual_slots(cfg, vllm_config=None) -> int:

@@ -1,5 +1,5 @@
 """Build ``echokv_amd/libechokv.so`` (gfx950) from ``echokv_amd/csrc/*.hip`` with hipcc,
-and the native host planner ``echokv_amd/libechokv_host.so`` from ``echokv_amd/host/plan.cpp``
+and the native host side ``echokv_amd/libechokv_host.so`` from ``echokv_amd/host/*.cpp``
 with g++.
 
     python -m echokv_amd.build            # or __graft_entry__.build()
@@ -49,7 +49,7 @@ def _run(cmd):
     return err
 
 
-HOST_SRC = PKG / "host" / "plan.cpp"
+HOST_SRCS = (PKG / "host" / "plan.cpp", PKG / "host" / "step.cpp")
 HOST_OUT = PKG / "libechokv_host.so"
 
 
@@ -57,7 +57,7 @@ def build_host() -> str:
     """The native host planner (CPU code, g++): ``libechokv_host.so``."""
     tmp = HOST_OUT.with_suffix(".so.tmp")
     log = _run([os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
-                f"-I{PKG.parent / 'include'}", str(HOST_SRC), "-o", str(tmp)])
+                f"-I{PKG.parent / 'include'}", *map(str, HOST_SRCS), "-o", str(tmp)])
     os.replace(tmp, HOST_OUT)
     return log
 

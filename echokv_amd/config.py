@@ -21,6 +21,10 @@ raises are those of ``echokv_vllm/config.py:40-99``:
     ECHOKV_KREF_WINDOW      K_ref ring size in tokens (default 64; >= ECHOKV_K_GROUP)
     ECHOKV_CANARY_MAX_Q     decode queries sampled per fire (default 8)
 
+This build's own: ECHOKV_OWN_GROUP_EXACT=1 (prefill sees each query's own K
+group at full precision) and ECHOKV_BATCH_INVARIANT=0 (the balanced decode
+schedule); ECHOKV_V_GROUP must be a power of 2 from 4 to 256.
+
 Read elsewhere: ECHOKV_CUDAGRAPH=0 keeps attention out of full graphs (the
 backend), ECHOKV_CHECK_HOST_SLOTS=1 checks the host slot mapping every step. The
 reference's Triton-only switches (ECHOKV_DISABLE_TRITON, ECHOKV_AUTOTUNE,
@@ -50,6 +54,7 @@ class EchoKVConfig:
     kref_window: int = 64
     canary_max_q: int = 8
     own_group_exact: bool = False
+    batch_invariant: bool = True
     controller: ControllerParams = field(default_factory=ControllerParams)
 
 
@@ -72,6 +77,12 @@ def _tier(name: str):
 
 def _is_pow2(x: int) -> bool:
     return x > 0 and not x & (x - 1)
+
+
+def v_group_supported(v_group: int, head_size: int | None = None) -> bool:
+    """V groups the kernels store and read: powers of two from 4 to 256 channels
+    (dividing the head size, when one is given)."""
+    return _is_pow2(v_group) and 4 <= v_group <= 256 and (head_size is None or head_size % v_group == 0)
 
 
 class Setting(NamedTuple):
@@ -97,7 +108,11 @@ SETTINGS: tuple[Setting, ...] = (
     Setting("ECHOKV_ALPHA", "alpha", float, lambda s: 0.1),
     Setting("ECHOKV_K_GROUP", "k_group", int, lambda s: 32,
             lambda v, s: None if v >= 16 and _is_pow2(v) else f"ECHOKV_K_GROUP must be a power of 2 and >= 16, got {v}"),
-    Setting("ECHOKV_V_GROUP", "v_group", int, lambda s: 32),
+    # The reference takes any V group dividing the head size; the kernels reduce a V
+    # group across lanes in power-of-two segments of 4-channel quads.
+    Setting("ECHOKV_V_GROUP", "v_group", int, lambda s: 32,
+            lambda v, s: None if v_group_supported(v) else
+            f"ECHOKV_V_GROUP must be a power of 2 from 4 to 256 (this build's kernels), got {v}"),
     Setting("ECHOKV_RESIDUAL_SLOTS", "residual_slots", int, lambda s: None),
     Setting("ECHOKV_CANARY_INTERVAL", "canary_interval", int, lambda s: 64,
             lambda v, s: None if v >= 1 else "ECHOKV_CANARY_INTERVAL must be >= 1"),
@@ -108,6 +123,10 @@ SETTINGS: tuple[Setting, ...] = (
     # at full precision, as decode did (the fix docs/ECHOKV_VLLM_PLUGIN.md:261-266 names).
     Setting("ECHOKV_OWN_GROUP_EXACT", "own_group_exact", _flag, lambda s: False,
             lambda v, s: None if not v or s["k_group"] <= 64 else "ECHOKV_OWN_GROUP_EXACT needs ECHOKV_K_GROUP <= 64"),
+    # This build's own: 1 (default) splits each decode sequence by its own length, so
+    # its result does not depend on the batch (the reference's decode semantics); 0
+    # spreads the batch's blocks evenly over the GPU (faster on uneven batches).
+    Setting("ECHOKV_BATCH_INVARIANT", "batch_invariant", lambda raw: raw != "0", lambda s: True),
 )
 
 _CONTROLLER_KEYS = ("tau0", "l0", "tau_scaling", "alpha", "init_bits", "fixed_bits", "frozen")

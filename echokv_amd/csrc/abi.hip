@@ -163,6 +163,16 @@ int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* b
 
 namespace {
 
+// The MFMA decode kernels take: D 64 or 128 with at least D/16 channels per V
+// group, 16-token tiles inside one K group (one k_scale / k_min row per tile),
+// power-of-two block size and K group, <= 4 chunks per page. Any other layout
+// takes decode_any.
+bool decode_mfma(const echokv_layout* L) {
+  const bool pow2 = !(L->block_size & (L->block_size - 1)) && !(L->k_group & (L->k_group - 1));
+  return (L->head_size == 64 || L->head_size == 128) && L->v_group % (L->head_size / 16) == 0 &&
+         L->k_group >= 16 && pow2 && L->chunks_per_page <= 4 && L->num_blocks * L->chunks_per_page < (1LL << 24);
+}
+
 // echokv_decode and echokv_decode_static: the checks, then decode + merge with
 // the given workspaces, or (static_scratch) with the library's static scratch.
 int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,
@@ -172,13 +182,7 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
                int32_t num_splits, int32_t blocks_per_split, int32_t tier, int32_t flags, float* acc, float* ml,
                bool static_scratch, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;
-  // The MFMA kernels: D 64 or 128 with at least D/16 channels per V group, 16-token
-  // tiles inside one K group (one k_scale / k_min row per tile), power-of-two block
-  // size and K group, <= 4 chunks per page. Any other layout takes decode_any.
-  const bool pow2 = !(L->block_size & (L->block_size - 1)) && !(L->k_group & (L->k_group - 1));
-  const bool mfma = (L->head_size == 64 || L->head_size == 128) && L->v_group % (L->head_size / 16) == 0 &&
-                    L->k_group >= 16 && pow2 && L->chunks_per_page <= 4 &&
-                    L->num_blocks * L->chunks_per_page < (1LL << 24);
+  const bool mfma = decode_mfma(L);
   if (!mfma && L->head_size > ek::kMaxAnyD) return ECHOKV_ESHAPE;
   if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
   const int gqa = num_q_heads / L->num_kv_heads;
@@ -284,6 +288,30 @@ int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int
   return decode_run(L, pages, block_res, res_group, res, query, q_s0, q_s1, q_dtype, num_q_heads, q_rows,
                     block_table, bt_s0, bt_rows, seq_lens, num_seqs, softmax_scale, num_splits, blocks_per_split,
                     tier, flags, nullptr, nullptr, true, out, o_s0, o_s1, out_dtype, stream);
+}
+
+int64_t echokv_decode_workspace_rows(const echokv_layout* L, int32_t num_q_heads, int32_t q_dtype,
+                                     int64_t num_seqs, int32_t num_splits, int32_t flags) {
+  if (!lay_ok(L) || num_q_heads <= 0 || num_q_heads % L->num_kv_heads || num_seqs < 0 || num_splits <= 0 ||
+      !dtype_ok(q_dtype) || (flags & ~ECHOKV_DECODE_BATCH_INVARIANT))
+    return -1;
+  const int64_t split_rows = num_seqs * num_splits;
+  if (!decode_mfma(L) || (flags & ECHOKV_DECODE_BATCH_INVARIANT) || num_seqs == 0) return split_rows;
+  // Balanced schedule: two partial slots per range; the range count depends on the
+  // tier's kernel (its occupancy), so the largest over the tiers.
+  ek::DecodeArgs a;
+  a.L = to_lay(L);
+  a.q_dtype = q_dtype;
+  a.num_seqs = num_seqs;
+  a.num_splits = num_splits;
+  int64_t rows = 0;
+  for (int tier : {2, 4, 8}) {
+    a.tier = tier;
+    long r = 0;
+    if (ek::decode_ranges(a, r) != hipSuccess) return -1;
+    rows = rows > 2 * r ? rows : 2 * r;
+  }
+  return rows < split_rows ? rows : split_rows;
 }
 
 int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,

@@ -27,166 +27,88 @@
 #include <vector>
 
 #include "echokv_host.h"
+#include "state.h"
 
-namespace {
+namespace ekh {
 
-constexpr int kExtra[9] = {0, 0, 0, 0, 1, 0, 0, 0, 3};  // pool chunks per tier beyond chunk 0
-
-struct Planner {
-  int64_t nb = 0;
-  bool growable = false;  // created without a block count: per-block arrays grow on demand
-  int bs = 0, kg = 0, gpb = 0, R = 0, W = 0;
-  // Residual slots.
-  std::vector<int32_t> free_stack;  // back() is handed out next
-  std::vector<int64_t> s_block, s_last, s_taken, s_prot;
-  std::vector<int32_t> s_group, s_fill;
-  std::vector<uint8_t> s_used;
-  std::vector<int32_t> block_slot;  // -1: no open group in the residual
-  std::vector<uint8_t> sealed;      // bit g: K group g sealed by an eviction
-  int64_t step = 0, taken = 0, kref_pos = 0, kref_fill = 0;
-  // Per-block bookkeeping read by the pools (tiered_cache.py:243-271).
-  std::vector<int64_t> fill_h, last_h, cum_h;
-
-  // The last plan.
-  int64_t n_rows = 0, n_fin = 0;
-  std::vector<int64_t> stage;  // [n_fin | tok 4 x n_rows | fin n_fin x (3 + kg) | res blocks | res values | grp slots | grp groups]
-  std::vector<int64_t> evict, opens, touched, res_b, res_v, grp_s, grp_g;
-  std::vector<int64_t> res_stamp, res_at, grp_stamp, grp_at;  // first-appearance position this step
-  // Scratch.
-  std::vector<int64_t> rows, key, order;
-
-  void grow(int64_t need) {
-    if (need <= nb) return;
-    const int64_t n = std::max<int64_t>(need, 2 * nb);
-    block_slot.resize(n, -1);
-    sealed.resize(n, 0);
-    fill_h.resize(n, 0);
-    last_h.resize(n, 0);
-    cum_h.resize(n, 0);
-    res_stamp.resize(n, 0);
-    res_at.resize(n, 0);
-    nb = n;
-  }
-  void res_op(int64_t b, int64_t v) {
-    if (res_stamp[b] == step) {
-      res_v[res_at[b]] = v;
-    } else {
-      res_stamp[b] = step;
-      res_at[b] = (int64_t)res_b.size();
-      res_b.push_back(b);
-      res_v.push_back(v);
-    }
-  }
-  void grp_op(int32_t s, int32_t g) {
-    if (grp_stamp[s] == step) {
-      grp_g[grp_at[s]] = g;
-    } else {
-      grp_stamp[s] = step;
-      grp_at[s] = (int64_t)grp_s.size();
-      grp_s.push_back(s);
-      grp_g.push_back(g);
-    }
-  }
-  void release(int32_t s) {
-    const int64_t b = s_block[s];
-    s_used[s] = 0;
-    block_slot[b] = -1;
-    free_stack.push_back(s);
-    res_op(b, -1);
-  }
-  // The least recently written slot outside this step's protected set, or -1.
-  int32_t victim() const {
-    int32_t best = -1;
-    for (int32_t s = 0; s < R; ++s) {
-      if (!s_used[s] || s_prot[s] == step) continue;
-      if (best < 0 || s_last[s] < s_last[best] || (s_last[s] == s_last[best] && s_taken[s] < s_taken[best])) best = s;
-    }
-    return best;
-  }
-  int32_t take(int64_t b, int32_t g) {
-    const int32_t s = free_stack.back();
-    free_stack.pop_back();
-    s_used[s] = 1;
-    s_block[s] = b;
-    s_group[s] = g;
-    s_fill[s] = 0;
-    s_last[s] = 0;
-    s_taken[s] = ++taken;
-    s_prot[s] = step;
-    block_slot[b] = s;
-    res_op(b, s);
-    grp_op(s, g);
-    return s;
-  }
-};
-
-struct Pool {
-  Planner* p = nullptr;
-  int64_t nb = 0;
-  int kc = 0, bs = 0;
-  std::vector<int64_t> free_chunks;  // back() is handed out next
-  int64_t pool_size = 0;
-  std::vector<int64_t> tag, table, mark;  // table: [nb, 3]
-  int64_t tok_tier[9] = {};
-  int64_t opened[9] = {};
-  int64_t downgraded = 0, demoted = 0, sealed_groups = 0;
-
-  void settle(int64_t b) {
-    tok_tier[tag[b]] += p->cum_h[b] - mark[b];
-    mark[b] = p->cum_h[b];
-  }
-  void give_back(int64_t b) {
-    for (int j = 0; j < kExtra[tag[b]]; ++j) free_chunks.push_back(table[3 * b + j]);
-  }
-};
-
-}  // namespace
-
-struct ekh_planner : Planner {};
-struct ekh_pool : Pool {};
-
-extern "C" {
-
-ekh_planner* ekh_planner_new(int64_t num_blocks, int32_t block_size, int32_t k_group, int32_t residual_slots,
-                             int32_t kref_window) {
-  if (block_size <= 0 || k_group <= 0 || block_size % k_group || block_size / k_group > 8 || residual_slots <= 0 ||
-      kref_window <= 0)
-    return nullptr;
-  ekh_planner* p = new (std::nothrow) ekh_planner();
-  if (!p) return nullptr;
-  p->growable = num_blocks <= 0;
-  if (p->growable) num_blocks = 1;
-  p->nb = num_blocks;
-  p->bs = block_size;
-  p->kg = k_group;
-  p->gpb = block_size / k_group;
-  p->R = residual_slots;
-  p->W = kref_window;
-  for (int32_t s = residual_slots - 1; s >= 0; --s) p->free_stack.push_back(s);
-  p->s_block.assign(residual_slots, -1);
-  p->s_last.assign(residual_slots, 0);
-  p->s_taken.assign(residual_slots, 0);
-  p->s_prot.assign(residual_slots, 0);
-  p->s_group.assign(residual_slots, 0);
-  p->s_fill.assign(residual_slots, 0);
-  p->s_used.assign(residual_slots, 0);
-  p->grp_stamp.assign(residual_slots, 0);
-  p->grp_at.assign(residual_slots, 0);
-  p->block_slot.assign(num_blocks, -1);
-  p->sealed.assign(num_blocks, 0);
-  p->fill_h.assign(num_blocks, 0);
-  p->last_h.assign(num_blocks, 0);
-  p->cum_h.assign(num_blocks, 0);
-  p->res_stamp.assign(num_blocks, 0);
-  p->res_at.assign(num_blocks, 0);
-  return p;
+void Planner::grow(int64_t need) {
+  if (need <= nb) return;
+  const int64_t n = std::max<int64_t>(need, 2 * nb);
+  block_slot.resize(n, -1);
+  sealed.resize(n, 0);
+  fill_h.resize(n, 0);
+  last_h.resize(n, 0);
+  cum_h.resize(n, 0);
+  res_stamp.resize(n, 0);
+  res_at.resize(n, 0);
+  nb = n;
 }
 
-void ekh_planner_free(ekh_planner* p) { delete p; }
+void Planner::res_op(int64_t b, int64_t v) {
+  if (res_stamp[b] == step) {
+    res_v[res_at[b]] = v;
+  } else {
+    res_stamp[b] = step;
+    res_at[b] = (int64_t)res_b.size();
+    res_b.push_back(b);
+    res_v.push_back(v);
+  }
+}
 
-int ekh_plan(ekh_planner* P, const int64_t* slot_mapping, int64_t n_rows, ekh_plan_view* out) {
-  if (!P || !out || n_rows < 0 || (n_rows && !slot_mapping)) return EKH_EINVAL;
-  Planner& p = *P;
+void Planner::grp_op(int32_t s, int32_t g) {
+  if (grp_stamp[s] == step) {
+    grp_g[grp_at[s]] = g;
+  } else {
+    grp_stamp[s] = step;
+    grp_at[s] = (int64_t)grp_s.size();
+    grp_s.push_back(s);
+    grp_g.push_back(g);
+  }
+}
+
+void Planner::release(int32_t s) {
+  const int64_t b = s_block[s];
+  s_used[s] = 0;
+  block_slot[b] = -1;
+  free_stack.push_back(s);
+  res_op(b, -1);
+}
+
+// The least recently written slot outside this step's protected set, or -1.
+int32_t Planner::victim() const {
+  int32_t best = -1;
+  for (int32_t s = 0; s < R; ++s) {
+    if (!s_used[s] || s_prot[s] == step) continue;
+    if (best < 0 || s_last[s] < s_last[best] || (s_last[s] == s_last[best] && s_taken[s] < s_taken[best])) best = s;
+  }
+  return best;
+}
+
+int32_t Planner::take(int64_t b, int32_t g) {
+  const int32_t s = free_stack.back();
+  free_stack.pop_back();
+  s_used[s] = 1;
+  s_block[s] = b;
+  s_group[s] = g;
+  s_fill[s] = 0;
+  s_last[s] = 0;
+  s_taken[s] = ++taken;
+  s_prot[s] = step;
+  block_slot[b] = s;
+  res_op(b, s);
+  grp_op(s, g);
+  return s;
+}
+
+}  // namespace ekh
+
+using ekh::kExtra;
+using ekh::Planner;
+using ekh::Pool;
+
+namespace ekh {
+
+int plan_rows(Planner& p, const int64_t* slot_mapping, int64_t n_rows) {
   int64_t top_slot = -1;
   for (int64_t r = 0; r < n_rows; ++r) top_slot = std::max(top_slot, slot_mapping[r]);
   if (top_slot >= p.nb * p.bs) {
@@ -274,8 +196,15 @@ int ekh_plan(ekh_planner* P, const int64_t* slot_mapping, int64_t n_rows, ekh_pl
 
   // Per-row outputs, and the fin rows (whole groups first, then the others).
   const int64_t w = 3 + kg;
-  std::vector<int64_t> tok_res(n_rows, -1), tok_sealed(n_rows, 0), tok_kref(n_rows, -1);
-  std::vector<int64_t> fin_whole, fin_rest;
+  p.tok_res.assign(n_rows, -1);
+  p.tok_sealed.assign(n_rows, 0);
+  p.tok_kref.assign(n_rows, -1);
+  std::vector<int64_t>& tok_res = p.tok_res;
+  std::vector<int64_t>& tok_sealed = p.tok_sealed;
+  std::vector<int64_t>& tok_kref = p.tok_kref;
+  std::vector<int64_t>& fin_whole = p.fin;
+  std::vector<int64_t> fin_rest;
+  fin_whole.clear();
   for (const Unit& x : units) {
     if (!x.whole) continue;
     fin_whole.push_back(x.blk);
@@ -342,18 +271,170 @@ int ekh_plan(ekh_planner* P, const int64_t* slot_mapping, int64_t n_rows, ekh_pl
   p.kref_pos = (p.kref_pos + k) % p.W;
   p.kref_fill = std::min<int64_t>(p.W, p.kref_fill + k);
 
-  // The staging image: one contiguous int64 buffer, copied to the device as is.
   p.n_fin = (int64_t)(fin_whole.size() + fin_rest.size()) / w;
+  fin_whole.insert(fin_whole.end(), fin_rest.begin(), fin_rest.end());
+  return EKH_OK;
+}
+
+void commit(Planner& p, int64_t step, const int64_t* touched, int64_t n_touched) {
+  for (int64_t i = 0; i < n_touched; ++i) {
+    const int64_t b = touched[3 * i];
+    p.fill_h[b] = std::max(p.fill_h[b], touched[3 * i + 1]);
+    p.last_h[b] = step;
+    p.cum_h[b] += touched[3 * i + 2];
+  }
+}
+
+}  // namespace ekh
+
+namespace ekh {
+
+int pool_open(Pool& q, const int64_t* blocks, int64_t n, int32_t target_bits, const int64_t* protect,
+              int64_t n_protect, uint8_t* headers, int64_t* victims, int64_t* n_victims) {
+  if (target_bits != 2 && target_bits != 4 && target_bits != 8) return EKH_EINVAL;
+  for (int64_t i = 0; i < n; ++i)
+    if (blocks[i] < 0 || blocks[i] >= q.nb) return EKH_EINVAL;
+  *n_victims = 0;
+  for (int64_t i = 0; i < n; ++i) {  // old chunks go back to the pool
+    const int64_t b = blocks[i];
+    q.settle(b);
+    q.give_back(b);
+    q.set_tag(b, 0);
+  }
+  const int64_t need = (int64_t)kExtra[target_bits] * n;
+  if (need > (int64_t)q.free_chunks.size()) {
+    // Least recently written full INT4 / INT8 blocks, never this step's.
+    std::vector<uint8_t> keep(q.nb, 0);
+    for (int64_t i = 0; i < n; ++i) keep[blocks[i]] = 1;
+    for (int64_t i = 0; i < n_protect; ++i)
+      if (protect[i] >= 0 && protect[i] < q.nb) keep[protect[i]] = 1;
+    std::vector<int64_t> cand;
+    for (int64_t b = 0; b < q.nb; ++b)
+      if (q.tag[b] >= 4 && q.p->fill_h[b] == q.bs && !keep[b]) cand.push_back(b);
+    std::stable_sort(cand.begin(), cand.end(),
+                     [&](int64_t a, int64_t b) { return q.p->last_h[a] < q.p->last_h[b]; });
+    const int64_t short_by = need - (int64_t)q.free_chunks.size();
+    int64_t freed = 0;
+    for (int64_t b : cand) {
+      if (freed >= short_by) break;
+      victims[(*n_victims)++] = b;
+      freed += kExtra[q.tag[b]];
+    }
+    for (int64_t i = 0; i < *n_victims; ++i) {  // requantized to INT2 on the device by the caller
+      const int64_t b = victims[i];
+      q.settle(b);
+      q.give_back(b);
+      q.set_tag(b, 2);
+    }
+    q.demoted += *n_victims;
+  }
+  // Greedy in block order: INT8 while it fits, then INT4, then INT2.
+  std::vector<int32_t> tiers(n, 2);
+  int64_t start = 0;
+  for (int bits : {8, 4}) {
+    if (bits > target_bits) continue;
+    const int ne = kExtra[bits];
+    const int64_t take = std::min<int64_t>(n - start, (int64_t)q.free_chunks.size() / ne);
+    for (int64_t i = start; i < start + take; ++i) {
+      for (int j = 0; j < ne; ++j) {
+        q.table[3 * blocks[i] + j] = q.free_chunks.back();
+        q.free_chunks.pop_back();
+      }
+      tiers[i] = bits;
+    }
+    start += take;
+  }
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t b = blocks[i];
+    q.opened[tiers[i]] += 1;
+    if (tiers[i] < target_bits) q.downgraded += 1;
+    q.set_tag(b, tiers[i]);
+    uint8_t* h = headers + 16 * i;
+    std::memset(h, 0, 16);
+    h[0] = (uint8_t)tiers[i];
+    for (int j = 0; j < 3; ++j) {
+      const int32_t id = (int32_t)q.table[3 * b + j];
+      std::memcpy(h + 4 + 4 * j, &id, 4);
+    }
+  }
+  return EKH_OK;
+}
+
+
+}  // namespace ekh
+
+namespace ekh {
+
+void seal_row(Pool& q, const int64_t* ev, int64_t* row) {
+  // ev = (slot, block, group, fill) -> device row (slot, block, group, fill, bits, mask)
+  const int64_t b = ev[1];
+  q.sealed_groups += 1;
+  const int32_t mask = q.p->sealed[b];
+  row[0] = ev[0];
+  row[1] = b;
+  row[2] = ev[2];
+  row[3] = ev[3];
+  row[4] = q.tag[b] ? q.tag[b] : 2;
+  row[5] = mask ? mask : (1 << ev[2]);
+}
+
+}  // namespace ekh
+
+
+extern "C" {
+
+ekh_planner* ekh_planner_new(int64_t num_blocks, int32_t block_size, int32_t k_group, int32_t residual_slots,
+                             int32_t kref_window) {
+  if (block_size <= 0 || k_group <= 0 || block_size % k_group || block_size / k_group > 8 || residual_slots <= 0 ||
+      kref_window <= 0)
+    return nullptr;
+  ekh_planner* p = new (std::nothrow) ekh_planner();
+  if (!p) return nullptr;
+  p->growable = num_blocks <= 0;
+  if (p->growable) num_blocks = 1;
+  p->nb = num_blocks;
+  p->bs = block_size;
+  p->kg = k_group;
+  p->gpb = block_size / k_group;
+  p->R = residual_slots;
+  p->W = kref_window;
+  for (int32_t s = residual_slots - 1; s >= 0; --s) p->free_stack.push_back(s);
+  p->s_block.assign(residual_slots, -1);
+  p->s_last.assign(residual_slots, 0);
+  p->s_taken.assign(residual_slots, 0);
+  p->s_prot.assign(residual_slots, 0);
+  p->s_group.assign(residual_slots, 0);
+  p->s_fill.assign(residual_slots, 0);
+  p->s_used.assign(residual_slots, 0);
+  p->grp_stamp.assign(residual_slots, 0);
+  p->grp_at.assign(residual_slots, 0);
+  p->block_slot.assign(num_blocks, -1);
+  p->sealed.assign(num_blocks, 0);
+  p->fill_h.assign(num_blocks, 0);
+  p->last_h.assign(num_blocks, 0);
+  p->cum_h.assign(num_blocks, 0);
+  p->res_stamp.assign(num_blocks, 0);
+  p->res_at.assign(num_blocks, 0);
+  return p;
+}
+
+void ekh_planner_free(ekh_planner* p) { delete p; }
+
+int ekh_plan(ekh_planner* P, const int64_t* slot_mapping, int64_t n_rows, ekh_plan_view* out) {
+  if (!P || !out || n_rows < 0 || (n_rows && !slot_mapping)) return EKH_EINVAL;
+  Planner& p = *P;
+  const int rc = ekh::plan_rows(p, slot_mapping, n_rows);
+  if (rc != EKH_OK) return rc;
+  // The staging image: one contiguous int64 buffer, copied to the device as is.
   const int64_t nres = (int64_t)p.res_b.size(), ngrp = (int64_t)p.grp_s.size();
-  p.stage.assign(1 + 4 * n_rows + p.n_fin * w + 2 * nres + 2 * ngrp, 0);
+  p.stage.assign(1 + 4 * n_rows + (int64_t)p.fin.size() + 2 * nres + 2 * ngrp, 0);
   int64_t* o = p.stage.data();
   *o++ = p.n_fin;
-  for (int64_t r = 0; r < n_rows; ++r) *o++ = slot_mapping[r];
-  o = std::copy(tok_res.begin(), tok_res.end(), o);
-  o = std::copy(tok_sealed.begin(), tok_sealed.end(), o);
-  o = std::copy(tok_kref.begin(), tok_kref.end(), o);
-  o = std::copy(fin_whole.begin(), fin_whole.end(), o);
-  o = std::copy(fin_rest.begin(), fin_rest.end(), o);
+  o = std::copy(slot_mapping, slot_mapping + n_rows, o);
+  o = std::copy(p.tok_res.begin(), p.tok_res.end(), o);
+  o = std::copy(p.tok_sealed.begin(), p.tok_sealed.end(), o);
+  o = std::copy(p.tok_kref.begin(), p.tok_kref.end(), o);
+  o = std::copy(p.fin.begin(), p.fin.end(), o);
   o = std::copy(p.res_b.begin(), p.res_b.end(), o);
   o = std::copy(p.res_v.begin(), p.res_v.end(), o);
   o = std::copy(p.grp_s.begin(), p.grp_s.end(), o);
@@ -378,12 +459,7 @@ int ekh_plan(ekh_planner* P, const int64_t* slot_mapping, int64_t n_rows, ekh_pl
 int ekh_commit(ekh_planner* p, int64_t step, const int64_t* touched, int64_t n_touched) {
   for (int64_t i = 0; i < n_touched; ++i)
     if (touched[3 * i] < 0 || touched[3 * i] >= p->nb) return EKH_EINVAL;
-  for (int64_t i = 0; i < n_touched; ++i) {
-    const int64_t b = touched[3 * i];
-    p->fill_h[b] = std::max(p->fill_h[b], touched[3 * i + 1]);
-    p->last_h[b] = step;
-    p->cum_h[b] += touched[3 * i + 2];
-  }
+  ekh::commit(*p, step, touched, n_touched);
   return EKH_OK;
 }
 
@@ -433,6 +509,7 @@ ekh_pool* ekh_pool_new(ekh_planner* planner, int32_t chunks_per_page) {
     for (int slot = chunks_per_page - 1; slot >= 1; --slot) q->free_chunks.push_back(page * chunks_per_page + slot);
   q->pool_size = (int64_t)q->free_chunks.size();
   q->tag.assign(q->nb, 0);
+  q->live[0] = q->nb;
   q->table.assign(3 * q->nb, 0);
   q->mark = planner->cum_h;
   return q;
@@ -443,88 +520,12 @@ void ekh_pool_free(ekh_pool* q) { delete q; }
 int ekh_pool_open(ekh_pool* Q, const int64_t* blocks, int64_t n, int32_t target_bits, const int64_t* protect,
                   int64_t n_protect, uint8_t* headers, int64_t* victims, int64_t* n_victims) {
   if (!Q || n < 0 || (n && (!blocks || !headers)) || !victims || !n_victims) return EKH_EINVAL;
-  if (target_bits != 2 && target_bits != 4 && target_bits != 8) return EKH_EINVAL;
-  Pool& q = *Q;
-  for (int64_t i = 0; i < n; ++i)
-    if (blocks[i] < 0 || blocks[i] >= q.nb) return EKH_EINVAL;
-  *n_victims = 0;
-  for (int64_t i = 0; i < n; ++i) {  // old chunks go back to the pool
-    const int64_t b = blocks[i];
-    q.settle(b);
-    q.give_back(b);
-    q.tag[b] = 0;
-  }
-  const int64_t need = (int64_t)kExtra[target_bits] * n;
-  if (need > (int64_t)q.free_chunks.size()) {
-    // Least recently written full INT4 / INT8 blocks, never this step's.
-    std::vector<uint8_t> keep(q.nb, 0);
-    for (int64_t i = 0; i < n; ++i) keep[blocks[i]] = 1;
-    for (int64_t i = 0; i < n_protect; ++i)
-      if (protect[i] >= 0 && protect[i] < q.nb) keep[protect[i]] = 1;
-    std::vector<int64_t> cand;
-    for (int64_t b = 0; b < q.nb; ++b)
-      if (q.tag[b] >= 4 && q.p->fill_h[b] == q.bs && !keep[b]) cand.push_back(b);
-    std::stable_sort(cand.begin(), cand.end(),
-                     [&](int64_t a, int64_t b) { return q.p->last_h[a] < q.p->last_h[b]; });
-    const int64_t short_by = need - (int64_t)q.free_chunks.size();
-    int64_t freed = 0;
-    for (int64_t b : cand) {
-      if (freed >= short_by) break;
-      victims[(*n_victims)++] = b;
-      freed += kExtra[q.tag[b]];
-    }
-    for (int64_t i = 0; i < *n_victims; ++i) {  // requantized to INT2 on the device by the caller
-      const int64_t b = victims[i];
-      q.settle(b);
-      q.give_back(b);
-      q.tag[b] = 2;
-    }
-    q.demoted += *n_victims;
-  }
-  // Greedy in block order: INT8 while it fits, then INT4, then INT2.
-  std::vector<int32_t> tiers(n, 2);
-  int64_t start = 0;
-  for (int bits : {8, 4}) {
-    if (bits > target_bits) continue;
-    const int ne = kExtra[bits];
-    const int64_t take = std::min<int64_t>(n - start, (int64_t)q.free_chunks.size() / ne);
-    for (int64_t i = start; i < start + take; ++i) {
-      for (int j = 0; j < ne; ++j) {
-        q.table[3 * blocks[i] + j] = q.free_chunks.back();
-        q.free_chunks.pop_back();
-      }
-      tiers[i] = bits;
-    }
-    start += take;
-  }
-  for (int64_t i = 0; i < n; ++i) {
-    const int64_t b = blocks[i];
-    q.opened[tiers[i]] += 1;
-    if (tiers[i] < target_bits) q.downgraded += 1;
-    q.tag[b] = tiers[i];
-    uint8_t* h = headers + 16 * i;
-    std::memset(h, 0, 16);
-    h[0] = (uint8_t)tiers[i];
-    for (int j = 0; j < 3; ++j) {
-      const int32_t id = (int32_t)q.table[3 * b + j];
-      std::memcpy(h + 4 + 4 * j, &id, 4);
-    }
-  }
-  return EKH_OK;
+  return ekh::pool_open(*Q, blocks, n, target_bits, protect, n_protect, headers, victims, n_victims);
 }
 
 int64_t ekh_pool_seal_row(ekh_pool* q, const int64_t* ev, int64_t* row) {
-  // ev = (slot, block, group, fill) -> device row (slot, block, group, fill, bits, mask)
-  const int64_t b = ev[1];
-  if (b < 0 || b >= q->nb) return EKH_EINVAL;
-  q->sealed_groups += 1;
-  const int32_t mask = q->p->sealed[b];
-  row[0] = ev[0];
-  row[1] = b;
-  row[2] = ev[2];
-  row[3] = ev[3];
-  row[4] = q->tag[b] ? q->tag[b] : 2;
-  row[5] = mask ? mask : (1 << ev[2]);
+  if (ev[1] < 0 || ev[1] >= q->nb) return EKH_EINVAL;
+  ekh::seal_row(*q, ev, row);
   return EKH_OK;
 }
 
@@ -549,6 +550,8 @@ void ekh_pool_reset_counters(ekh_pool* q) {
 }
 
 int64_t* ekh_pool_tags(ekh_pool* q) { return q->tag.data(); }
+
+void ekh_pool_live(const ekh_pool* q, int64_t* out) { std::copy(q->live, q->live + 9, out); }
 
 int64_t ekh_pool_free_list(const ekh_pool* q, int64_t* out, int64_t cap) {
   const int64_t n = (int64_t)q->free_chunks.size();

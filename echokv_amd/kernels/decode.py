@@ -36,6 +36,16 @@ def default_splits(block_table: torch.Tensor, block_size: int, blocks_per_split:
     return max(1, min(-(-max_blocks // blocks_per_split), MAX_SPLITS))
 
 
+def workspace_rows(store, num_q_heads: int, q_dtype: torch.dtype, num_seqs: int, num_splits: int,
+                   flags: int) -> int:
+    """Rows of ``(acc [rows, Hq, D], ml [rows, Hq, 2])`` a decode call with these arguments uses."""
+    rows = _lib.lib().echokv_decode_workspace_rows(_lib.byref(store.abi), num_q_heads, _lib.DTYPES[q_dtype],
+                                                   num_seqs, num_splits, flags)
+    if rows < 0:
+        raise ValueError("decode arguments the kernels do not take")
+    return int(rows)
+
+
 def decode_attention(
     store,
     query: torch.Tensor,
@@ -50,7 +60,7 @@ def decode_attention(
     num_splits: int | None = None,
     workspace: tuple[torch.Tensor, torch.Tensor] | str | None = None,
     tier: int | None = None,
-    batch_invariant: bool = False,
+    batch_invariant: bool = True,
 ) -> torch.Tensor:
     """Attention of one query token per sequence over each sequence's cache.
 
@@ -59,15 +69,17 @@ def decode_attention(
     included). Without ``out`` returns float32 ``[S, Hq, D]``; with ``out``
     writes sequence ``i`` to ``out[q_rows[i]]`` in ``out``'s dtype; length-0
     sequences (graph padding) leave their row untouched. ``workspace`` =
-    caller-owned ``(acc [S, Hq, splits, D], ml [S, Hq, splits, 2])`` float32, or
-    ``"static"``: the library's static scratch (no allocation at all, for code under
-    graph capture; at most 64 MiB of workspace, and calls on one GPU must not overlap).
-    ``tier`` selects the kernel specialised for the layer's tier (the backend passes
-    the layer controller's tier); by default the store's most common opened tier.
-    Blocks of other tiers are read correctly either way. By default the batch's
-    blocks are spread evenly over every workgroup the GPU holds (a sequence's result
-    then depends on the rest of the batch only through float rounding);
-    ``batch_invariant`` splits each sequence by its own length instead.
+    caller-owned ``(acc, ml)`` float32 holding ``workspace_rows(...)`` rows of ``Hq * D``
+    and ``Hq * 2`` values (``S * splits`` rows at most), or ``"static"``: the
+    library's static scratch (no allocation at all, for code under graph capture; at
+    most 64 MiB of workspace, and calls on one GPU must not overlap).
+    ``tier`` selects the kernel specialised for that tier; by default the tier most
+    of the store's blocks are stored at. Blocks of other tiers are read correctly
+    either way. With ``batch_invariant`` (the default, as the reference's decode) each
+    sequence is split by its own length, so its result does not depend on the rest
+    of the batch; ``batch_invariant=False`` spreads the batch's blocks evenly over
+    every workgroup the GPU holds instead (faster on uneven batches; a sequence's
+    result then depends on the rest of the batch through float rounding).
     """
     L = store.layout
     dev = query.device
@@ -92,13 +104,16 @@ def decode_attention(
         if workspace != "static":
             raise ValueError(f"workspace must be a (acc, ml) pair or 'static', got {workspace!r}")
         acc = ml = None
-    elif workspace is None:
-        acc = torch.empty(s, hq, num_splits, d, device=dev, dtype=torch.float32)
-        ml = torch.empty(s, hq, num_splits, 2, device=dev, dtype=torch.float32)
     else:
-        acc, ml = workspace
-        if acc.numel() < s * hq * num_splits * d or ml.numel() < s * hq * num_splits * 2:
-            raise ValueError("decode workspace is too small for this batch and split grid")
+        flags = _lib.DECODE_BATCH_INVARIANT if batch_invariant else 0
+        rows = workspace_rows(store, hq, query.dtype, s, num_splits, flags)
+        if workspace is None:
+            acc = torch.empty(rows, hq, d, device=dev, dtype=torch.float32)
+            ml = torch.empty(rows, hq, 2, device=dev, dtype=torch.float32)
+        else:
+            acc, ml = workspace
+            if acc.numel() < rows * hq * d or ml.numel() < rows * hq * 2:
+                raise ValueError(f"decode workspace holds fewer than the {rows} rows this call needs")
     if tier is None:
         tier = store.pool.majority_tier()
     res = _lib.residual(store.res_k)

@@ -28,6 +28,7 @@ from dataclasses import dataclass
 
 import numpy as np
 import torch
+from torch.profiler import record_function
 
 from echokv_amd import _host, _lib
 from echokv_amd._util import to_device
@@ -233,11 +234,17 @@ class ChunkPool:
             raise ValueError(f"eviction of block {ev.block} is outside this pool")
         return row.tolist()
 
+    def live_tiers(self) -> dict:
+        """Blocks stored at each tier now (kept by the pool as blocks open and demote)."""
+        out = np.zeros(9, np.int64)
+        _host.lib().ekh_pool_live(self._h, _host.i64p(out))
+        return {b: int(out[b]) for b in SUPPORTED_BITS}
+
     def majority_tier(self) -> int:
         """The tier most of the opened blocks are stored at (4 when nothing is open)."""
-        counts = np.bincount(self.tag_h, minlength=9)
-        best = max(SUPPORTED_BITS, key=lambda b: (counts[b], b == 4))
-        return best if counts[best] else 4
+        live = self.live_tiers()
+        best = max(SUPPORTED_BITS, key=lambda b: (live[b], b == 4))
+        return best if live[best] else 4
 
     def fresh_opens(self, plan: WritePlan) -> np.ndarray:
         """Blocks to open this step: offset-0 writes plus writes into never-opened blocks."""
@@ -396,9 +403,17 @@ class TieredKVCache:
                   _lib.ptr(k), _lib.ptr(v), 2, _lib.stream())
 
     def _seal_rows(self, rows: list) -> None:
-        ev = to_device(torch.tensor(rows, dtype=torch.int64).reshape(-1, 6), self.device)
+        self.seal_groups(to_device(torch.tensor(rows, dtype=torch.int64).reshape(-1, 6), self.device))
+
+    def seal_groups(self, rows: torch.Tensor) -> None:
+        """Seal evicted residual groups: ``rows`` int64 ``[n, 6]`` on the device, as
+        ``ChunkPool.seal_row`` makes them (``tiered_cache.py:379-394``)."""
+        if rows.dtype != torch.int64 or rows.dim() != 2 or rows.shape[1] != 6 or rows.stride(1) != 1:
+            raise ValueError("seal rows must be int64 [n, 6] with contiguous rows")
+        if rows.shape[0] == 0:
+            return
         res = _lib.residual(self.res_k)
-        _lib.call("echokv_seal_groups", _lib.byref(self.abi), _lib.ptr(self.pages), _lib.ptr(ev), ev.shape[0],
+        _lib.call("echokv_seal_groups", _lib.byref(self.abi), _lib.ptr(self.pages), _lib.ptr(rows), rows.shape[0],
                   _lib.byref(res), _lib.stream())
 
     def _seal(self, ev: Eviction) -> None:
@@ -422,13 +437,18 @@ class TieredKVCache:
         grids masked by the device counts, as a replayed graph needs."""
         from echokv_amd.kernels.write import FUSED_MAX_K_GROUP, finalize_k, write_step, write_tokens
 
+        # The reference's scopes (tiered_cache.py:428,431): one launch here does the
+        # work of both, so it is recorded under both names, nested.
         if self.layout.k_group <= FUSED_MAX_K_GROUP:
-            write_step(self, key, value, meta, kref, full_grid=capturing)
+            with record_function("echokv.write.k_finalize"), record_function("echokv.write.tokens"):
+                write_step(self, key, value, meta, kref, full_grid=capturing)
             return
         if capturing or meta.n_fin:
-            finalize_k(self, key, meta, full_grid=capturing)
+            with record_function("echokv.write.k_finalize"):
+                finalize_k(self, key, meta, full_grid=capturing)
         if meta.n_rows:
-            write_tokens(self, key, value, meta, kref)
+            with record_function("echokv.write.tokens"):
+                write_tokens(self, key, value, meta, kref)
 
     def write(self, key: torch.Tensor, value: torch.Tensor, slots: torch.Tensor, target_bits: int,
               kref: torch.Tensor | None = None) -> None:

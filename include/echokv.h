@@ -128,8 +128,9 @@ int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* b
 
 /* Paged decode attention: sequence i attends with query row q_rows[i] (NULL = i)
  * over block-table row bt_rows[i] (NULL = i) for seq_lens[i] tokens and writes
- * out[q_rows[i]]; seq_lens[i] == 0 leaves the row untouched. acc:
- * [num_seqs, Hq, num_splits, D] f32, ml: [num_seqs, Hq, num_splits, 2] f32 workspaces.
+ * out[q_rows[i]]; seq_lens[i] == 0 leaves the row untouched. acc: [rows, Hq, D]
+ * f32 and ml: [rows, Hq, 2] f32 workspaces, rows = echokv_decode_workspace_rows(...)
+ * of the same arguments (at most num_seqs * num_splits).
  * Default schedule: the batch's blocks are cut into equal ranges, one per workgroup
  * the chip holds (at most num_seqs * num_splits / 2); a sequence inside one range is
  * written directly, the others merged from partials. With flags &
@@ -152,6 +153,14 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
                   float softmax_scale, int32_t num_splits, int32_t blocks_per_split, int32_t tier,
                   int32_t flags, float* acc, float* ml, void* out, int64_t o_s0, int64_t o_s1,
                   int32_t out_dtype, echokv_stream_t stream);
+
+/* Rows of the acc / ml workspaces that echokv_decode uses with these arguments,
+ * for any tier: num_seqs * num_splits for the split schedule, two per range of the
+ * balanced one (ranges follow the kernels' occupancy on the current device). -1
+ * for arguments echokv_decode would refuse. No counterpart in the reference: its
+ * launcher allocates [S, Hq, splits, D] per call (echokv_vllm/kernels/decode.py:306-307). */
+int64_t echokv_decode_workspace_rows(const echokv_layout* L, int32_t num_q_heads, int32_t q_dtype,
+                                     int64_t num_seqs, int32_t num_splits, int32_t flags);
 
 /* echokv_decode without workspace arguments, for callers that cannot allocate
  * (code under HIP-graph capture, serving loops that forbid allocation): acc and

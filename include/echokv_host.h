@@ -97,6 +97,71 @@ void ekh_pool_reset_counters(ekh_pool* q);
 int64_t* ekh_pool_tags(ekh_pool* q);
 /* The chunk free list, bottom to top; returns its length. */
 int64_t ekh_pool_free_list(const ekh_pool* q, int64_t* out, int64_t cap);
+/* Blocks stored at each tier now, out[9] (index 0: never opened). */
+void ekh_pool_live(const ekh_pool* q, int64_t* out);
+
+/* ---- per-step driver of a KV-cache group ------------------------------------ */
+
+/* One engine step's batch, as vLLM's CommonAttentionMetadata gives it. */
+typedef struct ekh_batch {
+  int64_t num_reqs, num_tokens;
+  const int32_t* query_start;  /* [num_reqs + 1] */
+  const int32_t* seq_lens;     /* [num_reqs], the step's tokens included */
+  const int64_t* slot_mapping; /* [num_tokens], -1 = no write */
+} ekh_batch;
+
+/* Where each part of a step image sits (int64 words from its start) and how
+ * much of it the step uses. The image:
+ *   [0] fin rows, [1] token rows;
+ *   canary rows [canary_slots] at o_canary;
+ *   decode query rows, block-table rows, lengths (rows_dec each) at o_dec;
+ *   token rows: slot, residual slot, sealed, K_ref row (rows_tok each) at o_tok;
+ *   fin rows [rows_fin, 3 + k_group] at o_fin;
+ *   residual map: blocks, values (n_res each) at o_res;
+ *   residual groups: slots, groups (n_grp each) at o_grp;
+ *   opened block ids [n_open] at o_open;
+ *   page headers [layers, n_open, 16 bytes] at o_hdr;
+ *   seal rows [layers, n_seal, 6] at o_seal (the rows ekh_pool_seal_row makes).
+ * For a step of at most `cap` decode entries, token rows and fin rows
+ * (graph_rows = 1) rows_* equal the capacity, so everything up to o_res sits at
+ * fixed offsets. */
+typedef struct ekh_step_view {
+  int64_t step, len, o_canary, o_dec, o_tok, o_fin, o_res, o_grp, o_open, o_hdr, o_seal;
+  int64_t rows_dec, rows_tok, rows_fin;
+  int64_t n_dec, n_tokens, n_fin, n_res, n_grp, n_open, n_seal, n_canary, decode_only, graph_rows;
+  double canary_ctx;          /* mean context of the canary's requests */
+  int64_t n_prefill;
+  const int64_t* prefill;     /* [n_prefill, 4]: query start, query end, context, request */
+  int64_t n_victims;
+  const int64_t* victims;     /* [n_victims, 2]: layer, block -- requantize to INT2 before the headers */
+  const int64_t* image;       /* the caller's buffer, or the stepper's own when it was too small */
+} ekh_step_view;
+
+typedef struct ekh_stepper ekh_stepper;
+
+/* A driver over a planner and its layers' pools (all built on that planner);
+ * `cap`: the graph capacity in rows, `canary_slots`: query rows a fire stashes. */
+ekh_stepper* ekh_stepper_new(ekh_planner* planner, ekh_pool* const* pools, int32_t n_layers, int64_t cap,
+                             int32_t canary_slots);
+void ekh_stepper_free(ekh_stepper* s);
+
+/* Plan one step for every layer and write its image into `image` (or the
+ * stepper's own buffer when image_cap is too small). tiers[layer]: the tier
+ * blocks opened now take in that layer; fire: take the canary rows this step.
+ * Replaces the host side of echokv_vllm/backend.py:337-496 (the builder's
+ * batch layout, _plan and _Staging's image) and write_plan.py:98-240. */
+int ekh_stepper_run(ekh_stepper* s, const ekh_batch* batch, const int32_t* tiers, int32_t fire, int64_t* image,
+                    int64_t image_cap, ekh_step_view* out);
+
+/* vLLM's slot mapping computed on the host from a host copy of the block table
+ * ([table_rows, table_cols] int32, row stride table_stride) and the host
+ * sequence lengths: slot = table[row][pos / bs] * bs + pos % bs, where row is
+ * the batch row or row_map[batch row]; rows past the scheduled tokens get -1.
+ * EKH_EINVAL when the host copies cannot stand in for the device mapping.
+ * Replaces echokv_vllm/host_slots.py:170-195 (host_lens_and_slots). */
+int ekh_host_slots(const ekh_batch* batch, const int32_t* table, int64_t table_rows, int64_t table_cols,
+                   int64_t table_stride, const int64_t* row_map, int64_t row_map_len, int32_t block_size,
+                   int64_t* slots);
 
 #ifdef __cplusplus
 }

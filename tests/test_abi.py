@@ -32,7 +32,18 @@ def test_every_declared_symbol_is_exported(lib):
     for n in names:
         assert hasattr(lib, n), n
     assert set(names) == set(_lib.EXPORTS)
-    assert set(_lib._SIGS) == set(names) - {"echokv_error_string", "echokv_prefill_dense_workspace"}
+    assert set(_lib._SIGS) == set(names) - {"echokv_error_string", "echokv_prefill_dense_workspace",
+                                            "echokv_decode_workspace_rows"}
+
+
+def test_decode_workspace_rows_of_the_split_schedule(lib):
+    # The split schedule needs no device query: num_seqs * num_splits rows.
+    L = _layout()
+    assert lib.echokv_decode_workspace_rows(C.byref(L), 32, _lib.F16, 7, 5, _lib.DECODE_BATCH_INVARIANT) == 35
+    assert lib.echokv_decode_workspace_rows(C.byref(L), 32, _lib.F16, 0, 5, 0) == 0
+    assert lib.echokv_decode_workspace_rows(C.byref(L), 30, _lib.F16, 7, 5, 1) == -1  # GQA not whole
+    assert lib.echokv_decode_workspace_rows(C.byref(L), 32, 9, 7, 5, 1) == -1  # dtype
+    assert lib.echokv_decode_workspace_rows(C.byref(L), 32, _lib.F16, 7, 0, 1) == -1  # no splits
 
 
 def test_error_strings(lib):

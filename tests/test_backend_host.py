@@ -2,7 +2,7 @@
 block tables (the scenarios of tests/echokv_vllm/test_host_slots.py:24-135),
 the backend's answers to vLLM (backend.py:72-118), the implementation's
 refusals (backend.py:499-524), the control API (control.py:39-117), the
-per-step metadata image, and plugin registration gating."""
+reference's module path and entry point, and plugin registration gating."""
 
 from dataclasses import dataclass, replace
 from types import SimpleNamespace
@@ -13,8 +13,9 @@ import torch
 
 from echokv_amd import control, host_slots, plugin
 from echokv_amd._vllm import AttentionCGSupport, MultipleOf
-from echokv_amd.backend import EchoKVAttentionBackend, EchoKVAttentionImpl, EchoKVMetadataBuilder, StepImage
-from echokv_amd.host_slots import host_lens_and_slots, install_v1_dummy, install_v2, is_dummy_step
+from echokv_amd.backend import CanaryClock, EchoKVAttentionBackend, EchoKVAttentionImpl, EchoKVMetadataBuilder
+from echokv_amd.config import load_config
+from echokv_amd.host_slots import host_lens_and_slots, install_v1, install_v1_dummy, install_v2, is_dummy_step
 from echokv_amd.tiered_cache import TieredLayout
 
 BS = 16
@@ -113,7 +114,8 @@ def test_v1_registry_lookup_and_dummy_depth():
             self.block_table = SimpleNamespace(gpu=torch.zeros(2, 4, dtype=torch.int32),
                                                np=np.array([[3, 8, 0, 0], [5, 0, 0, 0]]))
 
-    host_slots._track_instances(Table, host_slots.REG.v1)
+    install_v1(Table)
+    install_v1(Table)  # idempotent
     t = Table()
     cm = cm_of(t.block_table.gpu, [0, 1, 3], [18, 2], 3)
     _, slots = host_lens_and_slots(cm, BS)
@@ -126,7 +128,7 @@ def test_v1_registry_lookup_and_dummy_depth():
 
     install_v1_dummy(Runner)
     assert Runner()._dummy_run(lambda: (is_dummy_step(cm), host_lens_and_slots(cm, BS))) == (True, None)
-    assert host_slots.REG.v1_dummy_depth == 0
+    assert host_slots.REGISTRY.v1_dummy_runs == 0
 
 
 def test_v2_dummy_steps_use_the_device_copy():
@@ -247,31 +249,67 @@ def test_control_api_steers_every_layer():
     assert control.reset_counters(m) == 3 and impl.forward_calls == 0
 
 
-# ---- the per-step metadata image -----------------------------------------------------
+# ---- canary schedule --------------------------------------------------------------
 
-def test_step_image_fixed_offsets_and_oversized_steps():
-    img = StepImage(cap=8, nq=3, w=5, tail=40, device="cpu")
-    dec = (np.array([1, 2]), np.array([0, 1]), np.array([10, 0]))
-    tok = np.arange(12).reshape(4, 3)
-    fin = np.arange(10).reshape(2, 5)
-    tail = [np.array([7, 8]), np.array([-1, 3])]
-    cnt, can, d, tk, fn, views = img.upload(2, np.array([4, 5, 6]), dec, tok, fin, tail)
-    assert int(cnt) == 2 and can.tolist() == [4, 5, 6]
-    assert [x.tolist() for x in d] == [[1, 2], [0, 1], [10, 0]]
-    assert tk.tolist() == tok.tolist() and tk.stride(0) == 8  # rows stride by the capacity
-    assert fn.shape == (8, 5) and fn[:2].tolist() == fin.tolist()
-    assert [v.tolist() for v in views] == [[7, 8], [-1, 3]]
-    first = tk.data_ptr()
-    _, _, _, tk2, _, _ = img.upload(0, np.zeros(3, np.int64), dec, tok, np.zeros((0, 5), np.int64), [])
-    assert tk2.data_ptr() == first  # the same addresses every step a graph replays
-    big = np.arange(40).reshape(4, 10)  # 10 rows > capacity: a buffer of its own
-    _, _, _, tk3, fn3, _ = img.upload(1, np.zeros(3, np.int64), dec, big, np.ones((1, 5), np.int64), [])
-    assert tk3.tolist() == big.tolist() and fn3.shape == (1, 5) and tk3.data_ptr() != first
+def test_canary_clock_fires_on_the_interval_and_waits_for_a_live_request():
+    clock = CanaryClock(interval=3)
+    armed = [clock.tick(dummy=False) for _ in range(3)]
+    assert armed == [False, False, True]
+    clock.fired(0, 0.0)  # no live request on the armed step: stays armed
+    assert clock.tick(dummy=True) and clock.steps == 3  # dummy steps do not count
+    clock.fired(2, 100.0)
+    assert not clock.armed and clock.stashed == (2, 100.0)
+    assert [clock.tick(dummy=False) for _ in range(3)] == [False, False, True]
+
+
+# ---- the reference's module path -------------------------------------------------------
+
+def test_reference_module_path_is_this_package():
+    import importlib
+
+    import echokv_amd.backend
+    import echokv_amd.kernels.decode
+    from echokv_vllm import control as ref_control
+    from echokv_vllm.kernels import decode as ref_decode
+
+    assert ref_control is control and ref_decode is echokv_amd.kernels.decode
+    mod, cls = plugin.BACKEND_PATH.rsplit(".", 1)
+    assert mod == "echokv_vllm.backend" and importlib.import_module(mod) is echokv_amd.backend
+    assert getattr(importlib.import_module(mod), cls) is EchoKVAttentionBackend
+    try:
+        import tomllib
+    except ImportError:  # Python 3.10
+        import tomli as tomllib
+    from pathlib import Path
+
+    meta = tomllib.loads((Path(__file__).resolve().parents[1] / "pyproject.toml").read_text())
+    assert meta["project"]["entry-points"]["vllm.general_plugins"] == {"echokv": "echokv_vllm.plugin:register"}
+
+
+# ---- V groups ----------------------------------------------------------------------------
+
+def test_v_groups_the_kernels_do_not_store_are_refused_up_front(monkeypatch):
+    for vg in ("4", "16", "64", "128"):
+        monkeypatch.setenv("ECHOKV_V_GROUP", vg)
+        assert load_config().v_group == int(vg)
+    monkeypatch.setenv("ECHOKV_V_GROUP", "32")
+    assert EchoKVAttentionBackend.supports_head_size(96)
+    for vg in ("24", "6", "2", "512"):
+        monkeypatch.setenv("ECHOKV_V_GROUP", vg)
+        with pytest.raises(ValueError, match="ECHOKV_V_GROUP"):
+            load_config()
+        with pytest.raises(ValueError, match="ECHOKV_V_GROUP"):
+            EchoKVAttentionBackend.supports_head_size(96)
+
+
+def test_batch_invariant_is_the_default_and_can_be_turned_off(monkeypatch):
+    monkeypatch.delenv("ECHOKV_BATCH_INVARIANT", raising=False)
+    assert load_config().batch_invariant
+    monkeypatch.setenv("ECHOKV_BATCH_INVARIANT", "0")
+    assert not load_config().batch_invariant
 
 
 def test_register_is_gated_by_echokv_enable(monkeypatch):
     monkeypatch.delenv("ECHOKV_ENABLE", raising=False)
     plugin.register()  # disabled: returns before importing vLLM
-    assert plugin.BACKEND_PATH == "echokv_amd.backend.EchoKVAttentionBackend"
-    mod, cls = plugin.BACKEND_PATH.rsplit(".", 1)
-    assert getattr(__import__(mod, fromlist=[cls]), cls) is EchoKVAttentionBackend
+    assert plugin.BACKEND_PATH == "echokv_vllm.backend.EchoKVAttentionBackend"

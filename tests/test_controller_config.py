@@ -105,7 +105,7 @@ def test_bad_values_raise_value_error_naming_the_variable(env, name):
 
 def test_every_variable_has_one_row():
     envs = [s.env for s in SETTINGS]
-    assert len(envs) == len(set(envs)) == 15
+    assert len(envs) == len(set(envs)) == 16
 
 
 # ---- canary.py:19-56 -----------------------------------------------------------------

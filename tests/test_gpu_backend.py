@@ -82,7 +82,7 @@ class CanaryCheck:
             return
         torch.cuda.synchronize()
         pl = self.builder.shared.planner
-        k = self.builder.measured[0]
+        k = self.builder.canary.stashed[0]
         self.snap = []
         for l in self.layers:
             ring = l.impl.kref_buf.cpu().numpy()
@@ -90,9 +90,9 @@ class CanaryCheck:
             self.snap.append((l.impl.stash[:k].float().cpu().numpy(), ring[order]))
 
     def after_build(self):
-        if self.snap is None or self.builder.pending is None:
+        if self.snap is None or self.builder.canary.scored is None:
             return
-        deltas = self.builder.pending[0].cpu().numpy()
+        deltas = self.builder.canary.scored[0].cpu().numpy()
         for li, (q, ring) in enumerate(self.snap):
             ref = OC.canary_kl(q, ring, SUPPORTED_BITS, KG, D ** -0.5)
             np.testing.assert_allclose(deltas[li], ref, rtol=2e-3, atol=2e-6)
@@ -163,7 +163,7 @@ def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
     starts = np.concatenate([[0], np.cumsum(PROMPTS)])
     slots = slots_for(table_np, [0] * nreq, PROMPTS)
     md = builder.build(0, Batch(device, table, starts, PROMPTS, slots, int(starts[-1])))
-    assert md.prefill and md.prefill_dense is not None and md.decode_rows is None
+    assert md.prefill is not None and md.prefill.dense is not None and md.decode is None
     q, k, v = rand(int(starts[-1]), HQ), rand(int(starts[-1]), H), rand(int(starts[-1]), H)
     outs = run_layers(layers, md, q, k, v)
     torch.cuda.synchronize()
@@ -172,10 +172,10 @@ def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
         ps = oracle_of(layer.impl)
         if env:  # own-group-exact prefill: each query's own K group from this step's keys
             ref = OA.prefill_own_group_exact(ps, q[li].float().cpu().numpy(), k[li].float().cpu().numpy(),
-                                             md.prefill, md.prefill_reqs, table_np, D ** -0.5)
+                                             md.prefill.entries, md.prefill.reqs, table_np, D ** -0.5)
         else:
-            ref = OA.prefill_attention(ps, q[li].float().cpu().numpy(), md.prefill, md.prefill_reqs, table_np,
-                                       D ** -0.5, vectorized=True)
+            ref = OA.prefill_attention(ps, q[li].float().cpu().numpy(), md.prefill.entries, md.prefill.reqs,
+                                       table_np, D ** -0.5, vectorized=True)
         worst = max(worst, maxdiff(outs[li].view(-1, HQ, D), ref))
         assert int(layer.impl.store.tag[table_np[1, 0]]) == layer.impl.controller.bits
     print(f"[backend prefill{' own-group' if env else ''}] max err {worst:.3e}", flush=True)
@@ -201,7 +201,7 @@ def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
         cm, new_lens = decode_batch()
         md = builder.build(0, cm)
         canary.after_build()
-        assert md.decode_rows is not None and md.decode_lens.shape[0] == pad and not md.prefill
+        assert md.decode is not None and md.decode.lens.shape[0] == pad and md.prefill is None
         q, k, v = rand(pad, HQ), rand(pad, H), rand(pad, H)
         outs = run_layers(layers, md, q, k, v)
         torch.cuda.synchronize()
@@ -239,3 +239,39 @@ def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
     assert all(l.impl.controller.fires >= 1 for l in layers), "every controller observed a δ̂"
     for layer in layers:
         assert layer.impl.forward_calls == 4  # prefill, 2 eager decodes, the captured call; replays stay in the graph
+
+
+def test_a_request_decodes_the_same_alone_and_in_a_batch(device, monkeypatch):
+    """The default decode schedule is batch-invariant, as the reference's
+    (docs/ECHOKV_VLLM_PLUGIN.md:118, decode.py:66-70): a request's output does not
+    depend on which other requests share its step, to the bit."""
+    for k, v in {"ECHOKV_K_GROUP": "16", "ECHOKV_MEM_BITS": "8", "ECHOKV_RESIDUAL_SLOTS": "24"}.items():
+        monkeypatch.setenv(k, v)
+    monkeypatch.delenv("ECHOKV_BATCH_INVARIANT", raising=False)
+    rng = np.random.default_rng(3)
+    nreq = len(PROMPTS)
+    table_np = rng.permutation(128)[: nreq * 32].reshape(nreq, 32).astype(np.int64)
+    table = torch.from_numpy(table_np).to(device, torch.int32)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(9)
+    total = sum(PROMPTS)
+    pre = [[torch.randn(total, h, D, device=device, generator=gen).half() for _ in range(LAYERS)] for h in (HQ, H, H)]
+    step = [[torch.randn(nreq, h, D, device=device, generator=gen).half() for _ in range(LAYERS)] for h in (HQ, H, H)]
+    starts = np.concatenate([[0], np.cumsum(PROMPTS)])
+    outs = {}
+    for who in ("batch", "alone"):
+        builder, layers, _ = make_engine(device, tiers=[4, 8, 2])
+        md = builder.build(0, Batch(device, table, starts, PROMPTS, slots_for(table_np, [0] * nreq, PROMPTS), total))
+        run_layers(layers, md, *pre)
+        reqs = list(range(nreq)) if who == "batch" else [1]
+        lens = [PROMPTS[r] + 1 for r in reqs]
+        slots = np.concatenate([slots_for(table_np[r : r + 1], [PROMPTS[r]], [1]) for r in reqs])
+        bt = table[reqs].contiguous()
+        md = builder.build(0, Batch(device, bt, np.arange(len(reqs) + 1), lens, slots, len(reqs)))
+        assert md.decode is not None and md.decode.batch_invariant
+        outs[who] = run_layers(layers, md, *[[x[li][reqs] for li in range(LAYERS)] for x in step])
+    torch.cuda.synchronize()
+    for li in range(LAYERS):
+        assert torch.equal(outs["batch"][li][1], outs["alone"][li][0]), f"layer {li}"
+    print("[backend] request 1 decodes bit-identically alone and in a batch of 4", flush=True)
+    _vllm.set_forward_metadata(None)
