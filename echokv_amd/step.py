@@ -19,6 +19,7 @@ slot is rewritten only once the copy that read it has completed.
 from __future__ import annotations
 
 import ctypes as C
+import time
 from dataclasses import dataclass
 
 import numpy as np
@@ -76,6 +77,7 @@ class StepDriver:
         self.host = [torch.zeros(self.words, dtype=torch.int64, pin_memory=pin) for _ in range(self.RING if pin else 1)]
         self.copied: list = [None] * len(self.host)
         self.turn = 0
+        self.wait_s = 0.0  # host time spent waiting for a ring slot (the host ran RING steps ahead)
         self._view = _host.StepView()
 
     def __del__(self) -> None:
@@ -91,7 +93,9 @@ class StepDriver:
         batch = _host.Batch(n, t, qsl.ctypes.data, lens.ctypes.data, slots.ctypes.data)
         i = self.turn
         if self.copied[i] is not None:
+            t_wait = time.perf_counter()
             self.copied[i].synchronize()  # the copy that read this image RING steps ago
+            self.wait_s += time.perf_counter() - t_wait
         buf = self.host[i]
         v = self._view
         rc = _host.lib().ekh_stepper_run(self._h, C.byref(batch), tiers.ctypes.data, int(fire), buf.data_ptr(),
