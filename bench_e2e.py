@@ -312,11 +312,14 @@ def serve(system, model, dev, prompts: np.ndarray, out_len: int, budget_tokens: 
     running: list = []  # request ids in batch order
     made = np.zeros(n_req, np.int64)  # output tokens so far
     lens = np.zeros(n_req, np.int64)  # tokens in the cache
-    last = torch.zeros(n_req + 1, dtype=torch.int64, device=dev)  # each request's newest token (+1 padding)
+    # Every tensor a captured graph reads or writes outlives every serve() call that
+    # replays it: they live in ``graphs`` (allocated once per system, at the largest size).
+    last = graphs["last"]  # each request's newest token, + one row that graph padding writes
+    if last.numel() < n_req + 1:
+        raise ValueError("graphs['last'] must hold a row per request plus one")
+    last.zero_()
     prompts_d = torch.from_numpy(prompts).to(dev)
-    cap_rows = max(graphs.get("cap", 0), 8)
-    req_buf = graphs.setdefault("req_buf", torch.zeros(cap_rows, dtype=torch.int64, device=dev))
-    pos_buf = graphs.setdefault("pos_buf", torch.zeros(cap_rows, dtype=torch.int64, device=dev))
+    req_buf, pos_buf = graphs["req_buf"], graphs["pos_buf"]
     steps = dict(prefill=0, decode=0, max_running=0, graph_captures=0)
     last_batch = None
     t0 = time.perf_counter()
@@ -347,7 +350,7 @@ def serve(system, model, dev, prompts: np.ndarray, out_len: int, budget_tokens: 
                 b = len(running)
                 rows = -(-b // 8) * 8
                 reqs = running + [None] * (rows - b)
-                req_ids = np.array(running + [n_req] * (rows - b), np.int64)
+                req_ids = np.array(running + [last.numel() - 1] * (rows - b), np.int64)
                 pos_np = np.array([lens[r] for r in running] + [0] * (rows - b), np.int64)
                 system.begin(reqs, [1] * b + [0] * (rows - b), [int(lens[r]) + 1 for r in running] + [0] * (rows - b),
                              rows)
@@ -356,7 +359,7 @@ def serve(system, model, dev, prompts: np.ndarray, out_len: int, budget_tokens: 
                 rows = -(-hi // 8) * 8
                 rows = min(rows, system.slots)
                 by_slot = {system.slot_of[r]: r for r in running}
-                req_ids = np.array([by_slot.get(s, n_req) for s in range(rows)], np.int64)
+                req_ids = np.array([by_slot.get(s, last.numel() - 1) for s in range(rows)], np.int64)
                 pos_np = np.array([lens[by_slot[s]] if s in by_slot else 0 for s in range(rows)], np.int64)
                 system.begin_decode(rows, pos_buf)
             req_buf[:rows].copy_(torch.from_numpy(req_ids), non_blocking=True)
@@ -453,7 +456,10 @@ def run_system(which: str, args) -> dict:
         system = EchoKVSystem(dev, budget, args.block_size, max_len + 64, cap=args.max_seqs, max_seqs=args.max_seqs)
     else:
         system = DenseSystem(dev, budget, max_len)
-    graphs = {"cap": args.max_seqs}
+    rows = max(args.max_seqs, 8) + 8
+    graphs = {"last": torch.zeros(max(args.prompts, args.warm_prompts) + 1, dtype=torch.int64, device=dev),
+              "req_buf": torch.zeros(rows, dtype=torch.int64, device=dev),
+              "pos_buf": torch.zeros(rows, dtype=torch.int64, device=dev)}
     res = {"system": system.name, "kv_capacity_tokens": int(system.capacity_tokens)}
     warm, _ = serve(system, model, dev, prompts[: args.warm_prompts], args.output_len, args.max_tokens,
                     args.max_seqs, graphs, echo)
