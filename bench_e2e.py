@@ -21,9 +21,12 @@ cache differ):
   when its whole footprint (prompt + outputs) fits the KV budget, so nothing is
   ever preempted; admitted prompts are prefilled whole, up to 8192 tokens a step;
   otherwise every running request decodes one token a step;
-* decode steps replay one HIP graph per padded batch size (multiples of 8),
-  captured the first time that size runs, as vLLM's full graphs do. Prefill steps
-  run eagerly.
+* every step is launched eagerly, one kernel at a time, decode steps padded to a
+  multiple of 8 rows (as vLLM pads a graph batch). ``--graphs`` replays each
+  padded decode size from one HIP graph instead, as vLLM's full graphs do; that
+  mode is not measured yet: its first two runs faulted on tensors the captured
+  graphs read after Python had freed them (the step's row index, then each
+  request's newest token); both are fixed in this file and the mode awaits a run.
 
 EchoKV runs through the product path: ``EchoKVMetadataBuilder.build`` once per
 step over fake ``CommonAttentionMetadata`` (with a host block table registered as
@@ -303,8 +306,10 @@ class DenseSystem:
 # ---- the engine ---------------------------------------------------------------------------
 
 def serve(system, model, dev, prompts: np.ndarray, out_len: int, budget_tokens: int, max_seqs: int, graphs: dict,
-          echo: bool) -> dict:
-    """Serve every prompt to ``out_len`` greedy tokens; returns timing and counts."""
+          echo: bool, use_graphs: bool = False) -> dict:
+    """Serve every prompt to ``out_len`` greedy tokens; returns timing and counts.
+    ``use_graphs``: replay decode steps from HIP graphs (one per padded batch size)
+    instead of launching them eagerly."""
     import torch
 
     n_req, plen = prompts.shape
@@ -364,14 +369,17 @@ def serve(system, model, dev, prompts: np.ndarray, out_len: int, budget_tokens: 
                 system.begin_decode(rows, pos_buf)
             req_buf[:rows].copy_(torch.from_numpy(req_ids), non_blocking=True)
             pos_buf[:rows].copy_(torch.from_numpy(pos_np), non_blocking=True)
-            g = graphs.get(rows)
-            if g is None:
+            def run(rows=rows):
+                # The row index is made inside the step: under capture it is a node of
+                # the graph, not a tensor that could be freed before a replay reads it.
                 ar = torch.arange(rows, device=dev)
+                nxt = model.forward(last[req_buf[:rows]], pos_buf[:rows], system.attn, ar)
+                last[req_buf[:rows]] = nxt
 
-                def run(rows=rows, ar=ar):
-                    nxt = model.forward(last[req_buf[:rows]], pos_buf[:rows], system.attn, ar)
-                    last[req_buf[:rows]] = nxt
-
+            g = graphs.get(rows)
+            if not use_graphs:
+                run()
+            elif g is None:
                 run()  # this step, eagerly (also the warm-up of the capture)
                 torch.cuda.synchronize()
                 g = torch.cuda.CUDAGraph()
@@ -462,10 +470,10 @@ def run_system(which: str, args) -> dict:
               "pos_buf": torch.zeros(rows, dtype=torch.int64, device=dev)}
     res = {"system": system.name, "kv_capacity_tokens": int(system.capacity_tokens)}
     warm, _ = serve(system, model, dev, prompts[: args.warm_prompts], args.output_len, args.max_tokens,
-                    args.max_seqs, graphs, echo)
+                    args.max_seqs, graphs, echo, args.graphs)
     log(f"{which}: warm-up {warm}")
     timed, last_batch = serve(system, model, dev, prompts, args.output_len, args.max_tokens, args.max_seqs, graphs,
-                              echo)
+                              echo, args.graphs)
     log(f"{which}: {timed}")
     res.update(timed)
     res["warmup"] = warm
@@ -491,10 +499,13 @@ def main():
     ap.add_argument("--max-tokens", type=int, default=8192, help="prefill tokens per step")
     ap.add_argument("--warm-prompts", type=int, default=16)
     ap.add_argument("--no-layer-times", dest="layer_times", action="store_false")
+    ap.add_argument("--graphs", action="store_true",
+                    help="replay decode steps from HIP graphs (not run on the GPU yet: see the module docstring)")
     args = ap.parse_args()
     os.environ.setdefault("ECHOKV_MEM_BITS", "4")
     out = {"workload": f"cfg5 stand-in: {args.prompts} x ({args.input_len} in, {args.output_len} out), greedy, "
-                       f"{args.kv_gib:g} GiB KV, block {args.block_size}, random-init bf16 Llama-3.1-8B shape",
+                       f"{args.kv_gib:g} GiB KV, block {args.block_size}, random-init bf16 Llama-3.1-8B shape, "
+                       f"decode steps {'graph-replayed' if args.graphs else 'eager'}",
            "echokv_env": {k: v for k, v in os.environ.items() if k.startswith("ECHOKV_")}}
     for which in (("echokv", "dense") if args.system == "both" else (args.system,)):
         out[which] = run_system(which, args)

@@ -41,10 +41,12 @@ def test_cfg1_decode_matches_reference_output(device, name):
     table = t(s.meta["table"], device, torch.int32)
     lens = t(s.meta["lens"], device)
     for bps in (1, 4, 16):
-        got = dec.decode_attention(store, t(q, device), table, lens, s.d ** -0.5, blocks_per_split=bps)
-        torch.cuda.synchronize()
-        err = maxdiff(got, g["decode_out"])
-        assert err <= TOL, f"{name} bps={bps}: max err {err}"
+        for inv in (False, True):
+            got = dec.decode_attention(store, t(q, device), table, lens, s.d ** -0.5, blocks_per_split=bps,
+                                       batch_invariant=inv)
+            torch.cuda.synchronize()
+            err = maxdiff(got, g["decode_out"])
+            assert err <= TOL, f"{name} bps={bps} invariant={inv}: max err {err}"
 
 
 @pytest.mark.parametrize("i", range(len(S.DECODE_CASES)))
@@ -101,10 +103,11 @@ def test_decode_softmax_scale_sign_and_zero(device, case_stores, scale):
         q = rng.standard_normal((len(s.meta["lens"]), 4 * s.h, s.d), dtype=np.float32)
         qt = t(q, device, torch.float16)
         ref = OA.decode_attention(sim.ps, qt.float().cpu().numpy(), s.meta["table"], s.meta["lens"], scale)
-        got = dec.decode_attention(store, qt, table, lens, scale, blocks_per_split=2)
-        torch.cuda.synchronize()
-        err = maxdiff(got, ref)
-        assert err <= TOL, f"{s.name} scale={scale}: max err {err}"
+        for inv in (False, True):
+            got = dec.decode_attention(store, qt, table, lens, scale, blocks_per_split=2, batch_invariant=inv)
+            torch.cuda.synchronize()
+            err = maxdiff(got, ref)
+            assert err <= TOL, f"{s.name} scale={scale} invariant={inv}: max err {err}"
 
 
 def test_decode_is_batch_invariant(device, case_stores):

@@ -69,9 +69,11 @@ def slots_of(table, lens, pos_fn, bs):
 
 
 def build_layer(device, lens, bits, *, h=8, d=128, bs=16, kg=16, vg=32, mem_bits=8, dtype=torch.float16, seed=1,
-                outliers=0.01, pages=None, table=None):
+                outliers=0.01, v_outliers=0.0, pages=None, table=None):
     """A layer store written through the product path: each sequence's first
-    len - 1 tokens in one step, then its last token in a second (decode) step."""
+    len - 1 tokens in one step, then its last token in a second (decode) step.
+    ``outliers`` / ``v_outliers``: the share of (head, channel) pairs of K / V
+    scaled x10."""
     rng = np.random.default_rng(seed)
     lens = np.asarray(lens, np.int64)
     if table is None:
@@ -84,11 +86,13 @@ def build_layer(device, lens, bits, *, h=8, d=128, bs=16, kg=16, vg=32, mem_bits
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     out_ch = torch.randperm(h * d, generator=gen, device=device)[: round(outliers * h * d)]
+    v_ch = torch.randperm(h * d, generator=gen, device=device)[: round(v_outliers * h * d)]
 
     def kv(n):
         k = torch.randn(n, h, d, generator=gen, device=device)
         k.view(n, h * d)[:, out_ch] *= 10
         v = torch.randn(n, h, d, generator=gen, device=device)
+        v.view(n, h * d)[:, v_ch] *= 10
         return k.to(dtype), v.to(dtype)
 
     pre = slots_of(table, lens, lambda i, n: np.arange(n - 1), bs)
@@ -126,14 +130,61 @@ def test_cfg2_full_layer_decode_matches_oracle(device, bits):
     scale = 128 ** -0.5
     for qt, name in ((q, "fp16 q"), (q.bfloat16(), "bf16 q")):
         ref = OA.decode_attention(ps, qt.float().cpu().numpy(), table, lens, scale, vectorized=True)
-        got = dec.decode_attention(store, qt, table_d, lens_d, scale, tier=bits)
-        check(f"cfg2 int{bits} {name}", got, ref)
+        got = dec.decode_attention(store, qt, table_d, lens_d, scale, tier=bits, batch_invariant=False)
+        check(f"cfg2 int{bits} {name} balanced schedule", got, ref)
         got = dec.decode_attention(store, qt, table_d, lens_d, scale, tier=bits, batch_invariant=True)
         check(f"cfg2 int{bits} {name} split schedule", got, ref)
         if name == "fp16 q":  # every tile through the generic path (the layer's tier set elsewhere)
             other = 4 if bits != 4 else 8
-            got = dec.decode_attention(store, qt, table_d, lens_d, scale, tier=other)
-            check(f"cfg2 int{bits} as tier {other}", got, ref)
+            for inv in (False, True):
+                got = dec.decode_attention(store, qt, table_d, lens_d, scale, tier=other, batch_invariant=inv)
+                check(f"cfg2 int{bits} as tier {other}" + (" split schedule" if inv else ""), got, ref)
+
+
+@pytest.mark.parametrize("bits", [8, 4, 2])
+@pytest.mark.parametrize("span", ["short", "long"])
+def test_cfg2_with_k_and_v_outliers(device, bits, span):
+    """BASELINE cfg2's inputs: 1% outlier channels x10 in K and in V. Outlier V
+    channels give values of magnitude 10-40 whose dequantized fp16 operand rounds
+    by up to 2^-7 .. 2^-6; short contexts (few tokens, large weights) are where
+    that rounding shows most in the output."""
+    rng = np.random.default_rng(21)
+    lens = rng.integers(16, 300, 32) if span == "short" else rng.integers(512, 8193, 64)
+    store, table = build_layer(device, lens, bits, seed=21, v_outliers=0.01)
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    lens_d = torch.from_numpy(lens).to(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(22)
+    q = torch.randn(len(lens), 32, 128, device=device, generator=gen).half()
+    ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, 128 ** -0.5, vectorized=True)
+    print(f"[cfg2 v-outliers {span} int{bits}] max |out| {np.abs(ref).max():.2f}", flush=True)
+    for inv in (False, True):
+        got = dec.decode_attention(store, q, table_d, lens_d, 128 ** -0.5, tier=bits, batch_invariant=inv)
+        check(f"cfg2 v-outliers {span} int{bits}" + (" split schedule" if inv else ""), got, ref)
+    out16 = torch.empty(len(lens), 32, 128, device=device, dtype=torch.float16)
+    dec.decode_attention(store, q, table_d, lens_d, 128 ** -0.5, tier=bits, out=out16)
+    raw = float(np.abs(out16.float().cpu().numpy() - ref).max())
+    check(f"cfg2 v-outliers {span} int{bits} fp16 out (raw max-abs {raw:.3e})", out16, ref)
+
+
+@pytest.mark.parametrize("bits", [8, 2])
+def test_gqa8_on_the_int8_and_int2_kernels(device, bits):
+    """GQA 8 (the 70B shape's Hq 64 / H 8) through the INT8- and INT2-specialised
+    kernels, several sequences, both schedules."""
+    rng = np.random.default_rng(23)
+    lens = rng.integers(100, 4000, 6)
+    store, table = build_layer(device, lens, bits, seed=23, v_outliers=0.01)
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(24)
+    q = torch.randn(len(lens), 64, 128, device=device, generator=gen).half()
+    ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, 128 ** -0.5, vectorized=True)
+    for inv in (False, True):
+        got = dec.decode_attention(store, q, table_d, torch.from_numpy(lens).to(device), 128 ** -0.5, tier=bits,
+                                   batch_invariant=inv)
+        check(f"gqa8 int{bits}" + (" split schedule" if inv else ""), got, ref)
 
 
 # ---- cfg3 -----------------------------------------------------------------------------
@@ -225,6 +276,23 @@ def test_cfg4_gqa8_long_context_split_paths(device):
         got = dec.decode_attention(store, q, table_d, lens_d, scale, tier=4, **kw)
         check(f"cfg4 {label}", got, ref)
     assert -(-nblk // 4) > 64 and -(-nblk // -(-nblk // 200)) > 64
+
+
+def test_cfg4_batch_at_int4_balanced(device):
+    """cfg4's decode batch at one tier: 16 sequences of 32,768 tokens, GQA 8, INT4,
+    the balanced schedule (the benchmark's) and the split one, against the
+    vectorized oracle."""
+    lens = np.full(16, 32768)
+    store, table = build_layer(device, lens, 4, seed=31, v_outliers=0.01)
+    ps = oracle_view(store)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(32)
+    q = torch.randn(16, 64, 128, device=device, generator=gen).half()
+    ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, 128 ** -0.5, vectorized=True)
+    for inv in (False, True):
+        got = dec.decode_attention(store, q, torch.from_numpy(table).to(device, torch.int32),
+                                   torch.from_numpy(lens).to(device), 128 ** -0.5, tier=4, batch_invariant=inv)
+        check("cfg4 16 x 32k int4" + (" split schedule" if inv else " balanced"), got, ref)
 
 
 def test_canary_at_hq64(device):
