@@ -230,7 +230,8 @@ class EchoKVSystem:
         st["avg_stored_bits"] = round(sum(b * n for b, n in written.items()) / total, 3) if total else None
         st["live_blocks_per_tier"] = [l.impl.store.pool.live_tiers() for l in self.layers]
         st["canary_fires"] = [l.impl.controller.fires for l in self.layers]
-        st["ema_layer0"] = {str(b): round(v, 6) for b, v in self.layers[0].impl.controller.ema.items()}
+        st["ema_layer0"] = {str(b): (None if v is None else round(v, 6))
+                            for b, v in self.layers[0].impl.controller.ema.items()}
         return st
 
 

@@ -12,12 +12,16 @@
 //                 the K min term is one more contraction of k_min with q into
 //                 the same accumulator; the block's open K group reads the
 //                 full-precision residual instead)
-//   O^T[d, q] += V[t, d]^T * P^T[t, q]   (v_mfma_f32_16x16x16f16, V dequantized
-//                 to fp16 in registers with its per-token fp16 scale / min)
+//   O^T[d, q] += V[t, d]^T * P^T[t, q]   (v_mfma_f32_16x16x16f16, with V = codes *
+//                 (scale hi + scale lo) + min as three exact fp16 operands: the
+//                 scale split so that codes * part fits fp16's 11 bits, and the
+//                 min, the same for the lane's channels, in one more MFMA)
 // Codes are exact in fp16. The query-side operand (q * k_scale, and the residual
 // keys) is carried as an fp16 hi + lo pair -- lo = fma(q, s, -hi) rounded once --
-// and contracted in two MFMA chains, so S is accurate to ~2^-22 instead of fp16's
-// 2^-11: keys with large outlier channels would otherwise dominate the error.
+// contracted into one fp32 accumulator, so S is accurate to ~2^-22 instead of
+// fp16's 2^-11: keys with large outlier channels would otherwise dominate the
+// error. Likewise V: a value of an outlier channel (|v| ~ 40) rounded to fp16 is
+// off by up to 2^-6, which a few heavy tokens carry into the output.
 // Lane (c, n) = (lane / 16, lane % 16) of the S^T product holds token n and
 // channels [c * D/4, (c+1) * D/4) in natural order; the S^T accumulator layout
 // (lane = 4 tokens x 1 query column) is exactly the B-operand layout of the
@@ -141,11 +145,10 @@ __device__ __forceinline__ h8_t kfrag_j(const uint32_t* kw, int j, const CodeK& 
   else return kfrag<2>(kw + (j >> 1), j & 1, k);
 }
 
-// V^T operand of the lane's channel j for its 4 tokens: v[i] = token i's slice
-// words, x4 / x2.. = pre-shifted copies; dequantized as c * s + m (one rounding).
+// The codes of the lane's V channel j for its 4 tokens, as fp16 (exact): v[i] =
+// token i's slice words, vs = pre-shifted copies. pv_tile dequantizes them.
 template <int BITS, int VW>
-__device__ __forceinline__ h4_t vfrag(int j, const uint32_t (*v)[VW], const uint32_t (*vs)[4], h2_t s01, h2_t s23,
-                                      h2_t m01, h2_t m23, const CodeK& k) {
+__device__ __forceinline__ h4_t vfrag(int j, const uint32_t (*v)[VW], const uint32_t (*vs)[4], const CodeK& k) {
   uint32_t x01, x23;
   if constexpr (BITS == 4) {
     const int by = j >> 1, sh = j & 1;  // odd channels: low nibble of the word >> 4
@@ -160,17 +163,15 @@ __device__ __forceinline__ h4_t vfrag(int j, const uint32_t (*v)[VW], const uint
     x01 = perm(vs[1][sh], vs[0][sh], pair_sel(by, by));
     x23 = perm(vs[3][sh], vs[2][sh], pair_sel(by, by));
   }
-  const h2_t v01 = __builtin_elementwise_fma(code_pair(x01, k), s01, m01);
-  const h2_t v23 = __builtin_elementwise_fma(code_pair(x23, k), s23, m23);
-  return h4_t{v01[0], v01[1], v23[0], v23[1]};
+  const h2_t c01 = code_pair(x01, k), c23 = code_pair(x23, k);
+  return h4_t{c01[0], c01[1], c23[0], c23[1]};
 }
 
-// INT4 V^T operands of all the lane's CPM (4 or 8) channels: a v_perm pairs the
+// INT4 V^T codes of all the lane's CPM (4 or 8) channels: a v_perm pairs the
 // bytes of tokens (0, 1) or (2, 3) holding four channels, the nibbles split into
-// even / odd channels one per byte, cvt_codes makes the exact fp16 codes and
-// one fma dequantizes (c * s + m, one rounding).
+// even / odd channels one per byte, cvt_codes makes the exact fp16 codes.
 template <int CPM>
-__device__ __forceinline__ void vfrags4(const uint32_t (*v)[1], h2_t s01, h2_t s23, h2_t m01, h2_t m23, h4_t* va) {
+__device__ __forceinline__ void vfrags4(const uint32_t (*v)[1], h4_t* va) {
   static_assert(CPM == 4 || CPM == 8, "INT4 V: the lane's channels of a token fit one word");
 #pragma unroll
   for (int hb = 0; hb < CPM / 4; ++hb) {  // bytes 2hb, 2hb+1 of each token: channels 4hb .. 4hb+3
@@ -180,8 +181,7 @@ __device__ __forceinline__ void vfrags4(const uint32_t (*v)[1], h2_t s01, h2_t s
     const uint32_t e01 = x01 & 0x0F0F0F0Fu, o01 = (x01 >> 4) & 0x0F0F0F0Fu;  // even / odd channels
     const uint32_t e23 = x23 & 0x0F0F0F0Fu, o23 = (x23 >> 4) & 0x0F0F0F0Fu;
     auto frag = [&](uint32_t c01, uint32_t c23) {
-      const h2_t a0 = __builtin_elementwise_fma(u2h(c01), s01, m01);
-      const h2_t a1 = __builtin_elementwise_fma(u2h(c23), s23, m23);
+      const h2_t a0 = u2h(c01), a1 = u2h(c23);
       return h4_t{a0[0], a0[1], a1[0], a1[1]};
     };
     va[4 * hb] = frag(cvt_codes<false>(e01), cvt_codes<false>(e23));
@@ -191,12 +191,12 @@ __device__ __forceinline__ void vfrags4(const uint32_t (*v)[1], h2_t s01, h2_t s
   }
 }
 
-// INT2 V^T operands of the lane's CPM (4 or 8) channels: a v_perm interleaves
+// INT2 V^T codes of the lane's CPM (4 or 8) channels: a v_perm interleaves
 // the code bytes of tokens (0, 1) / (2, 3) (byte b holds channels 4b .. 4b+3),
 // so each shift-and-mask leaves channel k of both tokens in bytes 0-1 and
 // channel 4+k in bytes 2-3, as cvt_codes takes them.
 template <int CPM>
-__device__ __forceinline__ void vfrags2(const uint32_t (*v)[1], h2_t s01, h2_t s23, h2_t m01, h2_t m23, h4_t* va) {
+__device__ __forceinline__ void vfrags2(const uint32_t (*v)[1], h4_t* va) {
   static_assert(CPM == 4 || CPM == 8, "INT2 V: the lane's channels of a token fit one word");
   const uint32_t sel = 0x05010400u;  // t0.b0, t1.b0, t0.b1, t1.b1
   const uint32_t x01 = perm(v[1][0], v[0][0], sel), x23 = perm(v[3][0], v[2][0], sel);
@@ -204,8 +204,7 @@ __device__ __forceinline__ void vfrags2(const uint32_t (*v)[1], h2_t s01, h2_t s
   for (int k = 0; k < 4; ++k) {
     const uint32_t c01 = (x01 >> (2 * k)) & 0x03030303u, c23 = (x23 >> (2 * k)) & 0x03030303u;
     auto frag = [&](uint32_t a01, uint32_t a23) {
-      const h2_t a0 = __builtin_elementwise_fma(u2h(a01), s01, m01);
-      const h2_t a1 = __builtin_elementwise_fma(u2h(a23), s23, m23);
+      const h2_t a0 = u2h(a01), a1 = u2h(a23);
       return h4_t{a0[0], a0[1], a1[0], a1[1]};
     };
     va[k] = frag(cvt_codes<false>(c01), cvt_codes<false>(c23));
@@ -288,13 +287,15 @@ struct Wave {
   static constexpr int CPM = D / 16;  // V channels per lane = 16x16x16 MFMAs per tile
   uint32_t qn[CPL / 2];               // fp16 query pairs (hi), natural channel order
   uint32_t ql[QLO ? CPL / 2 : 1];     // fp16 query pairs (lo = q - hi)
-  f4_t acc[CPM];                      // O^T fragments
+  f4_t acc[CPM];                      // O^T fragments: sum_t p * codes * V scale
+  f4_t acc_m;                         // sum_t p * V min of the lane's V group (every channel of it)
   float m_run, l_lane;                // running max (scaled log2 units), this lane's sum
   float scale;                        // |softmax scale| * log2(e), > 0 (a negative scale negates the query)
 };
 
 // S^T of one 16-token tile from its codes, K group by 32-channel block j:
-//   S^T += codes_j . (q * k_scale)_j^T   as fp16 hi / lo pairs (two chains)
+//   S^T += codes_j . (q * k_scale)_j^T   as fp16 hi / lo pairs (one fp32 accumulator:
+//                                         lo terms are ~2^-11 of hi, far above its rounding)
 //        - 1024 * sum_d (q * k_scale)_j  (BITS 8: fragments carry 1024 + c;
 //                                           any other BITS: the codes themselves)
 //        + k_min_j . q_j^T               (and q lo for float32 queries)
@@ -304,7 +305,7 @@ struct Wave {
 // lane's k_scale / k_min words of block j (channels 8 at a time, natural order).
 template <int D, bool QLO, int BITS>
 __device__ __forceinline__ void s_block(const Wave<D, QLO>& w, const uint32_t* ks, const uint32_t* km,
-                                        const h8_t& kf, int j, f4_t& sh, f4_t& sl) {
+                                        const h8_t& kf, int j, f4_t& s) {
   uint32_t hi[4], lo[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -319,19 +320,19 @@ __device__ __forceinline__ void s_block(const Wave<D, QLO>& w, const uint32_t* k
   const h8_t m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f,
                       (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f};
   const h8_t mn = w2h8(km[0], km[1], km[2], km[3]);
-  sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, h8, sh, 0, 0, 0);
-  sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, l8, sl, 0, 0, 0);
+  s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, h8, s, 0, 0, 0);
+  s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, l8, s, 0, 0, 0);
   if constexpr (BITS == 8) {  // INT4 / INT2 fragments carry the codes themselves
-    sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, h8, sh, 0, 0, 0);
-    sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, l8, sl, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, h8, s, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, l8, s, 0, 0, 0);
   } else {
     (void)m1024;
   }
-  sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-      mn, w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2], w.qn[4 * j + 3]), sh, 0, 0, 0);
+  s = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+      mn, w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2], w.qn[4 * j + 3]), s, 0, 0, 0);
   if constexpr (QLO)
-    sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-        mn, w2h8(w.ql[4 * j], w.ql[4 * j + 1], w.ql[4 * j + 2], w.ql[4 * j + 3]), sl, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        mn, w2h8(w.ql[4 * j], w.ql[4 * j + 1], w.ql[4 * j + 2], w.ql[4 * j + 3]), s, 0, 0, 0);
 }
 
 // S^T of a tile whose keys are the block's open K group, read from the
@@ -341,7 +342,7 @@ __device__ __forceinline__ void s_block(const Wave<D, QLO>& w, const uint32_t* k
 // is a template parameter, so every row load issues before the first MFMA waits.
 template <int D, bool QLO, int RDT>
 __device__ __forceinline__ void s_from_residual(const Wave<D, QLO>& w, const DecodeArgs& a, long rslot, int t0, int h,
-                                                int lane, f4_t& sh, f4_t& sl) {
+                                                int lane, f4_t& s) {
   constexpr int CPL = D / 4, NJ = D / 32;
   // Rows loaded together: f32 rows take twice the registers, and hi + lo halves.
   constexpr int STEP = RDT == ECHOKV_F32 ? 2 : NJ;
@@ -375,20 +376,62 @@ __device__ __forceinline__ void s_from_residual(const Wave<D, QLO>& w, const Dec
     for (int u = 0; u < STEP; ++u) {
       const int j = j0 + u;
       const h8_t qh = w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2], w.qn[4 * j + 3]);
-      sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[u], qh, sh, 0, 0, 0);
-      if constexpr (RDT == ECHOKV_F32) sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl[u], qh, sl, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[u], qh, s, 0, 0, 0);
+      if constexpr (RDT == ECHOKV_F32) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl[u], qh, s, 0, 0, 0);
       if constexpr (QLO) {
         const h8_t ql = w2h8(w.ql[4 * j], w.ql[4 * j + 1], w.ql[4 * j + 2], w.ql[4 * j + 3]);
-        sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[u], ql, sl, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[u], ql, s, 0, 0, 0);
       }
     }
   }
 }
 
+// The V statistics of the lane's 4 tokens (tokens past the sequence: 0) and the
+// split of their scales that makes every PV operand exact in fp16: s = hi + lo,
+// hi keeping the leading 11 - BITS significant bits, so codes * hi fits fp16's
+// 11 bits exactly, and so does codes * lo for 2- and 4-bit codes (8-bit: lo is
+// under a quarter of s, its product rounded to ~2^-14 of codes * s).
+struct VStats {
+  h2_t s01, s23, m01, m23;
+};
+template <int BITS>
+constexpr uint32_t vscale_mask() {
+  return BITS == 8 ? 0xFF00FF00u : (BITS == 4 ? 0xFFF0FFF0u : 0xFFFCFFFCu);
+}
+
 // Online-softmax update with the tile's unscaled scores x (masked: -inf), then
-// O^T += V^T P^T. p = exp2(scale * x - m): the scale rides in the fma.
-template <int D, bool QLO>
-__device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, const h4_t* va) {
+// O^T += V^T P^T with V = codes * (s hi + s lo) + min: one MFMA chain per scale
+// part, and one for the min (the lane's rows share one V group, so its rows of
+// acc_m are the min term of every channel it holds). No V operand is rounded:
+// values of V outlier channels (|v| up to ~40) would otherwise round by up to
+// 2^-6 in fp16. p = exp2(scale * x - m): the scale rides in the fma.
+// The lane's V codes of its 4 tokens, still packed as loaded (VW words a token),
+// and their statistics. The codes become fp16 only after the softmax, so only
+// the packed words stay live across it.
+template <int VW>
+struct VTile {
+  uint32_t w[4][VW];
+  VStats st;
+};
+
+template <int BITS, int CPM, int VW>
+__device__ __forceinline__ void v_codes(const uint32_t (*vw)[VW], h4_t* va) {
+  if constexpr (BITS == 4) {
+    vfrags4<CPM>(vw, va);
+  } else if constexpr (BITS == 2) {
+    vfrags2<CPM>(vw, va);
+  } else {
+    uint32_t vsh[4][4];
+    vshift<BITS, VW>(vw, vsh);
+    const CodeK vk = code_consts<BITS>();
+#pragma unroll
+    for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, vk);
+  }
+}
+
+template <int D, bool QLO, int BITS, int VW>
+__device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, const VTile<VW>& vt, uint32_t smask) {
+  const VStats& vs = vt.st;
   const float mt = rows_max(vmax(vmax3(x[0], x[1], x[2]), x[3])) * w.scale;
   const float m_new = vmax(w.m_run, mt);
   if (__builtin_amdgcn_ballot_w64(m_new > w.m_run + kLazyRescale)) {
@@ -396,6 +439,7 @@ __device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, cons
     w.l_lane *= alpha;
 #pragma unroll
     for (int j = 0; j < Wave<D, QLO>::CPM; ++j) w.acc[j] *= alpha;
+    w.acc_m *= alpha;
     w.m_run = m_new;
   }
   float p[4];
@@ -407,9 +451,18 @@ __device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, cons
   const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
   w.l_lane = __builtin_amdgcn_fdot2(h2_t{pb[2], pb[3]}, one, __builtin_amdgcn_fdot2(h2_t{pb[0], pb[1]}, one, w.l_lane, false),
                                     false);
+  h4_t va[Wave<D, QLO>::CPM];
+  v_codes<BITS, Wave<D, QLO>::CPM, VW>(vt.w, va);
+  const h2_t sh01 = u2h(h2u(vs.s01) & smask), sh23 = u2h(h2u(vs.s23) & smask);
+  const h2_t sl01 = vs.s01 - sh01, sl23 = vs.s23 - sh23;  // exact: the dropped bits
+  const h4_t shi = {sh01[0], sh01[1], sh23[0], sh23[1]}, slo = {sl01[0], sl01[1], sl23[0], sl23[1]};
 #pragma unroll
-  for (int j = 0; j < Wave<D, QLO>::CPM; ++j)
-    w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j], pb, w.acc[j], 0, 0, 0);
+  for (int j = 0; j < Wave<D, QLO>::CPM; ++j) {
+    w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j] * shi, pb, w.acc[j], 0, 0, 0);
+    w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j] * slo, pb, w.acc[j], 0, 0, 0);
+  }
+  const h4_t mins = {vs.m01[0], vs.m01[1], vs.m23[0], vs.m23[1]};
+  w.acc_m = __builtin_amdgcn_mfma_f32_16x16x16f16(mins, pb, w.acc_m, 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -463,7 +516,8 @@ __device__ __forceinline__ void load_as_bytes(const uint8_t* p, int bits, uint32
 // is a few memory round trips, not one per row.
 template <int D, bool QLO>
 __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs& a, long blk, int t0, int n_valid,
-                                         long rslot, bool in_res, int h, int lane, int bits, float* x, h4_t* va) {
+                                         long rslot, bool in_res, int h, int lane, int bits, float* x,
+                                         VTile<D / 64>& vt) {
   using W = Wave<D, QLO>;
   constexpr int CPL = W::CPL, NQK = W::NQK, CPM = W::CPM;
   const Lay& L = a.L;
@@ -474,11 +528,11 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
   const Hdr hd = load_hdr(pages, L, blk);
 
   // ---- S^T = K Q'^T (+ bias) -------------------------------------------
-  f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
+  f4_t s = {0.f, 0.f, 0.f, 0.f};
   if (in_res) {
-    if (a.res.dtype == ECHOKV_F16) s_from_residual<D, QLO, ECHOKV_F16>(w, a, rslot, t0, h, lane, sh, sl);
-    else if (a.res.dtype == ECHOKV_BF16) s_from_residual<D, QLO, ECHOKV_BF16>(w, a, rslot, t0, h, lane, sh, sl);
-    else s_from_residual<D, QLO, ECHOKV_F32>(w, a, rslot, t0, h, lane, sh, sl);
+    if (a.res.dtype == ECHOKV_F16) s_from_residual<D, QLO, ECHOKV_F16>(w, a, rslot, t0, h, lane, s);
+    else if (a.res.dtype == ECHOKV_BF16) s_from_residual<D, QLO, ECHOKV_BF16>(w, a, rslot, t0, h, lane, s);
+    else s_from_residual<D, QLO, ECHOKV_F32>(w, a, rslot, t0, h, lane, s);
   } else {
     const long e0 = ((long)(t0 / L.KG) * L.H + h) * D + c * CPL;
     const long rb = row_base_h(L, blk, hd, t0 + n, bits);
@@ -493,18 +547,18 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
       uint32_t ks[4], km[4];
       load_bytes<16>(pages + blk * L.stride + L.o_ks + 2 * e0 + 16 * j, ks);
       load_bytes<16>(pages + blk * L.stride + L.o_km + 2 * e0 + 16 * j, km);
-      s_block<D, QLO, 0>(w, ks, km, kfrag_bytes(kw + 2 * j), j, sh, sl);
+      s_block<D, QLO, 0>(w, ks, km, kfrag_bytes(kw + 2 * j), j, s);
     }
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float v = sh[i] + sl[i];
+    const float v = s[i];
     x[i] = (t0 + 4 * c + i < n_valid) ? v : -__builtin_inff();
   }
 
   // ---- V fragments: tokens t0+4c+i, channels n*CPM + j -------------------
   constexpr int VW = CPM / 4;  // words per token of the lane's V slice, one byte per code
-  uint32_t vw[4][VW], vsh[4][4];
+  uint32_t (&vw)[4][VW] = vt.w;
   const int G = D / L.VG;
   const int g = (n * CPM) / L.VG;
   _Float16 sv[4], mv[4];
@@ -539,12 +593,7 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
   if (bits == 8) load_v(std::integral_constant<int, 8>{});
   else if (bits == 4) load_v(std::integral_constant<int, 4>{});
   else load_v(std::integral_constant<int, 2>{});
-  vshift<8, VW>(vw, vsh);
-  const h2_t s01 = {sv[0], sv[1]}, s23 = {sv[2], sv[3]};
-  const h2_t m01 = {mv[0], mv[1]}, m23 = {mv[2], mv[3]};
-  const CodeK vk = code_consts<8>();
-#pragma unroll
-  for (int j = 0; j < CPM; ++j) va[j] = vfrag<8, VW>(j, vw, vsh, s01, s23, m01, m23, vk);
+  vt.st = VStats{{sv[0], sv[1]}, {sv[2], sv[3]}, {mv[0], mv[1]}, {mv[2], mv[3]}};
 }
 
 // ---------------------------------------------------------------------------
@@ -816,7 +865,8 @@ __device__ __forceinline__ void issue_tile(const DecodeArgs& a, const JobLane<D,
 // (log2 units, masked past n_rel valid tokens) and V fragments.
 template <int D, bool QLO, int BITS>
 __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const DecodeArgs& a, const LaneConst<D, BITS>& k,
-                                             const uint8_t* sp, int n_rel, int lane, float* x, h4_t* va) {
+                                             const uint8_t* sp, int n_rel, int lane, float* x,
+                                             VTile<(D / 16 * BITS / 8 >= 4 ? D / 16 * BITS / 8 / 4 : 1)>& vt) {
   using W = Wave<D, QLO>;
   using R = Ring<D, BITS>;
   constexpr int CPL = W::CPL, NQK = W::NQK, CPM = W::CPM;
@@ -832,7 +882,7 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
   }
   constexpr int VB = CPM * BITS / 8;
   constexpr int VW = VB >= 4 ? VB / 4 : 1;
-  uint32_t vw[4][VW], vsh[4][4];
+  uint32_t (&vw)[4][VW] = vt.w;
 #pragma unroll
   for (int i = 0; i < 4; ++i) load_bytes<VB>(sp + k.v_rd[i], vw[i]);
   // V scale / min of the lane's 4 tokens: 32-byte rows per token, scales then mins.
@@ -840,7 +890,7 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
   h2_t s01 = {vs[0], vs[16]}, s23 = {vs[32], vs[48]};
   h2_t m01 = {vs[256], vs[272]}, m23 = {vs[288], vs[304]};
 
-  f4_t sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
+  f4_t s = {0.f, 0.f, 0.f, 0.f};
   const CodeK ck = code_consts<BITS>();
   // k_scale / k_min words one 32-channel block ahead of their use, so each
   // block's LDS reads are in flight under the previous block's MFMAs.
@@ -854,10 +904,10 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
       load_bytes<16>(sp + k.s_rd + 4 * D * 2 + 16 * (j + 1), km[(j + 1) & 1]);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the next block's reads above this block's math
-    s_block<D, QLO, BITS>(w, ks[j & 1], km[j & 1], kfrag_j<BITS>(kw, j, ck), j, sh, sl);
+    s_block<D, QLO, BITS>(w, ks[j & 1], km[j & 1], kfrag_j<BITS>(kw, j, ck), j, s);
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = sh[i] + sl[i];
+  for (int i = 0; i < 4; ++i) x[i] = s[i];
   if (n_rel < 16) {
     // The block's last tile: tokens past the sequence get p = 0 and V = 0 (their
     // page bytes are arbitrary and 0 * inf would poison the sum).
@@ -871,18 +921,7 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = t + i < n_rel ? x[i] : -__builtin_inff();
   }
-  if constexpr (BITS == 4) {
-    (void)vsh;
-    vfrags4<CPM>(vw, s01, s23, m01, m23, va);
-  } else if constexpr (BITS == 2) {
-    (void)vsh;
-    vfrags2<CPM>(vw, s01, s23, m01, m23, va);
-  } else {
-    vshift<BITS, VW>(vw, vsh);
-    const CodeK vk = code_consts<BITS>();
-#pragma unroll
-    for (int j = 0; j < CPM; ++j) va[j] = vfrag<BITS, VW>(j, vw, vsh, s01, s23, m01, m23, vk);
-  }
+  vt.st = VStats{s01, s23, m01, m23};
 }
 
 // Wait for this wave's part of the tile about to be read: `ahead` tiles were
@@ -1051,6 +1090,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   }
 #pragma unroll
   for (int j = 0; j < W::CPM; ++j) w.acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
+  w.acc_m = f4_t{0.f, 0.f, 0.f, 0.f};
   w.m_run = -__builtin_inff();
   w.l_lane = 0.f;
 
@@ -1112,10 +1152,11 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
       if (!live) continue;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
       const int n_valid = seq_len - ((c0 + b) << a.bs_shift);
+      constexpr int VW = W::CPM * BITS / 8 >= 4 ? W::CPM * BITS / 8 / 4 : 1;
       float x[4];
-      h4_t va[W::CPM];
-      compute_tile<D, QLO, BITS>(w, a, kc, ring + (tt % R::NBUF) * R::SLOT, n_valid - t0, lane, x, va);
-      softmax_pv<D, QLO>(w, x, va);
+      VTile<VW> vt;
+      compute_tile<D, QLO, BITS>(w, a, kc, ring + (tt % R::NBUF) * R::SLOT, n_valid - t0, lane, x, vt);
+      softmax_pv<D, QLO, BITS, VW>(w, x, vt, vscale_mask<BITS>());
     }
     wait_vmcnt<0>();  // nothing of this chunk may still be landing in the ring
     wg_barrier();     // every wave is done reading the ring before the next chunk refills it
@@ -1132,14 +1173,17 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
         const bool in_res = rslot >= 0 && rgrp == (t0 >> a.kg_shift);
         const int n_valid = seq_len - ((c0 + b) << a.bs_shift);
         float x[4];
-        h4_t va[W::CPM];
-        tile_any<D, QLO>(w, a, blk, t0, n_valid, rslot, in_res, h, lane, tier, x, va);
-        softmax_pv<D, QLO>(w, x, va);
+        VTile<D / 64> vt;  // codes widened to bytes
+        tile_any<D, QLO>(w, a, blk, t0, n_valid, rslot, in_res, h, lane, tier, x, vt);
+        softmax_pv<D, QLO, 8, D / 64>(w, x, vt,
+                                      tier == 8 ? vscale_mask<8>() : (tier == 4 ? vscale_mask<4>() : vscale_mask<2>()));
       }
     }
   }
 
   const float l = rows_sum(w.l_lane);
+#pragma unroll
+  for (int j = 0; j < W::CPM; ++j) w.acc[j] += w.acc_m;  // the V min term, the same for the lane's channels
   if (live && n < a.gs) {
     const long qh = (long)h * a.gqa + a.g0 + n;
     if (sink.direct) {  // lane (c, n): channels (4c + i) * CPM + j of query head qh
