@@ -12,27 +12,30 @@
 //                 the K min term is one more contraction of k_min with q into
 //                 the same accumulator; the block's open K group reads the
 //                 full-precision residual instead)
-//   O^T[d, q] += V[t, d]^T * P^T[t, q]   (v_mfma_f32_16x16x16f16, with V = codes *
-//                 (scale hi + scale lo) + min as three exact fp16 operands: the
-//                 scale split so that codes * part fits fp16's 11 bits, and the
-//                 min, the same for the lane's channels, in one more MFMA)
+//   O^T[d, q] += V[t, d]^T * P^T[t, q]   (v_mfma_f32_16x16x32_f16, with V = codes *
+//                 (scale hi + scale lo) + min and P = p hi + p lo, every part an
+//                 exact fp16 operand: the scale split so that codes * part fits
+//                 fp16's 11 bits; K = 32 holds the lane's 4 tokens twice, so one
+//                 MFMA takes both scale parts against p hi, one more against p lo;
+//                 the min, the same for the lane's channels, in one more MFMA)
 // Codes are exact in fp16. The query-side operand (q * k_scale, and the residual
 // keys) is carried as an fp16 hi + lo pair -- lo = fma(q, s, -hi) rounded once --
 // contracted into one fp32 accumulator, so S is accurate to ~2^-22 instead of
 // fp16's 2^-11: keys with large outlier channels would otherwise dominate the
-// error. Likewise V: a value of an outlier channel (|v| ~ 40) rounded to fp16 is
-// off by up to 2^-6, which a few heavy tokens carry into the output.
+// error. Likewise V and P: a value of an outlier channel (|v| ~ 40) rounded to
+// fp16 is off by up to 2^-6, and weights rounded to fp16 (2^-12 each) move an
+// output whose values spread over +-40 by ~2e-3.
 // Lane (c, n) = (lane / 16, lane % 16) of the S^T product holds token n and
 // channels [c * D/4, (c+1) * D/4) in natural order; the S^T accumulator layout
-// (lane = 4 tokens x 1 query column) is exactly the B-operand layout of the
-// second MFMA, and the O^T accumulator keeps one query column per lane, so the
-// online softmax runs per lane with two cross-row max reductions per tile
-// (v_permlane16_swap / v_permlane32_swap). Query columns are the GQA heads of
-// the KV head, padded to 16. Codes become fp16 by placing them under the
-// exponent of 1024 (0x6400): V subtracts 1024 before the dequantizing fma, K
-// keeps 1024 + c and removes 1024 * sum(q * k_scale) with one more MFMA
-// contraction; v_perm_b32 picks the byte of each code pair, the low nibble of a
-// pre-shifted copy gives odd codes.
+// (lane = 4 tokens x 1 query column) is what the second MFMA's B operand takes
+// (the lane's 4 tokens, twice over K = 32), and the O^T accumulator keeps one
+// query column per lane, so the online softmax runs per lane with two cross-row
+// max reductions per tile (v_permlane16_swap / v_permlane32_swap). Query
+// columns are the GQA heads of the KV head, padded to 16. Codes become fp16
+// exactly: INT8 bytes under the exponent of 1024 (0x6400) -- V then subtracts
+// 1024, K keeps 1024 + c and removes 1024 * sum(q * k_scale) with one more MFMA
+// contraction -- and INT2 / INT4 through gfx950's fp8 conversion (a byte b < 16
+// read as E4M3 and scaled by 2^9 is b itself); v_perm_b32 gathers the code bytes.
 // The running max is rescaled lazily: only when some column's max grows by more
 // than 2^8 (probabilities stay <= 256, far inside fp16).
 //
@@ -253,7 +256,10 @@ __device__ __forceinline__ void load_bytes(const uint8_t* p, uint32_t* w) {
 }
 
 // max without the NaN-quieting canonicalizations fmaxf adds around values of
-// unknown origin (the scores are never NaN: masked ones are -inf).
+// unknown origin (the scores are never NaN: masked ones are -inf). Never give
+// these an MFMA result directly: the compiler places the wait states an MFMA's
+// result needs before its first VALU reader only for instructions it can see,
+// so an asm reader could see the accumulator before the MFMA has written it.
 __device__ __forceinline__ float vmax(float a, float b) {
   float r;
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
@@ -399,12 +405,6 @@ constexpr uint32_t vscale_mask() {
   return BITS == 8 ? 0xFF00FF00u : (BITS == 4 ? 0xFFF0FFF0u : 0xFFFCFFFCu);
 }
 
-// Online-softmax update with the tile's unscaled scores x (masked: -inf), then
-// O^T += V^T P^T with V = codes * (s hi + s lo) + min: one MFMA chain per scale
-// part, and one for the min (the lane's rows share one V group, so its rows of
-// acc_m are the min term of every channel it holds). No V operand is rounded:
-// values of V outlier channels (|v| up to ~40) would otherwise round by up to
-// 2^-6 in fp16. p = exp2(scale * x - m): the scale rides in the fma.
 // The lane's V codes of its 4 tokens, still packed as loaded (VW words a token),
 // and their statistics. The codes become fp16 only after the softmax, so only
 // the packed words stay live across it.
@@ -429,6 +429,11 @@ __device__ __forceinline__ void v_codes(const uint32_t (*vw)[VW], h4_t* va) {
   }
 }
 
+// Online-softmax update with the tile's unscaled scores x (masked: -inf), then
+// O^T += V^T P^T with V = codes * (s hi + s lo) + min and P = p hi + p lo, and
+// the min term in acc_m (the lane's rows share one V group, so its rows of acc_m
+// are the min term of every channel it holds). No operand is rounded. p =
+// exp2(scale * x - m): the scale rides in the fma.
 template <int D, bool QLO, int BITS, int VW>
 __device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, const VTile<VW>& vt, uint32_t smask) {
   const VStats& vs = vt.st;
@@ -445,24 +450,31 @@ __device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, cons
   float p[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], w.scale, -w.m_run));
-  const h4_t pb = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
-  // The sum takes the fp16 weights the PV product uses, so the output is a properly
-  // normalized average of the values: a dominant token's weight rounding cancels.
-  const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
-  w.l_lane = __builtin_amdgcn_fdot2(h2_t{pb[2], pb[3]}, one, __builtin_amdgcn_fdot2(h2_t{pb[0], pb[1]}, one, w.l_lane, false),
-                                    false);
+  w.l_lane += (p[0] + p[1]) + (p[2] + p[3]);
+  // p = hi + lo in fp16 (lo = the rounding of hi, rounded once: p to ~2^-22).
+  const h4_t ph = {(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+  const h4_t pl = {(_Float16)(p[0] - (float)ph[0]), (_Float16)(p[1] - (float)ph[1]), (_Float16)(p[2] - (float)ph[2]),
+                   (_Float16)(p[3] - (float)ph[3])};
   h4_t va[Wave<D, QLO>::CPM];
   v_codes<BITS, Wave<D, QLO>::CPM, VW>(vt.w, va);
   const h2_t sh01 = u2h(h2u(vs.s01) & smask), sh23 = u2h(h2u(vs.s23) & smask);
   const h2_t sl01 = vs.s01 - sh01, sl23 = vs.s23 - sh23;  // exact: the dropped bits
   const h4_t shi = {sh01[0], sh01[1], sh23[0], sh23[1]}, slo = {sl01[0], sl01[1], sl23[0], sl23[1]};
+  // 16x16x32 products whose K runs over the lane's 4 tokens twice: element e of
+  // a lane's operands is token 4c + (e & 3), A's halves the two scale parts, B's
+  // both p hi, then both p lo -- every product of the four parts, each exact.
+  const h8_t bh = __builtin_shufflevector(ph, ph, 0, 1, 2, 3, 4, 5, 6, 7);
+  const h8_t bl = __builtin_shufflevector(pl, pl, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
   for (int j = 0; j < Wave<D, QLO>::CPM; ++j) {
-    w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j] * shi, pb, w.acc[j], 0, 0, 0);
-    w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j] * slo, pb, w.acc[j], 0, 0, 0);
+    const h8_t a = __builtin_shufflevector(va[j] * shi, va[j] * slo, 0, 1, 2, 3, 4, 5, 6, 7);
+    w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, w.acc[j], 0, 0, 0);
+    w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, w.acc[j], 0, 0, 0);
   }
   const h4_t mins = {vs.m01[0], vs.m01[1], vs.m23[0], vs.m23[1]};
-  w.acc_m = __builtin_amdgcn_mfma_f32_16x16x16f16(mins, pb, w.acc_m, 0, 0, 0);
+  w.acc_m = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_shufflevector(mins, mins, 0, 1, 2, 3, 4, 5, 6, 7),
+                                                   __builtin_shufflevector(ph, pl, 0, 1, 2, 3, 4, 5, 6, 7), w.acc_m, 0,
+                                                   0, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -906,20 +918,25 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
     __builtin_amdgcn_sched_barrier(0);  // keep the next block's reads above this block's math
     s_block<D, QLO, BITS>(w, ks[j & 1], km[j & 1], kfrag_j<BITS>(kw, j, ck), j, s);
   }
+  // Tokens past the sequence (the block's last tile) get p = 0 and V = 0: their
+  // page bytes are arbitrary and 0 * inf would poison the sum. The scores are
+  // selected on every tile, before any branch: their first reader must follow
+  // the MFMAs in straight-line code, where the compiler places the wait states
+  // an MFMA result needs (across a branch it does not, and the max would read
+  // an unfinished accumulator).
+  const int t = 4 * c;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = s[i];
+  for (int i = 0; i < 4; ++i) {
+    x[i] = t + i < n_rel ? s[i] : -__builtin_inff();
+    asm volatile("" : "+v"(x[i]));  // emits nothing; keeps the select here, ahead of the branch
+  }
   if (n_rel < 16) {
-    // The block's last tile: tokens past the sequence get p = 0 and V = 0 (their
-    // page bytes are arbitrary and 0 * inf would poison the sum).
-    const int t = 4 * c;
     const uint32_t k01 = t + 1 < n_rel ? ~0u : (t < n_rel ? 0xFFFFu : 0u);
     const uint32_t k23 = t + 3 < n_rel ? ~0u : (t + 2 < n_rel ? 0xFFFFu : 0u);
     s01 = u2h(h2u(s01) & k01);
     m01 = u2h(h2u(m01) & k01);
     s23 = u2h(h2u(s23) & k23);
     m23 = u2h(h2u(m23) & k23);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = t + i < n_rel ? x[i] : -__builtin_inff();
   }
   vt.st = VStats{s01, s23, m01, m23};
 }
