@@ -68,7 +68,22 @@ def build_tiles(prefill, req_of, gqa: int, device, tokens: int | None = None) ->
         for t0 in range(0, nq, bm):
             rows.append((qs + t0, min(bm, nq - t0), pos0 + t0, ctx, r))
     tiles = to_device(torch.tensor(rows, dtype=torch.int32).reshape(-1, 5), device)
+    tiles.tile_tokens = bm  # checked against the kernel's tile size at launch, without a device read
     return tiles
+
+
+def check_tiles(tiles: torch.Tensor, tile_m: int) -> None:
+    """Refuse a tile table with more query tokens per tile than the kernel takes
+    (``tile_m``): the kernel would leave the extra rows unwritten. Tables from
+    ``build_tiles`` carry their size; others are read back (a device sync)."""
+    if tiles.dim() != 2 or tiles.shape[1] != 5:
+        raise ValueError("tiles must be an [n, 5] table (q_row0, n_tokens, q_pos0, ctx, request)")
+    made = getattr(tiles, "tile_tokens", None)
+    if made is None and tiles.numel():
+        made = int(tiles[:, 1].max())
+    if made is not None and made > tile_m:
+        raise ValueError(f"prefill tiles of {made} query tokens, but this layout's kernel takes at most {tile_m} "
+                         "per tile: build them with build_tiles(..., tokens=tile_m)")
 
 
 class DensePlan(NamedTuple):
@@ -301,10 +316,12 @@ def prefill_attention_fused(store, query: torch.Tensor, output: torch.Tensor, pr
     if not prefill:
         return
     L = store.layout
-    _lib.require_device(query, output, block_table, store.pages)
     hq = query.shape[1]
     gqa = hq // L.num_kv_heads
     tile_m = block_m(gqa) if kernels_take(L.head_size, gqa) else any_block_m(gqa)
+    if tiles is not None:
+        check_tiles(tiles, tile_m)
+    _lib.require_device(query, output, block_table, store.pages)
     if tiles is None:
         tiles = build_tiles(prefill, req_of, gqa, query.device, tokens=tile_m)
     if tiles.numel() == 0:

@@ -31,3 +31,25 @@ def test_dense_plan_covers_rows_and_contexts():
             assert all(rr == r and cc == c for rr, _, cc in packs[t0 : t0 + len(keys)])
         # heaviest request first
         assert qt[0][3] == 900
+
+
+def test_fused_prefill_refuses_tiles_larger_than_its_kernel_takes():
+    """Tiles built for the MFMA kernel (block_m tokens) handed to a layout that
+    takes the fp32 kernel (any_block_m tokens) are refused on the host, tagged
+    or not, before any device work; tiles of the right size pass the check."""
+    import pytest
+    import torch
+    from types import SimpleNamespace
+
+    store = SimpleNamespace(layout=SimpleNamespace(num_kv_heads=2, head_size=80), pages=torch.zeros(1))
+    gqa = 4
+    q = torch.zeros(40, 2 * gqa, 80)
+    prefill, req = [(0, 40, 40, 0)], [0]
+    assert not pf.kernels_take(80, gqa) and pf.block_m(gqa) > pf.any_block_m(gqa)
+    big = pf.build_tiles(prefill, req, gqa, "cpu")
+    for tiles in (big, big.clone()):  # tagged by build_tiles, and an untagged copy
+        with pytest.raises(ValueError, match="at most"):
+            pf.prefill_attention_fused(store, q, q, prefill, req, torch.zeros(1, 1), 0.1, tiles)
+    ok = pf.build_tiles(prefill, req, gqa, "cpu", tokens=pf.any_block_m(gqa))
+    with pytest.raises(RuntimeError, match="device tensors"):  # past the check: CPU tensors are refused next
+        pf.prefill_attention_fused(store, q, q, prefill, req, torch.zeros(1, 1), 0.1, ok)
