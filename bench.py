@@ -306,6 +306,8 @@ def run(args) -> dict:
         res["cpu_baseline"] = cpu_baseline(stores[int4[0]], shared, q[int4[0]], kn[int4[0]], vn[int4[0]], table, lens)
     if not args.no_prefill:
         res["prefill"] = run_prefill()
+    if not args.no_mixed:
+        res["mixed_tier"] = run_mixed()
     return res
 
 
@@ -409,6 +411,115 @@ def measured_traffic() -> int | None:
 
 
 C4_LAYERS, C4_S, C4_CTX, C4_HQ = 80, 16, 32768, 64  # config 4
+
+
+def run_mixed(reps: int = 20) -> dict:
+    """A mixed-tier layer at config 2's shape: every context's first two thirds
+    written at INT4 and the rest at INT8 (a layer the controller moved from 4 to
+    8; blocks keep the tier they were opened at), decoded with each tier's
+    specialised kernel -- the other tier's blocks then take the generic register
+    path -- beside the same contexts stored at one tier."""
+    import torch
+
+    from echokv_amd.kernels.decode import decode_attention
+    from echokv_amd.tiered_cache import TieredKVCache, TieredLayout
+    from echokv_amd.write_plan import SharedState, stage_plan
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(11)
+    ctx = rng.integers(512, 8193, S).astype(np.int64)
+    layout = TieredLayout(H, D, BS, MEM, KG, VG)
+    nbs = -(-ctx // BS)
+    nb = int(nbs.sum()) + 16
+    perm = rng.permutation(nb)
+    table = np.zeros((S, int(nbs.max())), np.int64)
+    o = 0
+    for i, n in enumerate(nbs):
+        table[i, :n] = perm[o : o + n]
+        o += n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(12)
+    cut = (ctx * 2 // 3 // BS) * BS  # block-aligned: the later blocks open at INT8
+
+    def layer(parts):
+        """A store written in len(parts) steps; parts = [(bits, start, end) per sequence fn]."""
+        shared = SharedState(nb, BS, KG, S + 16, kref_window=64, device=dev)
+        res = torch.zeros(S + 17, KG, H, D, dtype=torch.float16, device=dev)
+        st = TieredKVCache(layout, layout.alloc_pages(nb, dev), residual=res, shared=shared)
+        kref = torch.zeros(64, H, D, device=dev)
+        for bits, lo, hi in parts:
+            slots = np.concatenate([table[i][np.arange(lo[i], hi[i]) // BS] * BS + np.arange(lo[i], hi[i]) % BS
+                                    for i in range(S)])
+            plan = shared.planner.plan(slots)
+            op = st.prepare(plan, bits)
+            shared.commit(plan)
+            meta, extra = stage_plan(plan, dev, None)
+            shared.apply_res_map(*extra[:4])
+            if op is not None:
+                st.write_headers(torch.from_numpy(op[0]).to(dev), torch.from_numpy(op[1]).to(dev))
+            k = torch.randn(slots.size, H, D, device=dev, dtype=torch.float16, generator=gen)
+            v = torch.randn(slots.size, H, D, device=dev, dtype=torch.float16, generator=gen)
+            k.view(slots.size, H * D)[:, torch.randperm(H * D, generator=gen, device=dev)[: H * D // 100]] *= 10
+            st.apply(meta, k, v, kref)
+            del k, v
+        torch.cuda.synchronize()
+        return st
+
+    zero = np.zeros(S, np.int64)
+    stores = {"mixed": layer([(4, zero, cut), (8, cut, ctx)]), "int4": layer([(4, zero, ctx)]),
+              "int8": layer([(8, zero, ctx)])}
+    table_d = torch.from_numpy(table).to(dev, torch.int32)
+    lens_d = torch.from_numpy(ctx).to(dev)
+    q = torch.randn(S, HQ, D, device=dev, dtype=torch.float16, generator=gen)
+    out = torch.empty(S, HQ, D, device=dev, dtype=torch.float16)
+    num_splits = max(1, min(-(-table.shape[1] // 16), 64))
+    ws = (torch.empty(S, HQ, num_splits, D, device=dev), torch.empty(S, HQ, num_splits, 2, device=dev))
+
+    def time_us(st, tier: int, invariant: bool = False, mask: int | None = None) -> float:
+        tm = None if mask is None else torch.tensor([mask], dtype=torch.int32, device=dev)
+
+        def go():
+            decode_attention(st, q, table_d, lens_d, D ** -0.5, out=out, num_splits=num_splits, workspace=ws,
+                             tier=tier, batch_invariant=invariant, tier_mask=tm)
+
+        go()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            go()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    n8 = int((-(-(ctx - cut) // BS)).sum())
+    mixed_bytes = int(round(alg_bytes(ctx, 4) * (1 - (ctx - cut).sum() / ctx.sum())
+                            + alg_bytes(ctx, 8) * ((ctx - cut).sum() / ctx.sum())))
+    r = {"workload": "cfg2 shape, one layer: 64 x ctx U[512, 8192]; mixed = first 2/3 of each context at INT4, "
+                     "the rest at INT8; graph-replayed",
+         "mixed_blocks": {"4": int(nbs.sum()) - n8, "8": n8},
+         "mixed_alg_bytes": mixed_bytes}
+    # (label, store, kernel tier, split schedule, tier mask): one pass at a tier (the
+    # other tier's blocks on the generic path), or one pass per stored tier.
+    cases = (("mixed, one INT4 pass, balanced", "mixed", 4, False, None),
+             ("mixed, one INT8 pass, balanced", "mixed", 8, False, None),
+             ("mixed, one INT4 pass, split", "mixed", 4, True, None),
+             ("mixed, tier passes 4|8, split", "mixed", 4, True, 4 | 8),
+             ("int4, one pass, balanced", "int4", 4, False, None),
+             ("int4, one pass, split", "int4", 4, True, None),
+             ("int4, tier passes (mask 4: two empty launches), split", "int4", 4, True, 4),
+             ("int8, one pass, balanced", "int8", 8, False, None))
+    r["decode_us"] = {}
+    for label, name, tier, inv, mask in cases:
+        us = time_us(stores[name], tier, inv, mask)
+        b = mixed_bytes if name == "mixed" else alg_bytes(ctx, tier)
+        r["decode_us"][label] = {"us": round(us, 1), "GBs": round(b / us / 1e3, 1)}
+    return r
 
 
 def run_cfg4(reps: int = 5) -> dict:
@@ -635,6 +746,7 @@ def main():
     ap.add_argument("--reps", type=int, default=50, help="graph replays of the 16 INT4 layers' decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 prefill measurement")
+    ap.add_argument("--no-mixed", action="store_true", help="skip the mixed-tier layer measurement")
     ap.add_argument("--prefill-only", action="store_true", help="only the config-3 prefill measurement")
     ap.add_argument("--config4", action="store_true",
                     help="only config 4 (70B shape, 80 layers, about 102 GB of pages): decode per tier and the canary")

@@ -38,7 +38,7 @@ class Batch(C.Structure):
                 ("seq_lens", C.c_void_p), ("slot_mapping", C.c_void_p)]
 
 
-_STEP_WORDS = ("step", "len", "o_canary", "o_dec", "o_tok", "o_fin", "o_res", "o_grp", "o_open", "o_hdr", "o_seal",
+_STEP_WORDS = ("step", "len", "o_canary", "o_mask", "o_dec", "o_tok", "o_fin", "o_res", "o_grp", "o_open", "o_hdr", "o_seal",
                "rows_dec", "rows_tok", "rows_fin", "n_dec", "n_tokens", "n_fin", "n_res", "n_grp", "n_open",
                "n_seal", "n_canary", "decode_only", "graph_rows")
 

@@ -59,10 +59,10 @@ _SIGS = {
     "echokv_gather": [LP, P, P, P, RP, P, P, I64, P, P, P],
     "echokv_write_headers": [P, I32, I64, P, I64, P, P],
     "echokv_store_blocks": [LP, P, P, I64, P, P, I32, P],
-    "echokv_decode": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, I32, P, P, P,
-                      I64, I64, I32, P],
-    "echokv_decode_static": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, I32, P,
-                             I64, I64, I32, P],
+    "echokv_decode": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, P, I32, P, P,
+                      P, I64, I64, I32, P],
+    "echokv_decode_static": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, P, I64, P, P, I64, FL, I32, I32, I32, P, I32,
+                             P, I64, I64, I32, P],
     "echokv_prefill": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, I32, P, I64, FL, I32, P, P],
     "echokv_prefill_own_group": [LP, P, P, P, RP, P, I64, I64, I32, I32, P, I64, I64, I32, P, I64, P, I64, P, I64, I64,
                                  P, P, I64, I64, I32, FL, P],

@@ -133,11 +133,17 @@ class DecodeWork:
     num_splits: int  # split grid (fixed, so a graph replays it)
     workspace: tuple | None  # (acc, ml) shared by every layer; None: the call allocates
     batch_invariant: bool
+    tier_masks: torch.Tensor | None = None  # [layers, 2] int32: each layer's live tiers, read by the kernels
 
     def run(self, impl, query: torch.Tensor, block_table: torch.Tensor, out: torch.Tensor) -> None:
+        # On the split schedule each tier the layer holds runs on its own fast path
+        # (the mask is read when the kernels run, so a replayed graph follows it).
+        mask = None
+        if self.batch_invariant and self.tier_masks is not None:
+            mask = self.tier_masks[impl.group_index, :1]
         dec.decode_attention(impl.store, query, block_table, self.lens, impl.scale, q_rows=self.rows,
                              bt_rows=self.reqs, out=out, num_splits=self.num_splits, workspace=self.workspace,
-                             tier=impl.decode_tier(), batch_invariant=self.batch_invariant)
+                             tier=impl.decode_tier(), batch_invariant=self.batch_invariant, tier_mask=mask)
 
 
 @dataclass
@@ -222,8 +228,9 @@ class _Group:
         self.impls = [layer.impl for layer in layers]
         self.shared = SharedState(caches[0].shape[0], builder.kv_cache_spec.block_size, cfg.k_group,
                                   builder.residual_slots, cfg.kref_window, builder.device)
-        for impl, cache in zip(self.impls, caches):
+        for i, (impl, cache) in enumerate(zip(self.impls, caches)):
             impl.bind(cache, self.shared)
+            impl.group_index = i  # this layer's row of the step's per-layer device tables
         self.stores = [impl.store for impl in self.impls]
         self.driver = StepDriver(self.shared, self.stores, builder.cap, cfg.canary_max_q, builder.device)
         self.headers = HeaderWriter(self.stores)
@@ -332,7 +339,7 @@ class EchoKVMetadataBuilder(AttentionMetadataBuilder):
         md.fire = up.n_canary > 0
         if up.decode is not None:
             n_dec = up.decode[0].numel()
-            md.decode = DecodeWork(*up.decode, num_splits=self.num_splits,
+            md.decode = DecodeWork(*up.decode, num_splits=self.num_splits, tier_masks=up.tier_masks,
                                    workspace=group.impls[0].decode_workspace(n_dec, self.num_splits, self.cap),
                                    batch_invariant=self.cfg.batch_invariant)
         if up.prefill:

@@ -179,8 +179,9 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
                const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
                int32_t num_q_heads, const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
                const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs, float softmax_scale,
-               int32_t num_splits, int32_t blocks_per_split, int32_t tier, int32_t flags, float* acc, float* ml,
-               bool static_scratch, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
+               int32_t num_splits, int32_t blocks_per_split, int32_t tier, const int32_t* tier_mask, int32_t flags,
+               float* acc, float* ml, bool static_scratch, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+               echokv_stream_t stream) {
   if (!lay_ok(L)) return ECHOKV_ESHAPE;
   const bool mfma = decode_mfma(L);
   if (!mfma && L->head_size > ek::kMaxAnyD) return ECHOKV_ESHAPE;
@@ -190,6 +191,7 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   if (num_seqs < 0 || num_splits <= 0 || blocks_per_split <= 0 || !res_ok(res)) return ECHOKV_EINVAL;
   if (tier != 2 && tier != 4 && tier != 8) return ECHOKV_EINVAL;
   if (flags & ~ECHOKV_DECODE_BATCH_INVARIANT) return ECHOKV_EINVAL;
+  if (tier_mask && !(flags & ECHOKV_DECODE_BATCH_INVARIANT)) return ECHOKV_EINVAL;  // tier passes: split schedule
   if (num_seqs == 0) return ECHOKV_OK;
   if (!pages || !block_res || !res_group || !query || !block_table || !seq_lens || !out) return ECHOKV_EINVAL;
   if (!static_scratch && (!acc || !ml)) return ECHOKV_EINVAL;
@@ -215,6 +217,8 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   a.bps = blocks_per_split;
   a.num_seqs = num_seqs;
   a.tier = tier;
+  a.tier0 = tier;
+  a.tier_mask = nullptr;
   a.bs_shift = mfma ? __builtin_ctz((unsigned)L->block_size) : 0;
   a.kg_shift = mfma ? __builtin_ctz((unsigned)L->k_group) : 0;
   a.vg_shift = __builtin_ctz((unsigned)L->v_group);
@@ -247,9 +251,22 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   for (int g0 = 0; g0 < gqa; g0 += 16) {
     a.g0 = g0;
     a.gs = gqa - g0 < 16 ? gqa - g0 : 16;
-    const hipError_t d = mfma ? ek::launch_decode(a, num_seqs, (hipStream_t)stream)
-                              : ek::launch_decode_any(a, (hipStream_t)stream);
-    if (d != hipSuccess) return ECHOKV_ELAUNCH;
+    if (mfma && tier_mask) {
+      // One launch per tier, lowest first: each runs only if the layer holds its
+      // tier (read from tier_mask when it runs) and continues the partial rows the
+      // one before it left.
+      a.tier_mask = tier_mask;
+      for (int t : {2, 4, 8}) {
+        a.tier = t;
+        if (ek::launch_decode(a, num_seqs, (hipStream_t)stream) != hipSuccess) return ECHOKV_ELAUNCH;
+      }
+      a.tier = tier;
+      a.tier_mask = nullptr;
+    } else {
+      const hipError_t d = mfma ? ek::launch_decode(a, num_seqs, (hipStream_t)stream)
+                                : ek::launch_decode_any(a, (hipStream_t)stream);
+      if (d != hipSuccess) return ECHOKV_ELAUNCH;
+    }
     hipError_t e;
     if (a.ranges > 0) {
       e = ek::launch_merge_balanced(a, (hipStream_t)stream);
@@ -271,11 +288,12 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
                   const echokv_residual* res, const void* query, int64_t q_s0, int64_t q_s1, int32_t q_dtype,
                   int32_t num_q_heads, const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
                   const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs, float softmax_scale,
-                  int32_t num_splits, int32_t blocks_per_split, int32_t tier, int32_t flags, float* acc, float* ml,
-                  void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
+                  int32_t num_splits, int32_t blocks_per_split, int32_t tier, const int32_t* tier_mask,
+                  int32_t flags, float* acc, float* ml, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
+                  echokv_stream_t stream) {
   return decode_run(L, pages, block_res, res_group, res, query, q_s0, q_s1, q_dtype, num_q_heads, q_rows,
                     block_table, bt_s0, bt_rows, seq_lens, num_seqs, softmax_scale, num_splits, blocks_per_split,
-                    tier, flags, acc, ml, false, out, o_s0, o_s1, out_dtype, stream);
+                    tier, tier_mask, flags, acc, ml, false, out, o_s0, o_s1, out_dtype, stream);
 }
 
 int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res,
@@ -283,11 +301,11 @@ int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int
                          int64_t q_s1, int32_t q_dtype, int32_t num_q_heads, const int64_t* q_rows,
                          const int32_t* block_table, int64_t bt_s0, const int64_t* bt_rows, const int64_t* seq_lens,
                          int64_t num_seqs, float softmax_scale, int32_t num_splits, int32_t blocks_per_split,
-                         int32_t tier, int32_t flags, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
-                         echokv_stream_t stream) {
+                         int32_t tier, const int32_t* tier_mask, int32_t flags, void* out, int64_t o_s0,
+                         int64_t o_s1, int32_t out_dtype, echokv_stream_t stream) {
   return decode_run(L, pages, block_res, res_group, res, query, q_s0, q_s1, q_dtype, num_q_heads, q_rows,
                     block_table, bt_s0, bt_rows, seq_lens, num_seqs, softmax_scale, num_splits, blocks_per_split,
-                    tier, flags, nullptr, nullptr, true, out, o_s0, o_s1, out_dtype, stream);
+                    tier, tier_mask, flags, nullptr, nullptr, true, out, o_s0, o_s1, out_dtype, stream);
 }
 
 int64_t echokv_decode_workspace_rows(const echokv_layout* L, int32_t num_q_heads, int32_t q_dtype,

@@ -170,6 +170,13 @@ struct DecodeArgs {
   int num_splits, bps;
   long num_seqs;
   int tier;    // the layer's tier: selects the kernel specialised for it (2, 4 or 8)
+  // Tier passes (split schedule): null, or the layer's tiers with live blocks as a
+  // bit set of tier values (2 | 4 | 8; 0: `tier0` alone). Each kernel of the tiers
+  // 2, 4, 8 then runs its tier's blocks only; the lowest present tier also takes
+  // blocks of tiers outside the set and starts each span afresh, the others
+  // continue the span's partial result that the pass before them left.
+  const int32_t* tier_mask;
+  int tier0;
   // log2 of block size, K group and V group (powers of two), and a reciprocal for
   // chunk id / chunks_per_page: floor(id / KC) = umulhi(id, kc_mul) (kc_mul 0: KC = 1).
   int bs_shift, kg_shift, vg_shift;

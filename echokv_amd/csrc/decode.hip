@@ -1047,6 +1047,15 @@ struct SpanSink {
   int rem_after, total;
 };
 
+// A tier pass (DecodeArgs::tier_mask): which of a span's blocks this kernel takes,
+// and whether the span continues the partial result already in its rows.
+struct SpanPass {
+  bool on;     // false: every valid block (one pass over the layer)
+  bool other;  // also blocks whose tier is not in `mask`
+  int mask;    // the tiers that have passes (2 | 4 | 8)
+  bool carry;  // start from the span's partial row instead of afresh
+};
+
 // Wave priority from the share of the workgroup's range still ahead of it: the
 // co-resident workgroups of a CU start at different times, and the one with the
 // most left issues first, so they finish together instead of in start order.
@@ -1059,9 +1068,10 @@ __device__ __forceinline__ void range_priority(int left, int total) {
 
 // Blocks [b_start, b_end) of sequence `seq` for the KV heads of head group hg
 // (one wave per head).
-template <int D, int BITS, bool QLO>
+template <int D, int BITS, bool QLO, bool PASSES>
 __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b_start, int b_end, int hg, int wv,
-                                            int lane, uint8_t* ring, uint32_t ring0, SpanSink sink) {
+                                            int lane, uint8_t* ring, uint32_t ring0, SpanSink sink,
+                                            SpanPass pass = SpanPass{false, true, 0, false}) {
   using W = Wave<D, QLO>;
   using R = Ring<D, BITS>;
   const Lay& L = a.L;
@@ -1110,6 +1120,25 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   w.acc_m = f4_t{0.f, 0.f, 0.f, 0.f};
   w.m_run = -__builtin_inff();
   w.l_lane = 0.f;
+  // A later tier pass continues the partial result the passes before it left in
+  // the span's row (its sum in one lane of the column, so the cross-row sum
+  // restores it), loaded once the span has a block of this pass's tier; a span
+  // with none leaves its row as it is.
+  bool carried = !pass.carry;
+  auto load_carry = [&]() {
+    if (live && n < a.gs) {
+      const long row = sink.part_row0 + ((long)h * a.gqa + a.g0 + n) * sink.part_stride;
+      const float* src = a.acc + row * D;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < W::CPM; ++j) w.acc[j][i] = src[(4 * c + i) * W::CPM + j];
+      }
+      w.m_run = a.ml[row * 2];
+      w.l_lane = c == 0 ? a.ml[row * 2 + 1] : 0.f;
+    }
+    carried = true;
+  };
 
   const LaneConst<D, BITS> kc = lane_const<D, BITS>(a, wv, lane);
   const JobLane<D, BITS> jl = job_lane<D, BITS>(a, wv, hg, lane);
@@ -1118,17 +1147,54 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   for (int c0 = b_start; c0 < b_end; c0 += 64) {
     const int nb = b_end - c0 < 64 ? b_end - c0 : 64;
     if (c0 != b_start) bl = load_block<BITS>(a, lane < nb ? (long)a.bt[bt_row * a.bt_s0 + c0 + lane] : -1L);
-    const int last_tok = (c0 + nb) * L.BS < seq_len ? (c0 + nb) * L.BS : seq_len;
-    const int n_tiles = (last_tok - c0 * L.BS + 15) >> 4;
+    // PASSES: the blocks this kernel takes, moved to the front of the chunk's
+    // lanes in order, so the tile loop runs over them alone; b_orig keeps each
+    // one's place in the sequence. (Already in front -- every valid block of a
+    // one-pass launch, or of a layer stored at one tier -- they stay where they
+    // are.) Without PASSES every block keeps its lane and invalid ones are skipped.
+    int b_orig = lane;
+    int n_take = nb;
+    uint64_t m_blk = ~0ull;
+    if constexpr (!PASSES) {
+      m_blk = __builtin_amdgcn_ballot_w64(bl.blk >= 0);
+    } else {
+      const bool take = bl.blk >= 0 && (!pass.on || bl.tier == BITS || (pass.other && !(pass.mask & bl.tier)));
+      const uint64_t m_take = __builtin_amdgcn_ballot_w64(take);
+      n_take = __builtin_popcountll(m_take);
+      if (m_take != (n_take == 64 ? ~0ull : (1ull << n_take) - 1)) {
+        const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m_take >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)m_take, 0u));
+        const int to = 4 * (take ? below : n_take + (lane - below));  // a permutation of the lanes
+        auto push = [&](uint32_t v) { return (uint32_t)__builtin_amdgcn_ds_permute(to, (int)v); };
+        auto push64 = [&](uint64_t v) { return (uint64_t)push((uint32_t)v) | ((uint64_t)push((uint32_t)(v >> 32)) << 32); };
+        bl.pg = push64(bl.pg);
+        if constexpr (BITS >= 4) bl.cb1 = push64(bl.cb1);
+        if constexpr (BITS == 8) {
+          bl.cb2 = push64(bl.cb2);
+          bl.cb3 = push64(bl.cb3);
+        }
+        bl.blk = (int)push((uint32_t)bl.blk);
+        bl.tier = (int)push((uint32_t)bl.tier);
+        bl.fast_rg = (int)push((uint32_t)bl.fast_rg);
+        bl.rslot = (int)push((uint32_t)bl.rslot);
+        bl.rgrp = (int)push((uint32_t)bl.rgrp);
+        b_orig = (int)push((uint32_t)lane);
+      }
+    }
+    // Every taken block but the sequence's last is full; the last one taken may be it.
+    const int last_b = !PASSES ? nb - 1 : (n_take > 0 ? (int)rl((uint32_t)b_orig, n_take - 1) : 0);
+    const int last_n = seq_len - (c0 + last_b) * L.BS < L.BS ? seq_len - (c0 + last_b) * L.BS : L.BS;
+    const int n_tiles = n_take > 0 ? ((n_take - 1) * L.BS + last_n + 15) >> 4 : 0;
+    auto orig = [&](int b) { return PASSES ? (int)rl((uint32_t)b_orig, b) : b; };
+    if (PASSES && !carried && n_take > 0) load_carry();
 
     // A tile takes the pipelined path when its block is stored at the kernel's
     // tier with every chunk in range and it is not the block's open K group;
     // the others (rare: demoted / downgraded blocks, each sequence's open
     // group) are computed after the chunk's pipelined tiles, from global memory.
     // Per-block bit masks (one bit per lane = block) keep the per-tile test scalar.
-    const uint64_t m_fast = stats_ok ? __builtin_amdgcn_ballot_w64(bl.fast_rg != kNotFast) : 0ull;
+    const uint64_t m_fast = stats_ok ? __builtin_amdgcn_ballot_w64(lane < n_take && bl.fast_rg != kNotFast) : 0ull;
     const uint64_t m_open = __builtin_amdgcn_ballot_w64(bl.fast_rg >= 0);
-    const uint64_t m_blk = __builtin_amdgcn_ballot_w64(bl.blk >= 0);
     auto piped = [&](int tt) -> bool {
       const int b = tt >> tpb_shift;
       if (!((m_fast >> b) & 1)) return false;
@@ -1160,7 +1226,8 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
       wg_barrier();
       if (tt + R::NBUF - 1 < n_tiles) issue(tt + R::NBUF - 1);
       const int b = tt >> tpb_shift;
-      if (sink.total > 0 && (tt & 3) == 0) range_priority(b_end - c0 - b + sink.rem_after, sink.total);
+      const int bo = orig(b);
+      if (sink.total > 0 && (tt & 3) == 0) range_priority(b_end - c0 - bo + sink.rem_after, sink.total);
       if (!((m_blk >> b) & 1)) continue;
       if (!piped(tt)) {
         rare = true;
@@ -1168,7 +1235,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
       }
       if (!live) continue;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
-      const int n_valid = seq_len - ((c0 + b) << a.bs_shift);
+      const int n_valid = seq_len - ((c0 + bo) << a.bs_shift);
       constexpr int VW = W::CPM * BITS / 8 >= 4 ? W::CPM * BITS / 8 / 4 : 1;
       float x[4];
       VTile<VW> vt;
@@ -1188,7 +1255,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
         const int rgrp = (int)rl((uint32_t)bl.rgrp, b);
         const long rslot = (int)rl((uint32_t)bl.rslot, b);
         const bool in_res = rslot >= 0 && rgrp == (t0 >> a.kg_shift);
-        const int n_valid = seq_len - ((c0 + b) << a.bs_shift);
+        const int n_valid = seq_len - ((c0 + orig(b)) << a.bs_shift);
         float x[4];
         VTile<D / 64> vt;  // codes widened to bytes
         tile_any<D, QLO>(w, a, blk, t0, n_valid, rslot, in_res, h, lane, tier, x, vt);
@@ -1198,6 +1265,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
     }
   }
 
+  if (!carried) return;  // no block of this pass's tier: the row keeps the earlier passes' result
   const float l = rows_sum(w.l_lane);
 #pragma unroll
   for (int j = 0; j < W::CPM; ++j) w.acc[j] += w.acc_m;  // the V min term, the same for the lane's channels
@@ -1239,6 +1307,14 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
 template <int D, int BITS, bool QLO>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
+  SpanPass pass{false, true, 0, false};
+  if (a.tier_mask) {  // a tier pass: nothing to do unless the layer holds this tier
+    int m = *a.tier_mask & (2 | 4 | 8);
+    if (m == 0) m = a.tier0;
+    if (!(m & BITS)) return;
+    const int lowest = m & -m;
+    pass = SpanPass{true, BITS == lowest, m, BITS != lowest};
+  }
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar job branches
   const uint32_t ring0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)ring_lds);
@@ -1260,8 +1336,8 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   const int bps = split_blocks(a, n_blocks);
   const int b_start = split * bps;
   const int b_end = b_start + bps < n_blocks ? b_start + bps : n_blocks;
-  decode_span<D, BITS, QLO>(a, seq, b_start, b_end, (int)(item % n_hg), wv, lane, ring_lds, ring0,
-                            SpanSink{seq * a.hq * a.num_splits + split, a.num_splits, false, 0, 0});
+  decode_span<D, BITS, QLO, true>(a, seq, b_start, b_end, (int)(item % n_hg), wv, lane, ring_lds, ring0,
+                                  SpanSink{seq * a.hq * a.num_splits + split, a.num_splits, false, 0, 0}, pass);
 }
 
 // ---------------------------------------------------------------------------
@@ -1350,8 +1426,8 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
     if (nb > 0) {
       const bool whole = pos == first && end == first + nb;
       const long slot = 2 * r + (pos == lo ? 0 : 1);
-      decode_span<D, BITS, QLO>(a, seq, (int)(pos - first), (int)(end - first), hg, wv, lane, ring_lds, ring0,
-                                SpanSink{slot * a.hq, 1, whole, (int)(hi - end), (int)(hi - lo)});
+      decode_span<D, BITS, QLO, false>(a, seq, (int)(pos - first), (int)(end - first), hg, wv, lane, ring_lds,
+                                       ring0, SpanSink{slot * a.hq, 1, whole, (int)(hi - end), (int)(hi - lo)});
     }
     pos = end;
     first += nb;

@@ -157,7 +157,8 @@ int ekh_stepper_run(ekh_stepper* S, const ekh_batch* b, const int32_t* tiers, in
   ekh_step_view& v = *out;
   v.step = p.step;
   v.o_canary = 2;
-  v.o_dec = v.o_canary + even(s.nq);
+  v.o_mask = v.o_canary + even(s.nq);
+  v.o_dec = v.o_mask + even(nlay);
   v.o_tok = v.o_dec + 3 * r_dec;
   v.o_fin = v.o_tok + 4 * r_tok;
   v.o_res = v.o_fin + r_fin * w;
@@ -194,6 +195,12 @@ int ekh_stepper_run(ekh_stepper* S, const ekh_batch* b, const int32_t* tiers, in
   img[0] = p.n_fin;
   img[1] = t;
   std::copy(canary.begin(), canary.end(), img + v.o_canary);
+  // Each layer's tiers with live blocks (2 | 4 | 8), after this step's opens: the
+  // decode kernels read it to run each present tier's blocks on its own path.
+  for (int l = 0; l < nlay; ++l) {
+    const int64_t* live = s.pools[l]->live;
+    img[v.o_mask + l] = (live[2] ? 2 : 0) | (live[4] ? 4 : 0) | (live[8] ? 8 : 0);
+  }
   std::copy(s.dec_row.begin(), s.dec_row.end(), img + v.o_dec);
   std::copy(s.dec_req.begin(), s.dec_req.end(), img + v.o_dec + r_dec);
   std::copy(s.dec_len.begin(), s.dec_len.end(), img + v.o_dec + 2 * r_dec);

@@ -61,6 +61,7 @@ def decode_attention(
     workspace: tuple[torch.Tensor, torch.Tensor] | str | None = None,
     tier: int | None = None,
     batch_invariant: bool = True,
+    tier_mask: torch.Tensor | str | None = None,
 ) -> torch.Tensor:
     """Attention of one query token per sequence over each sequence's cache.
 
@@ -80,6 +81,12 @@ def decode_attention(
     of the batch; ``batch_invariant=False`` spreads the batch's blocks evenly over
     every workgroup the GPU holds instead (faster on uneven batches; a sequence's
     result then depends on the rest of the batch through float rounding).
+    ``tier_mask``: for a layer holding blocks at several tiers, each tier's blocks
+    on that tier's own fast path (one kernel launch per tier, lowest first, into the
+    same partial rows): an int32 device tensor whose element 0 holds the tiers as a
+    bit set of tier values (2 | 4 | 8), read when the kernels run, so a captured
+    graph follows it from step to step; or ``"auto"``: the tiers the store's pool
+    holds blocks at now (one tier: no passes). Needs ``batch_invariant``.
     """
     L = store.layout
     dev = query.device
@@ -114,13 +121,26 @@ def decode_attention(
             acc, ml = workspace
             if acc.numel() < rows * hq * d or ml.numel() < rows * hq * 2:
                 raise ValueError(f"decode workspace holds fewer than the {rows} rows this call needs")
+    if isinstance(tier_mask, str):
+        if tier_mask != "auto":
+            raise ValueError(f"tier_mask must be an int32 device tensor or 'auto', got {tier_mask!r}")
+        live = store.pool.live_tiers()
+        present = [b for b in (2, 4, 8) if live[b]]
+        tier_mask = None
+        if len(present) > 1:
+            tier_mask = torch.tensor([sum(present)], dtype=torch.int32, device=dev)
+    if tier_mask is not None:
+        if not batch_invariant:
+            raise ValueError("tier passes run on the split schedule: pass batch_invariant=True with tier_mask")
+        if tier_mask.dtype != torch.int32 or tier_mask.device != dev or tier_mask.numel() < 1:
+            raise ValueError("tier_mask must be an int32 tensor on the query's device")
     if tier is None:
         tier = store.pool.majority_tier()
     res = _lib.residual(store.res_k)
     head = (_lib.byref(store.abi), _lib.ptr(store.pages), _lib.ptr(store.block_res), _lib.ptr(store.res_group),
             _lib.byref(res), _lib.ptr(query), query.stride(0), query.stride(1), _lib.dtype_code(query), hq,
             _lib.ptr(q_rows), _lib.ptr(block_table), block_table.stride(0), _lib.ptr(bt_rows), _lib.ptr(lens), s,
-            float(softmax_scale), int(num_splits), int(blocks_per_split), int(tier),
+            float(softmax_scale), int(num_splits), int(blocks_per_split), int(tier), _lib.ptr(tier_mask),
             _lib.DECODE_BATCH_INVARIANT if batch_invariant else 0)
     tail = (_lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out), _lib.stream())
     if static:

@@ -35,6 +35,7 @@ class StepUpload:
 
     fin_count: torch.Tensor  # [1]: masks a graph's full-grid finalize
     canary_rows: torch.Tensor  # [canary slots] query rows the canary reads on a fire step
+    tier_masks: torch.Tensor  # [layers, 2] int32: element [l, 0] holds layer l's live tiers (2 | 4 | 8)
     decode: tuple | None  # (query rows, block-table rows, lengths), [n_dec] each; None: no decode entry
     tok: torch.Tensor  # [4, n_tokens] (row stride = capacity): slot, residual slot, sealed, K_ref row
     fin: torch.Tensor  # [fin rows, 3 + k_group]; the first n_fin are this step's
@@ -69,7 +70,7 @@ class StepDriver:
         self.nq = canary_slots
         self.w = 3 + shared.planner.g
         self.device = torch.device(device)
-        head = 2 + self.nq + self.nq % 2 + 7 * self.cap + self.cap * self.w
+        head = 2 + self.nq + self.nq % 2 + self.n_layers + self.n_layers % 2 + 7 * self.cap + self.cap * self.w
         tail = self.cap * (5 + 2 * self.n_layers) + 6 * self.n_layers * 8 + 64
         self.words = head + tail
         self.dev = torch.zeros(self.words, dtype=torch.int64, device=self.device)
@@ -161,6 +162,7 @@ class StepDriver:
         return StepUpload(
             fin_count=head[0:1],
             canary_rows=head[v.o_canary : v.o_canary + self.nq],
+            tier_masks=head[v.o_mask : v.o_mask + self.n_layers].view(torch.int32).view(self.n_layers, 2),
             decode=dec,
             tok=head[v.o_tok : v.o_tok + 4 * v.rows_tok].view(4, v.rows_tok)[:, : v.n_tokens],
             fin=head[v.o_fin : v.o_fin + v.rows_fin * self.w].view(v.rows_fin, self.w),

@@ -139,7 +139,13 @@ int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* b
  * length, so a sequence's result does not depend on the rest of the batch. tier
  * (2, 4 or 8) selects the kernel specialised for the layer's tier; blocks stored at
  * another tier, and each block's open K group, are still read correctly on a slower
- * path. Layouts: head_size 64 or 128 with v_group >= head_size / 16, k_group >= 16,
+ * path. tier_mask (device int32, or NULL) names the tiers the layer holds blocks at,
+ * as a bit set of tier values (2 | 4 | 8; 0 reads as `tier` alone), read when the
+ * kernels run (a captured graph follows it): the kernel of each of those tiers runs
+ * that tier's blocks on its own fast path, one after another into the same
+ * partial rows, and one merge follows. It needs ECHOKV_DECODE_BATCH_INVARIANT
+ * (the split schedule), and a sequence's result still depends on its own blocks
+ * only. Layouts: head_size 64 or 128 with v_group >= head_size / 16, k_group >= 16,
  * power-of-two block_size and k_group and <= 4 chunks per page run on the MFMA
  * kernels; any other layout (head_size up to 256) on an fp32 kernel with the split
  * schedule (flags and tier then select nothing).
@@ -151,8 +157,8 @@ int echokv_decode(const echokv_layout* L, const uint8_t* pages, const int64_t* b
                   const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
                   const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs,
                   float softmax_scale, int32_t num_splits, int32_t blocks_per_split, int32_t tier,
-                  int32_t flags, float* acc, float* ml, void* out, int64_t o_s0, int64_t o_s1,
-                  int32_t out_dtype, echokv_stream_t stream);
+                  const int32_t* tier_mask, int32_t flags, float* acc, float* ml, void* out, int64_t o_s0,
+                  int64_t o_s1, int32_t out_dtype, echokv_stream_t stream);
 
 /* Rows of the acc / ml workspaces that echokv_decode uses with these arguments,
  * for any tier: num_seqs * num_splits for the split schedule, two per range of the
@@ -176,8 +182,8 @@ int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int
                          const int64_t* q_rows, const int32_t* block_table, int64_t bt_s0,
                          const int64_t* bt_rows, const int64_t* seq_lens, int64_t num_seqs,
                          float softmax_scale, int32_t num_splits, int32_t blocks_per_split, int32_t tier,
-                         int32_t flags, void* out, int64_t o_s0, int64_t o_s1, int32_t out_dtype,
-                         echokv_stream_t stream);
+                         const int32_t* tier_mask, int32_t flags, void* out, int64_t o_s0, int64_t o_s1,
+                         int32_t out_dtype, echokv_stream_t stream);
 
 /* Chunked-prefill attention over the tiered pages (MFMA tiles), bottom-right causal:
  * tiles [n_tiles, 5] int32 = (first query row, tokens, first query position, ctx,

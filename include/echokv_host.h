@@ -114,6 +114,7 @@ typedef struct ekh_batch {
  * much of it the step uses. The image:
  *   [0] fin rows, [1] token rows;
  *   canary rows [canary_slots] at o_canary;
+ *   each layer's tiers with live blocks, as 2 | 4 | 8 (one word per layer) at o_mask;
  *   decode query rows, block-table rows, lengths (rows_dec each) at o_dec;
  *   token rows: slot, residual slot, sealed, K_ref row (rows_tok each) at o_tok;
  *   fin rows [rows_fin, 3 + k_group] at o_fin;
@@ -126,7 +127,7 @@ typedef struct ekh_batch {
  * (graph_rows = 1) rows_* equal the capacity, so everything up to o_res sits at
  * fixed offsets. */
 typedef struct ekh_step_view {
-  int64_t step, len, o_canary, o_dec, o_tok, o_fin, o_res, o_grp, o_open, o_hdr, o_seal;
+  int64_t step, len, o_canary, o_mask, o_dec, o_tok, o_fin, o_res, o_grp, o_open, o_hdr, o_seal;
   int64_t rows_dec, rows_tok, rows_fin;
   int64_t n_dec, n_tokens, n_fin, n_res, n_grp, n_open, n_seal, n_canary, decode_only, graph_rows;
   double canary_ctx;          /* mean context of the canary's requests */

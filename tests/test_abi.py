@@ -60,11 +60,11 @@ def _layout(**kw):
     return L
 
 
-def _decode(lib, L, tier=4, splits=4, seqs=1, flags=0):
+def _decode(lib, L, tier=4, splits=4, seqs=1, flags=0, tier_mask=None):
     res = _lib.Residual(C.c_void_p(16), 1, 2, 16 * 8 * 128, 8 * 128, 128)
     p = C.c_void_p(64)  # never dereferenced: every call below fails its checks first
     return lib.echokv_decode(C.byref(L), p, p, p, C.byref(res), p, 4096, 128, 1, 32, None, p, 64, None, p, seqs,
-                             0.088, splits, 16, tier, flags, p, p, p, 4096, 128, 1, None)
+                             0.088, splits, 16, tier, tier_mask, flags, p, p, p, 4096, 128, 1, None)
 
 
 def _layout_of(head_size=128, block_size=16, k_group=16, v_group=32):
@@ -83,6 +83,9 @@ def test_decode_rejects_bad_arguments_before_launching(lib):
     assert _decode(lib, _layout(), splits=0) != 0
     assert _decode(lib, _layout(), seqs=-1) != 0
     assert _decode(lib, _layout(), flags=2) != 0              # unknown schedule flag
+    # Tier passes continue partial rows: the split schedule only.
+    assert _decode(lib, _layout(), seqs=0, tier_mask=C.c_void_p(64)) == 1
+    assert _decode(lib, _layout(), seqs=0, tier_mask=C.c_void_p(64), flags=_lib.DECODE_BATCH_INVARIANT) == 0
     assert _decode(lib, _layout(), seqs=0) == 0              # nothing to do: no launch
 
 

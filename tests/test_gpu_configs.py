@@ -28,6 +28,7 @@ import numpy as np
 import pytest
 import torch
 
+from echokv_amd import _lib
 from echokv_amd.canary import canary_kl
 from echokv_amd.kernels import decode as dec
 from echokv_amd.kernels import prefill as pf
@@ -449,3 +450,88 @@ def test_decode_over_a_layer_view_spanning_more_than_4_gib(device, bits):
         ref[i] = OA.attend(q[i].float().cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), d ** -0.5)
     check(f"> 4 GiB view int{bits}", got, ref)
     del backing
+
+
+# ---- layers holding several tiers: tier passes -------------------------------------------
+
+def build_mixed_layer(device, lens, cuts, tiers, *, h=8, d=128, bs=16, kg=16, vg=32, seed=5):
+    """A layer written in len(tiers) steps: sequence i's tokens [cuts[j][i], cuts[j+1][i])
+    at tiers[j] (block-aligned cuts, so each block keeps the tier it opened at, as
+    after a controller's tier change). K carries 1% outlier channels x10."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, np.int64)
+    table, nb = block_table(rng, lens, bs)
+    layout = TieredLayout(h, d, bs, 8, kg, vg)
+    pages = torch.zeros(nb, bs * TieredLayout.per_token_bytes(h, d, 8, kg, vg), dtype=torch.uint8, device=device)
+    store = TieredKVCache(layout, pages, residual_slots=len(lens) + 16, residual_dtype=torch.float16)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    out_ch = torch.randperm(h * d, generator=gen, device=device)[: round(0.01 * h * d)]
+    for j, bits in enumerate(tiers):
+        slots = slots_of(table, lens, lambda i, n: np.arange(cuts[j][i], cuts[j + 1][i]), bs)
+        if not slots.size:
+            continue
+        k = torch.randn(slots.size, h, d, generator=gen, device=device)
+        k.view(slots.size, h * d)[:, out_ch] *= 10
+        v = torch.randn(slots.size, h, d, generator=gen, device=device)
+        store.write(k.half(), v.half(), torch.from_numpy(slots).to(device), bits)
+    torch.cuda.synchronize()
+    return store, table
+
+
+def test_mixed_tier_layer_with_tier_passes(device):
+    """A layer holding INT4, INT8 and INT2 blocks (each context: first third INT4,
+    second INT8, rest INT2; one context all INT8, one all INT4), decoded with one
+    pipelined pass per tier (tier_mask), against the oracle: the mask read from the
+    device, a mask naming an absent tier or missing a present one (the lowest pass
+    takes the rest), a sequence alone equal bit for bit to itself in the batch, and a
+    captured graph replayed under changing masks equal to eager calls."""
+    rng = np.random.default_rng(31)
+    lens = rng.integers(100, 3000, 24)
+    c1, c2 = (lens // 3 // 16) * 16, (2 * lens // 3 // 16) * 16
+    c1[0], c2[0] = 0, lens[0]  # all INT8
+    c1[1] = c2[1] = lens[1]    # all INT4
+    store, table = build_mixed_layer(device, lens, [np.zeros_like(lens), c1, c2, lens], [4, 8, 2])
+    live = store.pool.live_tiers()
+    print(f"[mixed] live blocks per tier {live}", flush=True)
+    assert all(live[b] for b in (2, 4, 8))
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    lens_d = torch.from_numpy(lens).to(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(32)
+    q = torch.randn(len(lens), 32, 128, device=device, generator=gen).half()
+    scale = 128 ** -0.5
+    ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, scale, vectorized=True)
+    ns = dec.default_splits(table_d, 16, 16, None)
+
+    def run(mask, qq=q, tb=table_d, ln=lens_d, **kw):
+        return dec.decode_attention(store, qq, tb, ln, scale, tier=4, tier_mask=mask, num_splits=ns, **kw)
+
+    full = torch.tensor([2 | 4 | 8], dtype=torch.int32, device=device)
+    got = run(full)
+    check("mixed tiers, passes 2|4|8", got, ref)
+    check("mixed tiers, passes from the pool", run("auto"), ref)
+    for m in (4 | 8, 2 | 4, 8, 0):  # a present tier without a pass: the lowest pass's generic path
+        check(f"mixed tiers, mask {m}", run(torch.tensor([m], dtype=torch.int32, device=device)), ref)
+    check("mixed tiers, one pass (no mask)", run(None), ref)
+    for i in (0, 1, 5):
+        alone = run(full, q[i : i + 1], table_d[i : i + 1], lens_d[i : i + 1])
+        assert torch.equal(alone[0], got[i]), f"sequence {i}: alone differs from in the batch"
+
+    mask = full.clone()
+    out = torch.empty_like(got)
+    rows = dec.workspace_rows(store, 32, q.dtype, len(lens), ns, _lib.DECODE_BATCH_INVARIANT)
+    ws = (torch.empty(rows, 32, 128, device=device), torch.empty(rows, 32, 2, device=device))
+    run(mask, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(mask, out=out, workspace=ws)
+    for m in (2 | 4 | 8, 4 | 8, 4, 0, 2 | 4 | 8):
+        mask.fill_(m)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = run(torch.tensor([m], dtype=torch.int32, device=device))
+        assert torch.equal(out, eager), f"graph replay with mask {m} differs from the eager call"
+        check(f"mixed tiers, graph replay, mask {m}", out, ref)

@@ -141,6 +141,8 @@ def test_stepper_equals_the_planner_and_pools_composed(bs, kg, mem, slots, seed)
             assert np.array_equal(old.pools[li].tag_h, new.pools[li].tag_h), msg
             assert old.pools[li].free == new.pools[li].free, msg
             assert old.pools[li].live_tiers() == new.pools[li].live_tiers(), msg
+            live = old.pools[li].live_tiers()  # the tiers the layer's decode runs passes for
+            assert int(up.tier_masks[li, 0]) == sum(b for b in (2, 4, 8) if live[b]), msg
         assert np.array_equal(old.shared.cum_h, new.shared.cum_h) and np.array_equal(old.shared.last_h,
                                                                                       new.shared.last_h), msg
 
@@ -178,8 +180,10 @@ def test_graph_visible_parts_keep_their_addresses():
                    False)
     b = driver.run(np.array([0, 1, 2, 3], np.int32), np.array([2, 2, 1], np.int32), np.array([1, 17, 32], np.int64),
                    tiers, True)
-    for x, y in ((a.tok, b.tok), (a.fin, b.fin), (a.fin_count, b.fin_count), (a.canary_rows, b.canary_rows)):
+    for x, y in ((a.tok, b.tok), (a.fin, b.fin), (a.fin_count, b.fin_count), (a.canary_rows, b.canary_rows),
+                 (a.tier_masks, b.tier_masks)):
         assert x.data_ptr() == y.data_ptr()
+    assert a.tier_masks[:, 0].tolist() == [4, 8]  # each layer opened its blocks at its own tier
     assert a.decode[0].data_ptr() == b.decode[0].data_ptr() and a.decode[2].data_ptr() == b.decode[2].data_ptr()
     assert a.tok.stride(0) == b.tok.stride(0) == 8  # token rows stride by the capacity
     assert b.decode[2].tolist() == [2, 2, 1] and b.canary_rows.tolist() == [0, 1, 2] and b.n_canary == 3
