@@ -134,16 +134,26 @@ class DecodeWork:
     workspace: tuple | None  # (acc, ml) shared by every layer; None: the call allocates
     batch_invariant: bool
     tier_masks: torch.Tensor | None = None  # [layers, 2] int32: each layer's live tiers, read by the kernels
+    host_tier_masks: np.ndarray | None = None  # [layers] the same, on the host
 
     def run(self, impl, query: torch.Tensor, block_table: torch.Tensor, out: torch.Tensor) -> None:
-        # On the split schedule each tier the layer holds runs on its own fast path
-        # (the mask is read when the kernels run, so a replayed graph follows it).
-        mask = None
+        # On the split schedule each tier the layer holds runs on its own fast path:
+        # under graph capture through the device mask (read when the kernels run, so
+        # a replayed graph follows the layer's tiers); eagerly, a layer holding one
+        # tier runs that tier's kernel alone.
+        tier, mask = impl.decode_tier(), None
         if self.batch_invariant and self.tier_masks is not None:
-            mask = self.tier_masks[impl.group_index, :1]
+            if _capturing(query):
+                mask = self.tier_masks[impl.group_index, :1]
+            else:
+                held = int(self.host_tier_masks[impl.group_index])
+                if held & (held - 1):
+                    mask = self.tier_masks[impl.group_index, :1]
+                elif held:
+                    tier = held
         dec.decode_attention(impl.store, query, block_table, self.lens, impl.scale, q_rows=self.rows,
                              bt_rows=self.reqs, out=out, num_splits=self.num_splits, workspace=self.workspace,
-                             tier=impl.decode_tier(), batch_invariant=self.batch_invariant, tier_mask=mask)
+                             tier=tier, batch_invariant=self.batch_invariant, tier_mask=mask)
 
 
 @dataclass
@@ -340,6 +350,7 @@ class EchoKVMetadataBuilder(AttentionMetadataBuilder):
         if up.decode is not None:
             n_dec = up.decode[0].numel()
             md.decode = DecodeWork(*up.decode, num_splits=self.num_splits, tier_masks=up.tier_masks,
+                                   host_tier_masks=up.host_tier_masks,
                                    workspace=group.impls[0].decode_workspace(n_dec, self.num_splits, self.cap),
                                    batch_invariant=self.cfg.batch_invariant)
         if up.prefill:

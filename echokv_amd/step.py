@@ -36,6 +36,7 @@ class StepUpload:
     fin_count: torch.Tensor  # [1]: masks a graph's full-grid finalize
     canary_rows: torch.Tensor  # [canary slots] query rows the canary reads on a fire step
     tier_masks: torch.Tensor  # [layers, 2] int32: element [l, 0] holds layer l's live tiers (2 | 4 | 8)
+    host_tier_masks: np.ndarray  # [layers] the same on the host
     decode: tuple | None  # (query rows, block-table rows, lengths), [n_dec] each; None: no decode entry
     tok: torch.Tensor  # [4, n_tokens] (row stride = capacity): slot, residual slot, sealed, K_ref row
     fin: torch.Tensor  # [fin rows, 3 + k_group]; the first n_fin are this step's
@@ -163,6 +164,7 @@ class StepDriver:
             fin_count=head[0:1],
             canary_rows=head[v.o_canary : v.o_canary + self.nq],
             tier_masks=head[v.o_mask : v.o_mask + self.n_layers].view(torch.int32).view(self.n_layers, 2),
+            host_tier_masks=np.ctypeslib.as_array(v.image, shape=(v.o_mask + self.n_layers,))[v.o_mask :].copy(),
             decode=dec,
             tok=head[v.o_tok : v.o_tok + 4 * v.rows_tok].view(4, v.rows_tok)[:, : v.n_tokens],
             fin=head[v.o_fin : v.o_fin + v.rows_fin * self.w].view(v.rows_fin, self.w),

@@ -209,6 +209,14 @@ def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
         lens = new_lens
         check_decode(layers, table_np, lens, q, outs, f"eager decode {step}")
 
+    # Each layer's controller moves to another tier before the graph is captured:
+    # the blocks opened from now on (request 3 crosses a block boundary during the
+    # replayed steps) take the new tier, so the layers come to hold two tiers after
+    # capture, and the replayed decode follows the step's device tier masks.
+    for layer, bits in zip(layers, (8, 2, 4)):
+        layer.impl.controller.bits = bits
+    held_before = [sum(b for b, n in l.impl.store.pool.live_tiers().items() if n) for l in layers]
+
     # Steps 4-9: one graph captured at the decode shape, replayed with fresh metadata.
     sq, sk, sv = rand(pad, HQ), rand(pad, H), rand(pad, H)
     souts = [torch.zeros(pad, HQ * D, device=device, dtype=torch.float16) for _ in range(LAYERS)]
@@ -235,6 +243,10 @@ def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
         canary.after_step(md)
         lens = new_lens
         check_decode(layers, table_np, lens, sq, souts, f"graph decode {step}")
+    held_after = [sum(b for b, n in l.impl.store.pool.live_tiers().items() if n) for l in layers]
+    print(f"[backend] tiers held by each layer: {held_before} before the graph, {held_after} after", flush=True)
+    assert any(a & (a - 1) and not (b & (b - 1)) for a, b in zip(held_after, held_before)), \
+        "a layer came to hold two tiers during the replayed steps"
     assert canary.checked >= 2, "the canary fired and was scored, eagerly and from graph-replayed steps"
     assert all(l.impl.controller.fires >= 1 for l in layers), "every controller observed a δ̂"
     for layer in layers:

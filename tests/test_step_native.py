@@ -143,6 +143,7 @@ def test_stepper_equals_the_planner_and_pools_composed(bs, kg, mem, slots, seed)
             assert old.pools[li].live_tiers() == new.pools[li].live_tiers(), msg
             live = old.pools[li].live_tiers()  # the tiers the layer's decode runs passes for
             assert int(up.tier_masks[li, 0]) == sum(b for b in (2, 4, 8) if live[b]), msg
+            assert int(up.host_tier_masks[li]) == int(up.tier_masks[li, 0]), msg
         assert np.array_equal(old.shared.cum_h, new.shared.cum_h) and np.array_equal(old.shared.last_h,
                                                                                       new.shared.last_h), msg
 
