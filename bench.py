@@ -4,7 +4,7 @@ quantized KV cache on one MI355X.
 32 layers, each Hq=32 / H=8 / D=128, page block 16, K group 16, V group 32,
 mem_bits 8 pages; tier vector = a seeded permutation of 8 x INT8, 16 x INT4,
 8 x INT2; batch 64 with context lengths ~U[512, 8192] (seed 1); fp16 K/V/Q
-~N(0,1) with 1% of K (head, channel) pairs x10 (outliers). One step = for
+~N(0,1) with 1% of the K and of the V (head, channel) pairs x10 (outliers). One step = for
 every layer, quantize-on-write of one new token per sequence (the fused write
 step: finalize of the completing K groups and the token rows in one launch) then
 decode attention (balanced schedule: decode + merge), all on the device; the host
@@ -113,6 +113,8 @@ def build_state(dev, steps_total: int, seed: int = 1):
         v = torch.randn(pre.size, H, D, device=dev, dtype=torch.float16, generator=gen)
         out_ch = torch.randperm(H * D, generator=gen, device=dev)[: round(0.01 * H * D)]
         k.view(pre.size, H * D)[:, out_ch] *= 10
+        v_ch = torch.randperm(H * D, generator=gen, device=dev)[: round(0.01 * H * D)]
+        v.view(pre.size, H * D)[:, v_ch] *= 10
         st.apply(meta, k, v, krefs[li])
         del k, v
     torch.cuda.synchronize()
@@ -285,7 +287,7 @@ def run(args) -> dict:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u8 codes (INT4) -> fp16 MFMA, fp32 accumulate",
-        "data": "synthetic: fp16 K/V/Q ~N(0,1), 1% K channels x10; random block tables",
+        "data": "synthetic: fp16 K/V/Q ~N(0,1), 1% of K and of V channels x10; random block tables",
         "config": {
             "workload": "cfg2: Llama-3.1-8B-shaped decode, 32 layers (8 INT8 / 16 INT4 / 8 INT2), batch 64, "
                         "ctx ~U[512,8192], Hq 32 / H 8 / D 128, page block 16, K group 16, V group 32",
@@ -543,7 +545,7 @@ def run_cfg4(reps: int = 5) -> dict:
     Hq 64 / H 8 / D 128 (GQA 8), page block 16, K group 16, V group 32, mem_bits 8
     pages (about 102 GB), 16 sequences of 32768 tokens. Every layer's context is
     written through the quantize-on-write path (one synthetic K/V set, fp16
-    ~N(0,1), 1% of K channels x10, reused by every layer), then each tier's layers'
+    ~N(0,1), 1% of K and of V channels x10, reused by every layer), then each tier's layers'
     decode (decode + merge) is captured as one HIP graph and replayed ``reps`` times
     between HIP events; the canary fires once over the 80 layers (8 query rows,
     the 64-key K_ref window, tiers 2 / 4 / 8), as on every 64th step."""
@@ -589,6 +591,8 @@ def run_cfg4(reps: int = 5) -> dict:
     v = torch.randn(pre.size, H, D, device=dev, dtype=torch.float16, generator=gen)
     out_ch = torch.randperm(H * D, generator=gen, device=dev)[: round(0.01 * H * D)]
     k.view(pre.size, H * D)[:, out_ch] *= 10
+    v_ch = torch.randperm(H * D, generator=gen, device=dev)[: round(0.01 * H * D)]
+    v.view(pre.size, H * D)[:, v_ch] *= 10
     for li, (st, op, kr) in enumerate(zip(stores, opened, krefs)):
         if op is not None:
             st.write_headers(torch.from_numpy(op[0]).to(dev), torch.from_numpy(op[1]).to(dev))
@@ -660,7 +664,7 @@ def run_cfg4(reps: int = 5) -> dict:
         "per_tier": per_tier,
         "canary_us_per_fire_80_layers": round(canary_us, 1),
         "setup_s": round(setup_s, 1),
-        "data": "synthetic: fp16 K/V ~N(0,1), 1% K channels x10 (one set for all layers), random block tables",
+        "data": "synthetic: fp16 K/V ~N(0,1), 1% of K and of V channels x10 (one set for all layers), random block tables",
     }
 
 

@@ -535,3 +535,31 @@ def test_mixed_tier_layer_with_tier_passes(device):
         eager = run(torch.tensor([m], dtype=torch.int32, device=device))
         assert torch.equal(out, eager), f"graph replay with mask {m} differs from the eager call"
         check(f"mixed tiers, graph replay, mask {m}", out, ref)
+
+
+@pytest.mark.parametrize("d,gqa,qdt,ws", [(64, 4, torch.float16, None), (128, 4, torch.float32, None),
+                                          (128, 20, torch.float16, None), (128, 4, torch.float16, "static")])
+def test_tier_passes_at_other_shapes(device, d, gqa, qdt, ws):
+    """Tier passes at head size 64, with float32 queries (the query hi / lo path), at
+    GQA 20 (query heads in groups of 16, each group its own passes) and on the
+    library's static workspace: against the oracle, and equal to themselves when a
+    sequence is decoded alone."""
+    h = 4
+    rng = np.random.default_rng(40 + d + gqa)
+    lens = rng.integers(60, 1500, 12)
+    c1, c2 = (lens // 3 // 16) * 16, (2 * lens // 3 // 16) * 16
+    store, table = build_mixed_layer(device, lens, [np.zeros_like(lens), c1, c2, lens], [8, 2, 4], h=h, d=d, seed=41)
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    lens_d = torch.from_numpy(lens).to(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(42)
+    q = torch.randn(len(lens), h * gqa, d, device=device, generator=gen).to(qdt)
+    ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, d ** -0.5, vectorized=True)
+    mask = torch.tensor([2 | 4 | 8], dtype=torch.int32, device=device)
+    ns = dec.default_splits(table_d, 16, 16, None)
+    kw = dict(tier=4, tier_mask=mask, num_splits=ns, workspace=ws)
+    got = dec.decode_attention(store, q, table_d, lens_d, d ** -0.5, **kw)
+    check(f"tier passes D{d} GQA{gqa} {str(qdt)[6:]}{' static' if ws else ''}", got, ref)
+    alone = dec.decode_attention(store, q[3:4], table_d[3:4], lens_d[3:4], d ** -0.5, **kw)
+    assert torch.equal(alone[0], got[3])
