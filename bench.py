@@ -325,6 +325,7 @@ def run(args) -> dict:
         res["prefill"] = run_prefill()
     if not args.no_mixed:
         res["mixed_tier"] = run_mixed()
+        res["head_size_256"] = run_d256()
     return res
 
 
@@ -537,6 +538,78 @@ def run_mixed(reps: int = 20) -> dict:
         b = mixed_bytes if name == "mixed" else alg_bytes(ctx, tier)
         r["decode_us"][label] = {"us": round(us, 1), "GBs": round(b / us / 1e3, 1)}
     return r
+
+
+def run_d256(reps: int = 10) -> dict:
+    """Head size 256 (the MFMA kernel at 128 channels, each KV head as two half-heads
+    whose waves add their partial scores): one INT4 layer of 64 sequences x ctx
+    U[512, 8192], H 8 / Hq 32, page block 16, K group 16, V group 32, against the same
+    contexts at head size 128."""
+    import torch
+
+    from echokv_amd.kernels.decode import decode_attention
+    from echokv_amd.tiered_cache import TieredKVCache, TieredLayout
+    from echokv_amd.write_plan import SharedState, stage_plan
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(13)
+    ctx = rng.integers(512, 8193, S).astype(np.int64)
+    nbs = -(-ctx // BS)
+    nb = int(nbs.sum()) + 16
+    perm = rng.permutation(nb)
+    table = np.zeros((S, int(nbs.max())), np.int64)
+    o = 0
+    for i, n in enumerate(nbs):
+        table[i, :n] = perm[o : o + n]
+        o += n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(14)
+    table_d = torch.from_numpy(table).to(dev, torch.int32)
+    lens_d = torch.from_numpy(ctx).to(dev)
+    out = {}
+    for d in (256, 128):
+        layout = TieredLayout(H, d, BS, MEM, KG, VG)
+        shared = SharedState(nb, BS, KG, S + 16, kref_window=64, device=dev)
+        res = torch.zeros(S + 17, KG, H, d, dtype=torch.float16, device=dev)
+        st = TieredKVCache(layout, layout.alloc_pages(nb, dev), residual=res, shared=shared)
+        slots = np.concatenate([table[i][np.arange(n) // BS] * BS + np.arange(n) % BS for i, n in enumerate(ctx)])
+        plan = shared.planner.plan(slots)
+        op = st.prepare(plan, 4)
+        shared.commit(plan)
+        meta, extra = stage_plan(plan, dev, None)
+        shared.apply_res_map(*extra[:4])
+        if op is not None:
+            st.write_headers(torch.from_numpy(op[0]).to(dev), torch.from_numpy(op[1]).to(dev))
+        k = torch.randn(slots.size, H, d, device=dev, dtype=torch.float16, generator=gen)
+        v = torch.randn(slots.size, H, d, device=dev, dtype=torch.float16, generator=gen)
+        st.apply(meta, k, v, torch.zeros(64, H, d, device=dev))
+        del k, v
+        q = torch.randn(S, HQ, d, device=dev, dtype=torch.float16, generator=gen)
+        o16 = torch.empty(S, HQ, d, device=dev, dtype=torch.float16)
+
+        def go():
+            decode_attention(st, q, table_d, lens_d, d ** -0.5, out=o16, tier=4)
+
+        go()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            go()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        b = alg_bytes(ctx, 4) * d // D  # every per-token term scales with the head size
+        out[f"D{d}"] = {"kernel": "decode_kernel<128, 4> (MFMA, split)" + (", half-heads" if d == 256 else ""),
+                        "us_per_layer": round(us, 1), "GBs": round(b / us / 1e3, 1)}
+        del st, shared, res
+    return {"workload": "one INT4 layer, 64 x ctx U[512, 8192], H 8 / Hq 32, default (batch-invariant) schedule",
+            **out}
 
 
 def run_cfg4(reps: int = 5) -> dict:

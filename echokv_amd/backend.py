@@ -60,9 +60,10 @@ from echokv_amd.step import StepDriver
 from echokv_amd.tiered_cache import HeaderWriter, TieredKVCache, TieredLayout
 from echokv_amd.write_plan import SharedState, WriteMeta
 
-# Head sizes the MFMA kernels are built for; others up to MAX_HEAD_SIZE take the
-# fp32 kernels.
-KERNEL_HEAD_SIZES = (64, 128)
+# Head sizes the MFMA decode kernels take (256 as two 128-channel half-heads);
+# others up to MAX_HEAD_SIZE take the fp32 kernels. Prefill's MFMA kernels take 64
+# and 128.
+KERNEL_HEAD_SIZES = (64, 128, 256)
 MAX_HEAD_SIZE = 256
 # Upper bound on decode splits per sequence (a fixed grid, so a graph replays it).
 MAX_DECODE_SPLITS = dec.MAX_SPLITS

@@ -164,13 +164,28 @@ int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* b
 namespace {
 
 // The MFMA decode kernels take: D 64 or 128 with at least D/16 channels per V
-// group, 16-token tiles inside one K group (one k_scale / k_min row per tile),
-// power-of-two block size and K group, <= 4 chunks per page. Any other layout
-// takes decode_any.
+// group, or D 256 as half-heads of 128 (V groups of 8 to 128 channels: each
+// inside one half), 16-token tiles inside one K group (one k_scale / k_min row per
+// tile), power-of-two block size and K group, <= 4 chunks per page. Any other
+// layout takes decode_any.
 bool decode_mfma(const echokv_layout* L) {
   const bool pow2 = !(L->block_size & (L->block_size - 1)) && !(L->k_group & (L->k_group - 1));
-  return (L->head_size == 64 || L->head_size == 128) && L->v_group % (L->head_size / 16) == 0 &&
-         L->k_group >= 16 && pow2 && L->chunks_per_page <= 4 && L->num_blocks * L->chunks_per_page < (1LL << 24);
+  const int D = L->head_size, VG = L->v_group;
+  const bool heads = D == 256 ? VG <= 128 && VG % 8 == 0 : (D == 64 || D == 128) && VG % (D / 16) == 0;
+  return heads && L->k_group >= 16 && pow2 && L->chunks_per_page <= 4 &&
+         L->num_blocks * L->chunks_per_page < (1LL << 24);
+}
+
+// The layout the MFMA kernels are given: head size 256 as 2H half-heads of 128
+// channels (DecodeArgs::pair; the same page bytes), any other as it is.
+void decode_view(const echokv_layout* L, ek::DecodeArgs& a) {
+  a.L = to_lay(L);
+  a.pair = 0;
+  if (L->head_size == 256 && decode_mfma(L)) {
+    a.L.H = 2 * L->num_kv_heads;
+    a.L.D = L->head_size / 2;
+    a.pair = 1;
+  }
 }
 
 // echokv_decode and echokv_decode_static: the checks, then decode + merge with
@@ -196,7 +211,7 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   if (!pages || !block_res || !res_group || !query || !block_table || !seq_lens || !out) return ECHOKV_EINVAL;
   if (!static_scratch && (!acc || !ml)) return ECHOKV_EINVAL;
   ek::DecodeArgs a;
-  a.L = to_lay(L);
+  decode_view(L, a);
   a.pages = pages;
   a.block_res = block_res;
   a.res_group = res_group;
@@ -318,7 +333,7 @@ int64_t echokv_decode_workspace_rows(const echokv_layout* L, int32_t num_q_heads
   // Balanced schedule: two partial slots per range; the range count depends on the
   // tier's kernel (its occupancy), so the largest over the tiers.
   ek::DecodeArgs a;
-  a.L = to_lay(L);
+  decode_view(L, a);
   a.q_dtype = q_dtype;
   a.num_seqs = num_seqs;
   a.num_splits = num_splits;

@@ -177,6 +177,13 @@ struct DecodeArgs {
   // continue the span's partial result that the pass before them left.
   const int32_t* tier_mask;
   int tier0;
+  // 1: head size 256 run as half-heads. L is then the layer seen as 2 * H heads of
+  // D / 2 channels (the same bytes: a token row holds each head's codes, and each
+  // statistic array each head's channels or V groups, side by side), and half-heads
+  // 2k and 2k + 1 are the channel halves of KV head k: they share its query heads,
+  // add their partial scores before the softmax, and write the two halves of its
+  // rows (acc rows then hold 2 * L.D floats).
+  int pair;
   // log2 of block size, K group and V group (powers of two), and a reciprocal for
   // chunk id / chunks_per_page: floor(id / KC) = umulhi(id, kc_mul) (kc_mul 0: KC = 1).
   int bs_shift, kg_shift, vg_shift;

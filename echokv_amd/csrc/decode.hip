@@ -344,16 +344,17 @@ __device__ __forceinline__ void s_block(const Wave<D, QLO>& w, const uint32_t* k
 // S^T of a tile whose keys are the block's open K group, read from the
 // full-precision residual (row = token % KG) and split into fp16 hi + lo
 // (fp16 / bf16 keys are exact in fp16: lo = 0 is skipped). Lane (c, n): token
-// t0 + n, channels [c * D/4, (c+1) * D/4), eight at a time. The residual's dtype
-// is a template parameter, so every row load issues before the first MFMA waits.
+// t0 + n, channels [c * D/4, (c+1) * D/4), eight at a time, of the head whose
+// channels start rh elements into a residual row. The residual's dtype is a
+// template parameter, so every row load issues before the first MFMA waits.
 template <int D, bool QLO, int RDT>
-__device__ __forceinline__ void s_from_residual(const Wave<D, QLO>& w, const DecodeArgs& a, long rslot, int t0, int h,
-                                                int lane, f4_t& s) {
+__device__ __forceinline__ void s_from_residual(const Wave<D, QLO>& w, const DecodeArgs& a, long rslot, int t0,
+                                                long rh, int lane, f4_t& s) {
   constexpr int CPL = D / 4, NJ = D / 32;
   // Rows loaded together: f32 rows take twice the registers, and hi + lo halves.
   constexpr int STEP = RDT == ECHOKV_F32 ? 2 : NJ;
   const int c = lane >> 4, n = lane & 15;
-  const long r0 = rslot * a.res.s0 + (long)((t0 + n) & (a.L.KG - 1)) * a.res.s1 + h * a.res.s2 + c * CPL;
+  const long r0 = rslot * a.res.s0 + (long)((t0 + n) & (a.L.KG - 1)) * a.res.s1 + rh + c * CPL;
 #pragma unroll
   for (int j0 = 0; j0 < NJ; j0 += STEP) {
     h8_t kh[STEP], kl[STEP];
@@ -523,12 +524,13 @@ __device__ __forceinline__ void load_as_bytes(const uint8_t* p, int bits, uint32
 
 // One 16-token tile [t0, t0 + 16) of block `blk` stored at `bits` (any tier):
 // codes are widened to bytes and go through the 8-bit math. tokens >= n_valid
-// are masked; in_res: the tile is the block's open K group (K from the residual).
+// are masked; in_res: the tile is the block's open K group (K from the residual,
+// head h's channels from element rh of a row).
 // The block header is read once and each part's loads issue together: the tile
 // is a few memory round trips, not one per row.
 template <int D, bool QLO>
 __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs& a, long blk, int t0, int n_valid,
-                                         long rslot, bool in_res, int h, int lane, int bits, float* x,
+                                         long rslot, bool in_res, int h, long rh, int lane, int bits, float* x,
                                          VTile<D / 64>& vt) {
   using W = Wave<D, QLO>;
   constexpr int CPL = W::CPL, NQK = W::NQK, CPM = W::CPM;
@@ -542,9 +544,9 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
   // ---- S^T = K Q'^T (+ bias) -------------------------------------------
   f4_t s = {0.f, 0.f, 0.f, 0.f};
   if (in_res) {
-    if (a.res.dtype == ECHOKV_F16) s_from_residual<D, QLO, ECHOKV_F16>(w, a, rslot, t0, h, lane, s);
-    else if (a.res.dtype == ECHOKV_BF16) s_from_residual<D, QLO, ECHOKV_BF16>(w, a, rslot, t0, h, lane, s);
-    else s_from_residual<D, QLO, ECHOKV_F32>(w, a, rslot, t0, h, lane, s);
+    if (a.res.dtype == ECHOKV_F16) s_from_residual<D, QLO, ECHOKV_F16>(w, a, rslot, t0, rh, lane, s);
+    else if (a.res.dtype == ECHOKV_BF16) s_from_residual<D, QLO, ECHOKV_BF16>(w, a, rslot, t0, rh, lane, s);
+    else s_from_residual<D, QLO, ECHOKV_F32>(w, a, rslot, t0, rh, lane, s);
   } else {
     const long e0 = ((long)(t0 / L.KG) * L.H + h) * D + c * CPL;
     const long rb = row_base_h(L, blk, hd, t0 + n, bits);
@@ -653,6 +655,25 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Workgroup barrier without a memory fence (a fence would wait for the DMAs in
 // flight); the wave's own LDS reads are complete first.
 __device__ __forceinline__ void wg_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Half-heads (DecodeArgs::pair): waves 2k and 2k + 1 of a workgroup hold the two
+// channel halves of one KV head and so each the partial scores of its half. Each
+// adds the other's through LDS: a + b == b + a in IEEE arithmetic, so both waves
+// hold the same scores and run the same softmax. Two buffers, alternated by the
+// exchange count xi: a wave writes buffer xi & 1 only after the barrier of
+// exchange xi - 1, which its partner meets only once its read of exchange xi - 2
+// (the same buffer) has returned. Every wave of the workgroup takes part in every
+// exchange (the barrier is the workgroup's).
+constexpr int kPairLds = 2 * 4 * 4 * 64 * 4;  // [buffer][wave][score][lane] float32
+__device__ __forceinline__ void pair_scores(uint8_t* xch, int& xi, int wv, int lane, float* x) {
+  float* buf = (float*)xch + (xi & 1) * (4 * 4 * 64);
+  ++xi;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) buf[(wv * 4 + i) * 64 + lane] = x[i];
+  wg_barrier();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = x[i] + buf[((wv ^ 1) * 4 + i) * 64 + lane];
+}
 
 template <int D, int BITS>
 struct Ring {
@@ -1068,7 +1089,7 @@ __device__ __forceinline__ void range_priority(int left, int total) {
 
 // Blocks [b_start, b_end) of sequence `seq` for the KV heads of head group hg
 // (one wave per head).
-template <int D, int BITS, bool QLO, bool PASSES>
+template <int D, int BITS, bool QLO, bool PASSES, bool PAIR>
 __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b_start, int b_end, int hg, int wv,
                                             int lane, uint8_t* ring, uint32_t ring0, SpanSink sink,
                                             SpanPass pass = SpanPass{false, true, 0, false}) {
@@ -1081,6 +1102,18 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   const int c = lane >> 4, n = lane & 15;
   const int h = hg * kHeadsPerGroup + wv;
   const bool live = h < L.H;  // a wave past the last head still loads its share of every tile
+  // Half-heads (PAIR, DecodeArgs::pair): KV head kh = h / 2, channels from half * D of its query
+  // and output rows, RD floats per workspace row. A wave past the last head then
+  // computes on its slot's bytes too (never written out), so that every wave meets
+  // every score exchange; its memory reads use the last head (ha).
+  constexpr bool pair = PAIR;
+  const int kh = pair ? h >> 1 : h;
+  const int half = pair ? h & 1 : 0;
+  const int RD = pair ? 2 * D : D;
+  const int ha = live ? h : L.H - 1;
+  const long rh = pair ? (long)(ha >> 1) * a.res.s2 + (ha & 1) * D : (long)ha * a.res.s2;
+  uint8_t* const xch = ring + R::WG_BYTES;  // the score exchange (pair only)
+  int xi = 0;
 
   W w;
   // The first chunk's block table row is requested with the query, so their
@@ -1089,7 +1122,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   BlockLane bl;
   {
     const bool qv = live && n < a.gs;
-    const long qb = q_row * a.q_s0 + (long)(h * a.gqa + a.g0 + (qv ? n : 0)) * a.q_s1 + c * W::CPL;
+    const long qb = q_row * a.q_s0 + (long)(kh * a.gqa + a.g0 + (qv ? n : 0)) * a.q_s1 + half * D + c * W::CPL;
     float xq[W::CPL];
     // Scores are scaled inside the exponent (exp2(s * x - m)); the max is taken
     // on unscaled scores, which needs the scale positive: a negative one flips
@@ -1127,8 +1160,8 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   bool carried = !pass.carry;
   auto load_carry = [&]() {
     if (live && n < a.gs) {
-      const long row = sink.part_row0 + ((long)h * a.gqa + a.g0 + n) * sink.part_stride;
-      const float* src = a.acc + row * D;
+      const long row = sink.part_row0 + ((long)kh * a.gqa + a.g0 + n) * sink.part_stride;
+      const float* src = a.acc + row * RD + half * D;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -1233,18 +1266,19 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
         rare = true;
         continue;
       }
-      if (!live) continue;
+      if (!live && !pair) continue;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
       const int n_valid = seq_len - ((c0 + bo) << a.bs_shift);
       constexpr int VW = W::CPM * BITS / 8 >= 4 ? W::CPM * BITS / 8 / 4 : 1;
       float x[4];
       VTile<VW> vt;
       compute_tile<D, QLO, BITS>(w, a, kc, ring + (tt % R::NBUF) * R::SLOT, n_valid - t0, lane, x, vt);
+      if (pair) pair_scores(xch, xi, wv, lane, x);
       softmax_pv<D, QLO, BITS, VW>(w, x, vt, vscale_mask<BITS>());
     }
     wait_vmcnt<0>();  // nothing of this chunk may still be landing in the ring
     wg_barrier();     // every wave is done reading the ring before the next chunk refills it
-    if (rare && live) {
+    if (rare && (live || pair)) {
 #pragma unroll 1
       for (int tt = 0; tt < n_tiles; ++tt) {
         const int b = tt >> tpb_shift;
@@ -1258,7 +1292,8 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
         const int n_valid = seq_len - ((c0 + orig(b)) << a.bs_shift);
         float x[4];
         VTile<D / 64> vt;  // codes widened to bytes
-        tile_any<D, QLO>(w, a, blk, t0, n_valid, rslot, in_res, h, lane, tier, x, vt);
+        tile_any<D, QLO>(w, a, blk, t0, n_valid, rslot, in_res, ha, rh, lane, tier, x, vt);
+        if (pair) pair_scores(xch, xi, wv, lane, x);
         softmax_pv<D, QLO, 8, D / 64>(w, x, vt,
                                       tier == 8 ? vscale_mask<8>() : (tier == 4 ? vscale_mask<4>() : vscale_mask<2>()));
       }
@@ -1270,10 +1305,10 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
 #pragma unroll
   for (int j = 0; j < W::CPM; ++j) w.acc[j] += w.acc_m;  // the V min term, the same for the lane's channels
   if (live && n < a.gs) {
-    const long qh = (long)h * a.gqa + a.g0 + n;
-    if (sink.direct) {  // lane (c, n): channels (4c + i) * CPM + j of query head qh
+    const long qh = (long)kh * a.gqa + a.g0 + n;
+    if (sink.direct) {  // lane (c, n): channels (4c + i) * CPM + j of query head qh (of its half)
       const float inv = 1.0f / l;
-      const long o = q_row * a.o_s0 + qh * a.o_s1;
+      const long o = q_row * a.o_s0 + qh * a.o_s1 + half * D;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v[W::CPM];
@@ -1284,13 +1319,13 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
       return;
     }
     const long row = sink.part_row0 + qh * sink.part_stride;
-    float* dst = a.acc + row * D;
+    float* dst = a.acc + row * RD + half * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int j = 0; j < W::CPM; ++j) dst[(4 * c + i) * W::CPM + j] = w.acc[j][i];
     }
-    if (c == 0) {
+    if (c == 0 && half == 0) {  // the two halves hold the same (max, sum)
       a.ml[row * 2] = w.m_run;
       a.ml[row * 2 + 1] = l;
     }
@@ -1304,7 +1339,8 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
 // and they come last in dispatch order instead of between the busy ones.
 // Three waves per SIMD (<= 168 VGPRs) where the ring leaves LDS for three
 // workgroups per CU; INT8's larger ring and the float32-query variant get two.
-template <int D, int BITS, bool QLO>
+// PAIR: head size 256 as half-heads (DecodeArgs::pair), D = 128.
+template <int D, int BITS, bool QLO, bool PAIR>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
   SpanPass pass{false, true, 0, false};
@@ -1336,7 +1372,7 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   const int bps = split_blocks(a, n_blocks);
   const int b_start = split * bps;
   const int b_end = b_start + bps < n_blocks ? b_start + bps : n_blocks;
-  decode_span<D, BITS, QLO, true>(a, seq, b_start, b_end, (int)(item % n_hg), wv, lane, ring_lds, ring0,
+  decode_span<D, BITS, QLO, true, PAIR>(a, seq, b_start, b_end, (int)(item % n_hg), wv, lane, ring_lds, ring0,
                                   SpanSink{seq * a.hq * a.num_splits + split, a.num_splits, false, 0, 0}, pass);
 }
 
@@ -1399,7 +1435,7 @@ __device__ __forceinline__ void seq_of_block(const DecodeArgs& a, long x, int la
   first = base;
 }
 
-template <int D, int BITS, bool QLO>
+template <int D, int BITS, bool QLO, bool PAIR>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_balanced_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
   const int lane = threadIdx.x & 63;
@@ -1426,7 +1462,7 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
     if (nb > 0) {
       const bool whole = pos == first && end == first + nb;
       const long slot = 2 * r + (pos == lo ? 0 : 1);
-      decode_span<D, BITS, QLO, false>(a, seq, (int)(pos - first), (int)(end - first), hg, wv, lane, ring_lds,
+      decode_span<D, BITS, QLO, false, PAIR>(a, seq, (int)(pos - first), (int)(end - first), hg, wv, lane, ring_lds,
                                        ring0, SpanSink{slot * a.hq, 1, whole, (int)(hi - end), (int)(hi - lo)});
     }
     pos = end;
@@ -1579,7 +1615,13 @@ __device__ __forceinline__ void merge_row(const MergeArgs& a, long row, long seq
       for (int u = 0; u < 16; ++u) {
         const long s = g + u < used ? g + u : 0;  // past the last split: split 0, unused
         const float* src = a.acc + (base + s) * D + C * lane;
-        if constexpr (C == 2) {
+        if constexpr (C == 4) {
+          const float4 v = *(const float4*)src;
+          x[u][0] = v.x;
+          x[u][1] = v.y;
+          x[u][2] = v.z;
+          x[u][3] = v.w;
+        } else if constexpr (C == 2) {
           const float2 v = *(const float2*)src;
           x[u][0] = v.x;
           x[u][1] = v.y;
@@ -1652,30 +1694,35 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   merge_row<D>(a, row, seq, head, used, lane);
 }
 
-template <int D, int BITS, bool QLO>
+// Dynamic LDS of a decode workgroup: the ring, and with PAIR the score exchange
+// (every tier's ring leaves room for it at the workgroups per CU the launch bounds give).
+template <int D, int BITS, bool PAIR>
+constexpr int decode_lds() { return Ring<D, BITS>::WG_BYTES + (PAIR ? kPairLds : 0); }
+
+template <int D, int BITS, bool QLO, bool PAIR>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
   const dim3 block(64 * kHeadsPerGroup);
-  const size_t lds = (size_t)Ring<D, BITS>::WG_BYTES;
+  constexpr int lds = decode_lds<D, BITS, PAIR>();
   const long n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
   const long span = 8 * n_hg;  // the kernels permute workgroups within runs of `span`
   if (a.ranges > 0) {
     static std::atomic<uint64_t> attr_done{0};  // devices whose limit is raised, one bit each
-    if (ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO>, (int)lds, &attr_done) != hipSuccess)
+    if (ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO, PAIR>, lds, &attr_done) != hipSuccess)
       return hipErrorInvalidValue;
     const long wgs = (a.ranges * n_hg + span - 1) / span * span;
-    hipLaunchKernelGGL((decode_balanced_kernel<D, BITS, QLO>), dim3((unsigned)wgs), block, lds, s, a);
+    hipLaunchKernelGGL((decode_balanced_kernel<D, BITS, QLO, PAIR>), dim3((unsigned)wgs), block, lds, s, a);
     return hipGetLastError();
   }
   static std::atomic<uint64_t> attr_done{0};
-  if (ensure_lds_limit((const void*)decode_kernel<D, BITS, QLO>, (int)lds, &attr_done) != hipSuccess)
+  if (ensure_lds_limit((const void*)decode_kernel<D, BITS, QLO, PAIR>, lds, &attr_done) != hipSuccess)
     return hipErrorInvalidValue;
   const long items = (a.num_seqs * a.num_splits * n_hg + span - 1) / span * span;
-  hipLaunchKernelGGL((decode_kernel<D, BITS, QLO>), dim3((unsigned)items), block, lds, s, a);
+  hipLaunchKernelGGL((decode_kernel<D, BITS, QLO, PAIR>), dim3((unsigned)items), block, lds, s, a);
   return hipGetLastError();
 }
 
 // Workgroups of the balanced kernel the current device holds at once (cached per device).
-template <int D, int BITS, bool QLO>
+template <int D, int BITS, bool QLO, bool PAIR>
 hipError_t balanced_slots(long& slots) {
   constexpr int kMaxDevices = 64;
   static std::atomic<long> per_device[kMaxDevices];
@@ -1686,13 +1733,14 @@ hipError_t balanced_slots(long& slots) {
   long v = per_device[dev].load(std::memory_order_acquire);
   if (v <= 0) {
     int cus = 0, per_cu = 0;
-    const size_t lds = (size_t)Ring<D, BITS>::WG_BYTES;
+    const size_t lds = (size_t)decode_lds<D, BITS, PAIR>();
     static std::atomic<uint64_t> attr_done{0};
-    if ((e = ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO>, (int)lds, &attr_done)) != hipSuccess)
+    if ((e = ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO, PAIR>, (int)lds, &attr_done)) !=
+        hipSuccess)
       return e;
     if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)decode_balanced_kernel<D, BITS, QLO>,
-                                                          64 * kHeadsPerGroup, lds)) != hipSuccess)
+    if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+             &per_cu, (const void*)decode_balanced_kernel<D, BITS, QLO, PAIR>, 64 * kHeadsPerGroup, lds)) != hipSuccess)
       return e;
     v = (long)(cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
     per_device[dev].store(v, std::memory_order_release);
@@ -1701,19 +1749,23 @@ hipError_t balanced_slots(long& slots) {
   return hipSuccess;
 }
 
-template <int D, bool QLO>
+template <int D, bool QLO, bool PAIR>
 hipError_t decode_slots_d(const DecodeArgs& a, long& slots) {
-  if (a.tier == 8) return balanced_slots<D, 8, QLO>(slots);
-  if (a.tier == 2) return balanced_slots<D, 2, QLO>(slots);
-  return balanced_slots<D, 4, QLO>(slots);
+  if (a.tier == 8) return balanced_slots<D, 8, QLO, PAIR>(slots);
+  if (a.tier == 2) return balanced_slots<D, 2, QLO, PAIR>(slots);
+  return balanced_slots<D, 4, QLO, PAIR>(slots);
 }
 
 hipError_t decode_ranges(const DecodeArgs& a, long& ranges) {
   const bool qlo = a.q_dtype == ECHOKV_F32;
   long slots = 0;
   hipError_t e;
-  if (a.L.D == 128) e = qlo ? decode_slots_d<128, true>(a, slots) : decode_slots_d<128, false>(a, slots);
-  else if (a.L.D == 64) e = qlo ? decode_slots_d<64, true>(a, slots) : decode_slots_d<64, false>(a, slots);
+  if (a.L.D == 128 && a.pair)
+    e = qlo ? decode_slots_d<128, true, true>(a, slots) : decode_slots_d<128, false, true>(a, slots);
+  else if (a.L.D == 128)
+    e = qlo ? decode_slots_d<128, true, false>(a, slots) : decode_slots_d<128, false, false>(a, slots);
+  else if (a.L.D == 64 && !a.pair)
+    e = qlo ? decode_slots_d<64, true, false>(a, slots) : decode_slots_d<64, false, false>(a, slots);
   else return hipErrorInvalidValue;
   if (e != hipSuccess) return e;
   const long n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
@@ -1724,25 +1776,29 @@ hipError_t decode_ranges(const DecodeArgs& a, long& ranges) {
   return hipSuccess;
 }
 
-template <int D, bool QLO>
+template <int D, bool QLO, bool PAIR>
 hipError_t launch_decode_d(const DecodeArgs& a, hipStream_t s) {
-  if (a.tier == 8) return launch_decode_t<D, 8, QLO>(a, s);
-  if (a.tier == 2) return launch_decode_t<D, 2, QLO>(a, s);
-  return launch_decode_t<D, 4, QLO>(a, s);
+  if (a.tier == 8) return launch_decode_t<D, 8, QLO, PAIR>(a, s);
+  if (a.tier == 2) return launch_decode_t<D, 2, QLO, PAIR>(a, s);
+  return launch_decode_t<D, 4, QLO, PAIR>(a, s);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
   (void)num_seqs;  // a.num_seqs
   const bool qlo = a.q_dtype == ECHOKV_F32;
-  if (a.L.D == 128) return qlo ? launch_decode_d<128, true>(a, s) : launch_decode_d<128, false>(a, s);
-  if (a.L.D == 64) return qlo ? launch_decode_d<64, true>(a, s) : launch_decode_d<64, false>(a, s);
+  if (a.L.D == 128 && a.pair) return qlo ? launch_decode_d<128, true, true>(a, s) : launch_decode_d<128, false, true>(a, s);
+  if (a.pair) return hipErrorInvalidValue;
+  if (a.L.D == 128) return qlo ? launch_decode_d<128, true, false>(a, s) : launch_decode_d<128, false, false>(a, s);
+  if (a.L.D == 64) return qlo ? launch_decode_d<64, true, false>(a, s) : launch_decode_d<64, false, false>(a, s);
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_merge_balanced(const DecodeArgs& a, hipStream_t s) {
   const long wgs = (a.num_seqs * a.hq + 3) / 4;
-  if (a.L.D == 128) hipLaunchKernelGGL(merge_balanced_kernel<128>, dim3((unsigned)wgs), dim3(256), 0, s, a);
-  else if (a.L.D == 64) hipLaunchKernelGGL(merge_balanced_kernel<64>, dim3((unsigned)wgs), dim3(256), 0, s, a);
+  const int d = a.pair ? 2 * a.L.D : a.L.D;  // the head size of the rows
+  if (d == 128) hipLaunchKernelGGL(merge_balanced_kernel<128>, dim3((unsigned)wgs), dim3(256), 0, s, a);
+  else if (d == 64) hipLaunchKernelGGL(merge_balanced_kernel<64>, dim3((unsigned)wgs), dim3(256), 0, s, a);
+  else if (d == 256) hipLaunchKernelGGL(merge_balanced_kernel<256>, dim3((unsigned)wgs), dim3(256), 0, s, a);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }
@@ -1777,6 +1833,7 @@ hipError_t launch_merge(const MergeArgs& a, long num_seqs, hipStream_t s) {
   const long wgs = (a.rows + 3) / 4;
   if (a.D == 128) hipLaunchKernelGGL(merge_kernel<128>, dim3((unsigned)wgs), dim3(256), 0, s, a);
   else if (a.D == 64) hipLaunchKernelGGL(merge_kernel<64>, dim3((unsigned)wgs), dim3(256), 0, s, a);
+  else if (a.D == 256) hipLaunchKernelGGL(merge_kernel<256>, dim3((unsigned)wgs), dim3(256), 0, s, a);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }

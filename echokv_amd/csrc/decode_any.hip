@@ -1,8 +1,9 @@
 // Paged decode attention for the layouts the MFMA decode kernels do not take
 // (echokv_vllm/kernels/decode.py:95-129, the reference's PyTorch path for shapes
-// its Triton kernel refuses): head sizes other than 64 / 128 (any multiple of 4
-// up to 256), K groups under 16, block sizes or K groups that are not powers of
-// two, more than 4 chunks per page.
+// its Triton kernel refuses): head sizes other than 64 / 128 / 256 (any multiple
+// of 4 up to 256), V groups under D / 16 channels (at head size 256: outside 8 to
+// 128), K groups under 16, block sizes or K groups that are not powers of two,
+// more than 4 chunks per page.
 //
 // One workgroup per (sequence, KV head, split) in fp32 arithmetic, the split
 // schedule of the MFMA kernels (splits of max(blocks_per_split, ceil(blocks /

@@ -145,7 +145,8 @@ int echokv_store_blocks(const echokv_layout* L, uint8_t* pages, const int64_t* b
  * that tier's blocks on its own fast path, one after another into the same
  * partial rows, and one merge follows. It needs ECHOKV_DECODE_BATCH_INVARIANT
  * (the split schedule), and a sequence's result still depends on its own blocks
- * only. Layouts: head_size 64 or 128 with v_group >= head_size / 16, k_group >= 16,
+ * only. Layouts: head_size 64 or 128 with v_group >= head_size / 16, or head_size
+ * 256 with v_group 8 to 128 (each KV head as two 128-channel halves), k_group >= 16,
  * power-of-two block_size and k_group and <= 4 chunks per page run on the MFMA
  * kernels; any other layout (head_size up to 256) on an fp32 kernel with the split
  * schedule (flags and tier then select nothing).

@@ -377,15 +377,16 @@ def test_v_group_and_head_size_variants(device, d, vg, bits, h):
         check(f"prefill {path} D{d} VG{vg} int{bits}", out, ref)
 
 
-@pytest.mark.parametrize("d,bs,kg,vg,h,gqa", [(96, 16, 16, 32, 4, 4), (256, 16, 16, 32, 4, 4), (128, 16, 8, 32, 4, 4),
-                                               (128, 48, 16, 32, 4, 4), (128, 16, 16, 4, 4, 4), (80, 32, 32, 16, 4, 2),
-                                               (96, 16, 16, 32, 2, 20)])
+@pytest.mark.parametrize("d,bs,kg,vg,h,gqa", [(96, 16, 16, 32, 4, 4), (256, 16, 16, 32, 4, 4), (256, 32, 32, 256, 2, 4),
+                                               (128, 16, 8, 32, 4, 4), (128, 48, 16, 32, 4, 4), (128, 16, 16, 4, 4, 4),
+                                               (80, 32, 32, 16, 4, 2), (96, 16, 16, 32, 2, 20)])
 @pytest.mark.parametrize("bits", [8, 4, 2])
 def test_layouts_outside_the_mfma_kernels(device, d, bs, kg, vg, h, gqa, bits):
-    """Head sizes other than 64 / 128 (up to 256), K groups under 16, block sizes
-    that are not powers of two and V groups under D/16 take the fp32 decode kernel
-    (the reference's PyTorch path serves them there), GQA 20 in two passes of query
-    heads; prefill attends through decode rows. Both equal the oracle."""
+    """Head sizes other than 64 / 128 / 256 (up to 256), head size 256 with one V
+    group per head, K groups under 16, block sizes that are not powers of two and V
+    groups under D/16 take the fp32 decode kernel (the reference's PyTorch path
+    serves them there), GQA 20 in two passes of query heads; prefill attends
+    through decode rows (head size 256 included). Both equal the oracle."""
     lens = np.array([1, 17, 300, 64, 1000])
     store, table = build_layer(device, lens, bits, h=h, d=d, bs=bs, kg=kg, vg=vg, seed=8, outliers=0.02)
     ps = oracle_view(store)
@@ -411,6 +412,38 @@ def test_layouts_outside_the_mfma_kernels(device, d, bs, kg, vg, h, gqa, bits):
     ref = OA.prefill_attention(ps, qp.float().cpu().numpy(), prefill, list(range(5)), table, d ** -0.5,
                                vectorized=True)
     check(f"prefill {label}", out, ref)
+
+
+@pytest.mark.parametrize("h,gqa,vg,dt", [(8, 4, 32, torch.float16), (3, 4, 64, torch.bfloat16), (1, 20, 16, torch.float32),
+                                         (2, 8, 128, torch.float16)])
+@pytest.mark.parametrize("bits", [8, 4, 2])
+def test_head_size_256_as_half_heads(device, h, gqa, vg, dt, bits):
+    """Head size 256 on the 128-channel MFMA kernels: each KV head's channel halves on
+    two waves that add their partial scores before the softmax. Even and odd KV head
+    counts (H 3 and H 1: a workgroup's last two waves are past the last head and
+    still meet every score exchange), GQA 20 (two passes of query heads), V groups
+    of 16 (every tile on the register path) to 128, fp16 / bf16 / float32 queries,
+    K / V and residual (the open K groups), a 2500-token sequence in one span (the
+    64-block chunk loop); both schedules against the oracle, and a sequence decoded
+    alone equal to itself in the batch (split schedule)."""
+    lens = np.array([1, 17, 300, 64, 1000, 2500])
+    store, table = build_layer(device, lens, bits, h=h, d=256, vg=vg, dtype=dt, seed=9, outliers=0.02,
+                               v_outliers=0.01)
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    lens_d = torch.from_numpy(lens).to(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(99)
+    q = torch.randn(len(lens), gqa * h, 256, device=device, generator=gen).to(dt)
+    ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, 256 ** -0.5, vectorized=True)
+    label = f"D256 H{h} GQA{gqa} VG{vg} {str(dt)[6:]} int{bits}"
+    got = dec.decode_attention(store, q, table_d, lens_d, 256 ** -0.5, tier=bits, batch_invariant=False)
+    check(f"{label} balanced", got, ref)
+    for ns in (None, 1):
+        got = dec.decode_attention(store, q, table_d, lens_d, 256 ** -0.5, tier=bits, num_splits=ns)
+        check(f"{label} split, splits {ns or 'default'}", got, ref)
+    alone = dec.decode_attention(store, q[4:5], table_d[4:5], lens_d[4:5], 256 ** -0.5, tier=bits, num_splits=1)
+    assert torch.equal(alone[0], got[4])
 
 
 @pytest.mark.parametrize("bits", [2, 4, 8])
@@ -538,12 +571,13 @@ def test_mixed_tier_layer_with_tier_passes(device):
 
 
 @pytest.mark.parametrize("d,gqa,qdt,ws", [(64, 4, torch.float16, None), (128, 4, torch.float32, None),
-                                          (128, 20, torch.float16, None), (128, 4, torch.float16, "static")])
+                                          (128, 20, torch.float16, None), (128, 4, torch.float16, "static"),
+                                          (256, 4, torch.float16, None), (256, 4, torch.float32, None)])
 def test_tier_passes_at_other_shapes(device, d, gqa, qdt, ws):
-    """Tier passes at head size 64, with float32 queries (the query hi / lo path), at
-    GQA 20 (query heads in groups of 16, each group its own passes) and on the
-    library's static workspace: against the oracle, and equal to themselves when a
-    sequence is decoded alone."""
+    """Tier passes at head sizes 64 and 256 (half-heads), with float32 queries (the
+    query hi / lo path), at GQA 20 (query heads in groups of 16, each group its own
+    passes) and on the library's static workspace: against the oracle, and equal to
+    themselves when a sequence is decoded alone."""
     h = 4
     rng = np.random.default_rng(40 + d + gqa)
     lens = rng.integers(60, 1500, 12)
