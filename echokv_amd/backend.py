@@ -60,9 +60,9 @@ from echokv_amd.step import StepDriver
 from echokv_amd.tiered_cache import HeaderWriter, TieredKVCache, TieredLayout
 from echokv_amd.write_plan import SharedState, WriteMeta
 
-# Head sizes the MFMA decode kernels take (256 as two 128-channel half-heads);
-# others up to MAX_HEAD_SIZE take the fp32 kernels. Prefill's MFMA kernels take 64
-# and 128.
+# Head sizes the MFMA kernels take (decode at 256 as two 128-channel half-heads,
+# prefill at 256 on the fused kernel alone); others up to MAX_HEAD_SIZE take the
+# fp32 kernels.
 KERNEL_HEAD_SIZES = (64, 128, 256)
 MAX_HEAD_SIZE = 256
 # Upper bound on decode splits per sequence (a fixed grid, so a graph replays it).
@@ -365,7 +365,8 @@ class EchoKVMetadataBuilder(AttentionMetadataBuilder):
         dev = self.device
         if pf.kernels_take(impl0.head_size, self.gqa):
             if not pf.use_dense(entries, impl0.head_size):
-                work.tiles = pf.build_tiles(entries, work.reqs, self.gqa, dev)
+                work.tiles = pf.build_tiles(entries, work.reqs, self.gqa, dev,
+                                            tokens=pf.block_m(self.gqa, impl0.head_size))
             else:
                 plan = pf.build_dense_plan(entries, work.reqs, self.gqa, dev)
                 nbytes = pf.dense_workspace_bytes(impl0.store, plan.packs.shape[0])
@@ -424,7 +425,7 @@ class EchoKVAttentionImpl(AttentionImpl):
         self.num_kv_heads = num_kv_heads or num_heads
         self.kv_cache_dtype = kv_cache_dtype
         self.cfg = cfg = load_config()
-        if cfg.own_group_exact and not pf.kernels_take(head_size, self.num_heads // self.num_kv_heads):
+        if cfg.own_group_exact and not pf.own_group_takes(head_size, self.num_heads // self.num_kv_heads):
             raise NotImplementedError("ECHOKV_OWN_GROUP_EXACT needs head size 64 or 128 and GQA <= 128")
         self.controller = LayerController(cfg.controller)
         # Allocated at model construction so vLLM's memory profiler counts them: the

@@ -355,11 +355,12 @@ int echokv_prefill(const echokv_layout* L, const uint8_t* pages, const int64_t* 
   if (!lay_ok(L)) return ECHOKV_ESHAPE;
   if (num_q_heads <= 0 || num_q_heads % L->num_kv_heads) return ECHOKV_ESHAPE;
   const int gqa = num_q_heads / L->num_kv_heads;
-  // The MFMA kernel: head size 64 or 128, at most kPrefillRows query rows per
-  // tile. Any other layout (head size up to kMaxAnyD) takes the fp32 kernel.
-  const bool mfma = (L->head_size == 64 || L->head_size == 128) && gqa <= ek::kPrefillRows;
-  if (!mfma && (L->head_size > ek::kMaxAnyD || own_group)) return ECHOKV_ESHAPE;
-  if (tile_m != (mfma ? ek::prefill_tile_tokens(gqa) : ek::any_tile_tokens(gqa))) return ECHOKV_ESHAPE;
+  // The MFMA kernel: head size 64, 128 or 256, at most prefill_rows query rows
+  // per tile. Any other layout (head size up to kMaxAnyD) takes the fp32 kernel.
+  const int D = L->head_size;
+  const bool mfma = (D == 64 || D == 128 || D == 256) && gqa <= ek::prefill_rows(D);
+  if (!mfma && (D > ek::kMaxAnyD || own_group)) return ECHOKV_ESHAPE;
+  if (tile_m != (mfma ? ek::prefill_tile_tokens(gqa, D) : ek::any_tile_tokens(gqa))) return ECHOKV_ESHAPE;
   if (own_group != 0 && own_group != 1) return ECHOKV_EINVAL;
   if (own_group && (L->k_group & (L->k_group - 1))) return ECHOKV_ESHAPE;
   if (!dtype_ok(q_dtype) || !dtype_ok(out_dtype)) return ECHOKV_EDTYPE;

@@ -13,8 +13,10 @@ constexpr int kCanaryMaxD = 256;
 constexpr size_t kLdsBytes = 160 * 1024;  // LDS per CU on gfx950
 constexpr int kPrefillRows = 128;    // prefill: query rows (tokens x GQA heads) per workgroup
 
-// Query tokens per prefill tile for a GQA group size.
-inline int prefill_tile_tokens(int gqa) { return kPrefillRows / gqa; }
+// Query rows of a prefill workgroup (head size 256: half, one 16-row block per
+// wave) and query tokens per tile for a GQA group size.
+inline int prefill_rows(int head_size) { return head_size == 256 ? kPrefillRows / 2 : kPrefillRows; }
+inline int prefill_tile_tokens(int gqa, int head_size) { return prefill_rows(head_size) / gqa; }
 
 // Long-chunk (two-pass) prefill: keys per workspace tile, waves (32 query rows
 // each) per attention workgroup, and the workspace bytes of one tile and head.

@@ -2,7 +2,9 @@
 //
 // One workgroup (4 waves) per (query tile, KV head). A tile holds up to
 // 128 / GQA query tokens; its rows are (token, GQA head) pairs, 128 rows, 32
-// per wave (two 16-row blocks). The context is walked in 32-key tiles: the
+// per wave (two 16-row blocks) -- at head size 256, 64 / GQA tokens and one
+// 16-row block per wave (RB), so a wave's accumulators and query fragments take
+// the registers they take at 128. The context is walked in 32-key tiles: the
 // workgroup dequantizes each key tile once into LDS -- K row-major as an fp16
 // hi + lo pair (exact to ~2^-22), V transposed in fp16 -- and every wave then
 // runs, per 16-row block,
@@ -25,7 +27,7 @@ constexpr int kVPad = 8;            // fp16 padding per V^T row
 __device__ __forceinline__ h2_t u2h_(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
 }  // namespace
 
-template <int D, bool QLO>
+template <int D, bool QLO, int RB>
 __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   constexpr int KS = D + kKPad;       // K tile row stride (halves)
   constexpr int VS = kKeys + kVPad;   // V^T row stride (halves)
@@ -47,14 +49,14 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   const int gqa = a.gqa;
   const int n_rows = n_tok * gqa;
 
-  // Query fragments (B operand of S^T): row = 32*wave + 16*rb + n, channels
+  // Query fragments (B operand of S^T): row = 16*RB*wave + 16*rb + n, channels
   // 32j + 8c .. +8 in natural order.
-  h8_t qf[2][NQK], qfl[2][QLO ? NQK : 1];
-  int qpos[2], qlim[2];  // keys < qlim are visible
-  bool rvalid[2];
+  h8_t qf[RB][NQK], qfl[RB][QLO ? NQK : 1];
+  int qpos[RB], qlim[RB];  // keys < qlim are visible
+  bool rvalid[RB];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int r = 32 * wave + 16 * rb + n;
+  for (int rb = 0; rb < RB; ++rb) {
+    const int r = 16 * RB * wave + 16 * rb + n;
     rvalid[rb] = r < n_rows;
     const int tok = rvalid[rb] ? r / gqa : 0;
     const int hh = h * gqa + (rvalid[rb] ? r % gqa : 0);
@@ -71,10 +73,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
       }
     }
   }
-  f4_t acc[2][NPV];
-  float m_run[2], l_lane[2];
+  f4_t acc[RB][NPV];
+  float m_run[RB], l_lane[RB];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+  for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
     for (int j = 0; j < NPV; ++j) acc[rb][j] = f4_t{0.f, 0.f, 0.f, 0.f};
     m_run[rb] = -__builtin_inff();
@@ -142,7 +144,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     __syncthreads();
 
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+    for (int rb = 0; rb < RB; ++rb) {
       f4_t s[2];
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
@@ -198,12 +200,12 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   }
 
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+  for (int rb = 0; rb < RB; ++rb) {
     float l = l_lane[rb];
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
     if (!rvalid[rb]) continue;
-    const int r = 32 * wave + 16 * rb + n;
+    const int r = 16 * RB * wave + 16 * rb + n;
     const long ob = (q_row0 + r / gqa) * a.o_s0 + (long)(h * gqa + r % gqa) * a.o_s1;
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (a.lse && c == 0) a.lse[(q_row0 + r / gqa) * a.hq + h * gqa + r % gqa] = l > 0.f ? m_run[rb] + __log2f(l) : -__builtin_inff();
@@ -219,11 +221,14 @@ hipError_t launch_prefill(const PrefillArgs& a, long n_tiles, hipStream_t s) {
   const dim3 grid((unsigned)n_tiles, (unsigned)a.L.H);
   const bool qlo = a.q_dtype == ECHOKV_F32;
   if (a.L.D == 128) {
-    if (qlo) hipLaunchKernelGGL((prefill_kernel<128, true>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((prefill_kernel<128, false>), grid, dim3(256), 0, s, a);
+    if (qlo) hipLaunchKernelGGL((prefill_kernel<128, true, 2>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((prefill_kernel<128, false, 2>), grid, dim3(256), 0, s, a);
   } else if (a.L.D == 64) {
-    if (qlo) hipLaunchKernelGGL((prefill_kernel<64, true>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((prefill_kernel<64, false>), grid, dim3(256), 0, s, a);
+    if (qlo) hipLaunchKernelGGL((prefill_kernel<64, true, 2>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((prefill_kernel<64, false, 2>), grid, dim3(256), 0, s, a);
+  } else if (a.L.D == 256) {
+    if (qlo) hipLaunchKernelGGL((prefill_kernel<256, true, 1>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((prefill_kernel<256, false, 1>), grid, dim3(256), 0, s, a);
   } else {
     return hipErrorInvalidValue;
   }

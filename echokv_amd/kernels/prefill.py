@@ -20,10 +20,13 @@ through LDS. ``dequant_dense`` keeps the reference's dense-dequantization
 entry point (``[total_ctx, H, D]`` K/V).
 
 Both kernels are built for head sizes 64 and 128 (and at most ``ROWS`` query
-heads per KV head). Any other layout (the reference's PyTorch path serves them)
-takes an fp32 kernel through the same entry point (``echokv_prefill``): tiles of
-``any_block_m(gqa)`` query tokens, so a workgroup's (token, query head) columns
-are at most 16, each tile streaming its causal context once.
+heads per KV head); head size 256 takes the fused kernel at every chunk length,
+with half the rows per tile (``rows(256)``: ``64 // GQA`` tokens). Own-group-exact
+attention needs head size 64 or 128. Any other layout (the reference's PyTorch
+path serves them) takes an fp32 kernel through the same entry point
+(``echokv_prefill``): tiles of ``any_block_m(gqa)`` query tokens, so a
+workgroup's (token, query head) columns are at most 16, each tile streaming its
+causal context once.
 """
 
 from __future__ import annotations
@@ -45,9 +48,14 @@ def gqa_pad(gqa: int) -> int:
     return 1 << (gqa - 1).bit_length()
 
 
-def block_m(gqa: int) -> int:
-    """Query tokens per tile."""
-    return max(1, ROWS // gqa)
+def rows(head_size: int = 128) -> int:
+    """Query rows (tokens x GQA heads) per workgroup of the fused kernel."""
+    return ROWS // 2 if head_size == 256 else ROWS
+
+
+def block_m(gqa: int, head_size: int = 128) -> int:
+    """Query tokens per tile of the fused kernel."""
+    return max(1, rows(head_size) // gqa)
 
 
 def any_block_m(gqa: int) -> int:
@@ -59,7 +67,8 @@ def build_tiles(prefill, req_of, gqa: int, device, tokens: int | None = None) ->
     """Tile table ``[n, 5]`` int32: (q_row0, n_tokens, q_pos0, ctx, request).
 
     ``prefill`` holds (q_start, q_end, ctx, _) per prefill request, ``req_of``
-    the matching block-table row; ``tokens`` per tile, by default ``block_m(gqa)``."""
+    the matching block-table row; ``tokens`` per tile, by default ``block_m(gqa)`` (head
+    size 64 / 128)."""
     bm = tokens or block_m(gqa)
     rows = []
     for (qs, qe, ctx, *_), r in zip(prefill, req_of):
@@ -175,7 +184,12 @@ def _out_view(output: torch.Tensor, hq: int) -> torch.Tensor:
 
 def kernels_take(head_size: int, gqa: int) -> bool:
     """Whether the MFMA prefill kernels serve this layout (else the fp32 kernel)."""
-    return head_size in (64, 128) and gqa <= ROWS
+    return head_size in (64, 128, 256) and gqa <= rows(head_size)
+
+
+def own_group_takes(head_size: int, gqa: int) -> bool:
+    """Whether own-group-exact prefill serves this layout (head size 64 or 128)."""
+    return head_size in (64, 128) and kernels_take(head_size, gqa)
 
 
 def use_dense(prefill, head_size: int) -> bool:
@@ -243,9 +257,10 @@ def prefill_attention(store, query: torch.Tensor, output: torch.Tensor, prefill,
     may be built once per step."""
     if not prefill:
         return
-    if not kernels_take(store.layout.head_size, query.shape[1] // store.layout.num_kv_heads):
-        if own_group_key is not None:
-            raise ValueError("own-group-exact prefill needs head size 64 or 128 and at most 128 query heads per KV head")
+    gqa = query.shape[1] // store.layout.num_kv_heads
+    if own_group_key is not None and not own_group_takes(store.layout.head_size, gqa):
+        raise ValueError("own-group-exact prefill needs head size 64 or 128 and at most 128 query heads per KV head")
+    if not kernels_take(store.layout.head_size, gqa):
         prefill_attention_fused(store, query, output, prefill, req_of, block_table, softmax_scale)
         return
     part, lse = output, None
@@ -318,7 +333,7 @@ def prefill_attention_fused(store, query: torch.Tensor, output: torch.Tensor, pr
     L = store.layout
     hq = query.shape[1]
     gqa = hq // L.num_kv_heads
-    tile_m = block_m(gqa) if kernels_take(L.head_size, gqa) else any_block_m(gqa)
+    tile_m = block_m(gqa, L.head_size) if kernels_take(L.head_size, gqa) else any_block_m(gqa)
     if tiles is not None:
         check_tiles(tiles, tile_m)
     _lib.require_device(query, output, block_table, store.pages)

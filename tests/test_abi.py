@@ -117,13 +117,17 @@ def _prefill(lib, L, hq=32, tile_m=32, n_tiles=0, own_group=0):
 
 
 def test_prefill_tile_sizes_by_kernel(lib):
-    """MFMA tiles hold 128 / GQA tokens; other layouts (fp32 kernel) 16 / GQA, no own group."""
+    """MFMA tiles hold 128 / GQA tokens (64 / GQA at head size 256); other layouts
+    (fp32 kernel) 16 / GQA, no own group."""
     assert _prefill(lib, _layout_of(), tile_m=32) == 0                    # D 128, GQA 4: 128 / 4
     assert _prefill(lib, _layout_of(), tile_m=4) == 2
+    assert _prefill(lib, _layout_of(head_size=256), tile_m=16) == 0       # D 256, GQA 4: 64 / 4
+    assert _prefill(lib, _layout_of(head_size=256), tile_m=32) == 2
+    assert _prefill(lib, _layout_of(head_size=256), hq=8 * 20, tile_m=3) == 0  # GQA 20: 64 // 20
+    assert _prefill(lib, _layout_of(head_size=256), hq=8 * 80, tile_m=1) == 0  # GQA 80 > 64: fp32 kernel
     assert _prefill(lib, _layout_of(head_size=96), tile_m=4) == 0         # fp32 kernel: 16 / 4
     assert _prefill(lib, _layout_of(head_size=96), tile_m=32) == 2
     assert _prefill(lib, _layout_of(head_size=96), tile_m=4, own_group=1) == 2
-    assert _prefill(lib, _layout_of(head_size=256), hq=8 * 20, tile_m=1) == 0  # GQA 20: one token per tile
     assert _prefill(lib, _layout_of(head_size=512), tile_m=4) == 2
 
 

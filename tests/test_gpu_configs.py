@@ -446,6 +446,34 @@ def test_head_size_256_as_half_heads(device, h, gqa, vg, dt, bits):
     assert torch.equal(alone[0], got[4])
 
 
+@pytest.mark.parametrize("h,gqa,dt", [(8, 4, torch.float16), (3, 20, torch.bfloat16), (2, 4, torch.float32)])
+@pytest.mark.parametrize("bits", [8, 4, 2])
+def test_head_size_256_prefill_on_the_mfma_kernel(device, h, gqa, dt, bits):
+    """Head size 256 prefill on the fused MFMA kernel (64 // GQA query tokens per
+    tile, one 16-row block per wave): chunks of 1 to 300 tokens over contexts up to
+    1000, GQA 4 and 20, fp16 / bf16 / float32 queries (the query lo part), odd KV
+    head counts, K outlier channels x10 (cfg3's activations, as every prefill test
+    here: prefill's V and P operands are single fp16 values); against the oracle."""
+    lens = np.array([1, 17, 300, 64, 1000])
+    store, table = build_layer(device, lens, bits, h=h, d=256, dtype=dt, seed=12, outliers=0.02)
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(120)
+    prefill, row = [], 0
+    for n in lens.tolist():
+        nq = min(300, n)
+        prefill.append((row, row + nq, n, 0))
+        row += nq
+    qp = torch.randn(row, gqa * h, 256, device=device, generator=gen).to(dt)
+    out = torch.zeros(row, gqa * h, 256, device=device)
+    pf.prefill_attention(store, qp, out, prefill, list(range(5)), table_d, 256 ** -0.5)
+    torch.cuda.synchronize()
+    ref = OA.prefill_attention(ps, qp.float().cpu().numpy(), prefill, list(range(5)), table, 256 ** -0.5,
+                               vectorized=True)
+    check(f"prefill D256 H{h} GQA{gqa} {str(dt)[6:]} int{bits}", out, ref)
+
+
 @pytest.mark.parametrize("bits", [2, 4, 8])
 def test_decode_over_a_layer_view_spanning_more_than_4_gib(device, bits):
     """One layer's view of a pool interleaved across 32 layers (page stride = 32

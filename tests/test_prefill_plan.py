@@ -53,3 +53,27 @@ def test_fused_prefill_refuses_tiles_larger_than_its_kernel_takes():
     ok = pf.build_tiles(prefill, req, gqa, "cpu", tokens=pf.any_block_m(gqa))
     with pytest.raises(RuntimeError, match="device tensors"):  # past the check: CPU tensors are refused next
         pf.prefill_attention_fused(store, q, q, prefill, req, torch.zeros(1, 1), 0.1, ok)
+
+
+def test_head_size_256_tiles_hold_half_the_rows():
+    """At head size 256 the fused MFMA kernel takes 64 query rows per tile (64 //
+    GQA tokens): tiles built at head size 128's size are refused on the host,
+    tiles of the right size pass; own-group-exact prefill is not offered there."""
+    import pytest
+    import torch
+    from types import SimpleNamespace
+
+    gqa = 4
+    assert pf.kernels_take(256, gqa) and not pf.own_group_takes(256, gqa) and pf.own_group_takes(128, gqa)
+    assert pf.block_m(gqa, 256) == 16 and pf.block_m(gqa) == 32 and not pf.kernels_take(256, 80)
+    store = SimpleNamespace(layout=SimpleNamespace(num_kv_heads=2, head_size=256), pages=torch.zeros(1))
+    q = torch.zeros(40, 2 * gqa, 256)
+    prefill, req = [(0, 40, 40, 0)], [0]
+    with pytest.raises(ValueError, match="at most"):
+        pf.prefill_attention_fused(store, q, q, prefill, req, torch.zeros(1, 1), 0.1,
+                                   pf.build_tiles(prefill, req, gqa, "cpu"))
+    ok = pf.build_tiles(prefill, req, gqa, "cpu", tokens=pf.block_m(gqa, 256))
+    with pytest.raises(RuntimeError, match="device tensors"):
+        pf.prefill_attention_fused(store, q, q, prefill, req, torch.zeros(1, 1), 0.1, ok)
+    with pytest.raises(ValueError, match="own-group"):
+        pf.prefill_attention(store, q, q, prefill, req, torch.zeros(1, 1), 0.1, own_group_key=q)
