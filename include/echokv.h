@@ -189,8 +189,9 @@ int echokv_decode_static(const echokv_layout* L, const uint8_t* pages, const int
 /* Chunked-prefill attention over the tiered pages (MFMA tiles), bottom-right causal:
  * tiles [n_tiles, 5] int32 = (first query row, tokens, first query position, ctx,
  * block-table row); each tile holds <= tile_m query tokens: tile_m = 128 / GQA on the
- * MFMA kernel (head size 64 or 128, GQA <= 128), else 16 / GQA (1 from GQA 16 on) on
- * an fp32 kernel for head sizes up to 256 (no own_group there). own_group = 1 leaves
+ * MFMA kernel (head size 64 or 128, GQA <= 128; 64 / GQA at head size 256, GQA <= 64),
+ * else 16 / GQA (1 from GQA 16 on) on an fp32 kernel for head sizes up to 256 (no
+ * own_group there). own_group = 1 leaves
  * each query's own K group out (a query at p sees keys < p & ~(k_group - 1); k_group
  * a power of two); lse (nullable, float [query rows, num_q_heads]) receives each
  * row's log2-domain log-sum-exp of the scaled scores (-inf: no visible key).
