@@ -103,18 +103,22 @@ int echokv_write_step(const echokv_layout* L, uint8_t* pages, const void* key, i
   if (n_rows < 0 || fin_grid < 0 || tok_s0 < n_rows || !res_ok(res)) return ECHOKV_EINVAL;
   if (n_rows + fin_grid == 0) return ECHOKV_OK;
   if (!pages || !key || !fin_count || (n_rows && (!value || !tok)) || (fin_grid && !fin)) return ECHOKV_EINVAL;
-  // Fin rows stage their group in LDS when key and residual share a dtype, every
-  // four-channel run is aligned for one vector load, and the group fits the LDS.
-  int staged = -1;
-  if (kv_dtype == res->dtype && ek::step_staged_lds(L->k_group, kv_dtype) <= ek::kStepStagedMaxLds) {
-    const uintptr_t al = kv_dtype == ECHOKV_F32 ? 16 : 8;
-    if ((uintptr_t)key % al == 0 && (uintptr_t)res->ptr % al == 0 && k_s0 % 4 == 0 && k_s1 % 4 == 0 &&
-        res->s0 % 4 == 0 && res->s1 % 4 == 0 && res->s2 % 4 == 0)
-      staged = kv_dtype;
-  }
+  // Fin rows read their group with one vector load per four channels when key and
+  // residual share a dtype and every four-channel run is aligned for it. Such rows
+  // are split over workgroups of 64 (head, quad) items, a group over 4 lanes per
+  // item, for k_group 8 to 64; other k_groups stage the group in LDS when it fits.
+  const int KG = L->k_group;
+  const uintptr_t al = kv_dtype == ECHOKV_F32 ? 16 : 8;
+  const bool vec = kv_dtype == res->dtype && (uintptr_t)key % al == 0 && (uintptr_t)res->ptr % al == 0 &&
+                   k_s0 % 4 == 0 && k_s1 % 4 == 0 && res->s0 % 4 == 0 && res->s1 % 4 == 0 && res->s2 % 4 == 0;
+  const int items = L->num_kv_heads * (L->head_size / 4);
+  const int parts = vec && KG >= 8 && KG <= 64 && !(KG & (KG - 1)) ? (items + 63) / 64 : 0;
+  if (parts > 0 && fin_grid > INT32_MAX / parts) return ECHOKV_EINVAL;
+  const int staged =
+      vec && (parts > 0 || ek::step_staged_lds(KG, kv_dtype) <= ek::kStepStagedMaxLds) ? kv_dtype : -1;
   ek::StepArgs a{ek::WriteTokArgs{to_lay(L), pages, key, k_s0, k_s1, value, v_s0, v_s1, kv_dtype, tok, tok_s0,
                                   to_res(res), kref, kref_s0, kref_s1},
-                 fin, fin_count, fin_grid, n_rows, staged};
+                 fin, fin_count, fin_grid, n_rows, staged, parts};
   return launched(ek::launch_write_step(a, (hipStream_t)stream));
 }
 

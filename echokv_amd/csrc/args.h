@@ -66,6 +66,10 @@ struct StepArgs {
   long fin_grid;
   long n_rows;
   int staged;  // dtype of key and residual when fin rows stage their group in LDS, else -1
+  // > 0: each fin row is split over fin_parts workgroups of 64 (head, quad) items,
+  // its K group over 4 lanes per item (staged dtype, k_group 8 to 64); 0: one
+  // workgroup per fin row.
+  int fin_parts;
 };
 
 // Dynamic LDS of a staged fused step, and the largest the launch takes without

@@ -22,27 +22,34 @@ namespace ek {
 template <typename ResHere>
 __device__ __forceinline__ void write_token_row(const WriteTokArgs& a, long t, ResHere res_here) {
   const Lay& L = a.L;
+  // The row's plan and its first pass's K / V words do not depend on one another:
+  // they are requested together, before the slot is known (row t of key and value
+  // exists whatever the slot), so the row costs two memory round trips.
   const long slot = a.tok[t];
-  if (slot < 0) return;
-  const long blk = slot / L.BS;
-  const int off = (int)(slot % L.BS);
-  if (blk >= L.nb) return;
-  // Every load this row needs is independent of the others: issue them together
-  // (the kernel is a chain of memory round trips, not of arithmetic).
-  const Hdr hd = load_hdr(a.pages, L, blk);
   const long rslot = a.tok[a.tok_s0 + t];
   const int64_t sealed = a.tok[2 * a.tok_s0 + t];
   const long kidx = a.kref ? a.tok[3 * a.tok_s0 + t] : -1;
   const int quads = L.D / 4;
   const int items = L.H * quads;
+  float x0[4] = {0.f, 0.f, 0.f, 0.f}, k0[4] = {0.f, 0.f, 0.f, 0.f};
+  if ((int)threadIdx.x < items) {
+    const int h = (int)threadIdx.x / quads, c = (int)threadIdx.x % quads;
+    ld_n<4>(a.value, a.kv_dtype, t * a.v_s0 + h * a.v_s1 + 4 * c, x0);
+    ld_n<4>(a.key, a.kv_dtype, t * a.k_s0 + h * a.k_s1 + 4 * c, k0);
+  }
+  if (slot < 0) return;
+  const long blk = slot / L.BS;
+  const int off = (int)(slot % L.BS);
+  if (blk >= L.nb) return;
+  const Hdr hd = load_hdr(a.pages, L, blk);
   const int G = L.D / L.VG;
   bool rh = true;
   for (int base = 0; base < items; base += kThreads) {
     const int i = base + (int)threadIdx.x;
     const bool act = i < items;
     const int h = act ? i / quads : 0, c = act ? i % quads : 0;
-    float x[4] = {0.f, 0.f, 0.f, 0.f}, k[4] = {0.f, 0.f, 0.f, 0.f};
-    if (act) {
+    float x[4] = {x0[0], x0[1], x0[2], x0[3]}, k[4] = {k0[0], k0[1], k0[2], k0[3]};
+    if (act && base > 0) {
       ld_n<4>(a.value, a.kv_dtype, t * a.v_s0 + h * a.v_s1 + 4 * c, x);
       ld_n<4>(a.key, a.kv_dtype, t * a.k_s0 + h * a.k_s1 + 4 * c, k);
     }
@@ -364,13 +371,20 @@ __device__ __forceinline__ void collect_deferred(const WriteTokArgs& a, long n_r
   }
 }
 
-// Round trip 1 of a fin row: its residual slot, the device count and the step's
-// token slots, then the deferred rows. Returns false when the row is past the count.
-__device__ __forceinline__ bool fin_prologue(const StepArgs& s, long f, Deferred& def, int64_t* grow) {
+// Round trip 1 of a fin row: its (block, group, residual slot), the device count
+// and the step's token slots, then the deferred rows. Returns false when the row
+// is past the count.
+struct FinHead {
+  long blk, rs;
+  int grp;
+};
+__device__ __forceinline__ bool fin_prologue(const StepArgs& s, long f, Deferred& def, int64_t* grow,
+                                             FinHead* head = nullptr) {
   const WriteTokArgs& a = s.w;
   const int64_t* row = s.fin + f * (3 + a.L.KG);
   const long count = *s.fin_count;
   const long rs = row[2];
+  if (head) *head = FinHead{row[0], rs, (int)row[1]};
   if (grow && (int)threadIdx.x < a.L.KG) grow[threadIdx.x] = row[3 + threadIdx.x];
   const bool mine = (long)threadIdx.x < s.n_rows;
   const long tslot = mine ? a.tok[threadIdx.x] : -1;
@@ -501,6 +515,129 @@ __device__ __forceinline__ void fin_staged(const StepArgs& s, long f, typename R
   }
 }
 
+// Fin row f split over workgroups (StepArgs::fin_parts > 0): part `part` takes
+// items [64 part, 64 part + 64) ((head, quad) pairs), and each item's K group is
+// spread over the 4 lanes 16 apart (quarter r = lane / 16 holds positions
+// r TPT .. r TPT + TPT - 1 in registers). The per-channel min / max meet by two
+// lane swaps (min and max are exact, so the order does not matter), and each
+// thread quantizes and stores its own positions: a group's codes cost TPT
+// dependent divisions per thread, not k_group. The residual words of a deferred
+// row are rewritten by the thread that read that position (if it read the
+// residual there), after its read.
+template <int DT, int TPT>
+__device__ __forceinline__ void fin_split(const StepArgs& s, const FinHead& fh, int part, const Deferred& def,
+                                          const int64_t* grow) {
+  using V = typename Raw4<DT>::V;
+  constexpr long esz = DT == ECHOKV_F32 ? 4 : 2;
+  const WriteTokArgs& a = s.w;
+  const Lay& L = a.L;
+  const int KG = L.KG;  // = 4 * TPT
+  const long blk = fh.blk;
+  const int grp = fh.grp;
+  const long rs_raw = fh.rs;
+  const long rs = rs_raw < 0 ? 0 : rs_raw;  // -1: every token of the group is in this step's key
+  const bool ok = blk >= 0 && blk < L.nb && grp >= 0 && grp < L.BS / KG && rs < a.res.rows;
+  const int lane = threadIdx.x & 63, r = lane >> 4;
+  const int quads = L.D / 4;
+  const int i = part * 64 + (int)(threadIdx.x >> 6) * 16 + (lane & 15);
+  const bool act = i < L.H * quads;  // whole 16-lane groups: every quarter of an item agrees
+  const int h = act ? i / quads : 0, c = act ? i % quads : 0;
+  const Hdr hd = load_hdr(a.pages, L, ok ? blk : 0);  // block 0 stands in for a bad row (nothing is stored)
+  const char* key = (const char*)a.key;
+  const char* res = (const char*)a.res.ptr;
+  float x[TPT][4];
+  float mn[4], mx[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    mn[e] = __builtin_inff();
+    mx[e] = -__builtin_inff();
+  }
+  if (act && ok) {
+    V v[TPT];
+#pragma unroll
+    for (int u = 0; u < TPT; ++u) {
+      const int p = r * TPT + u;
+      const long t = grow[p];
+      const char* src = t >= 0 ? key + esz * (t * a.k_s0 + h * a.k_s1 + 4 * c)
+                               : res + esz * (rs * a.res.s0 + (long)p * a.res.s1 + h * a.res.s2 + 4 * c);
+      v[u] = *(const V*)src;
+    }
+#pragma unroll
+    for (int u = 0; u < TPT; ++u) {
+      raw4_to_f<DT>(v[u], x[u]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        mn[e] = fminf(mn[e], x[u][e]);
+        mx[e] = fmaxf(mx[e], x[u][e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {  // the item's four quarters: lanes l, l ^ 16, l ^ 32, l ^ 48
+    mn[e] = fminf(mn[e], __shfl_xor(mn[e], 16, 64));
+    mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], 16, 64));
+    mn[e] = fminf(mn[e], __shfl_xor(mn[e], 32, 64));
+    mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], 32, 64));
+  }
+  if (act && ok) {
+    const int bits = tier_of(hd.tag);
+    float sc[4], mi[4];
+    const long se = ((long)grp * L.H + h) * L.D + 4 * c;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      _Float16 s16, m16;
+      group_stats(mn[e], mx[e], bits, s16, m16, sc[e], mi[e]);
+      if (r == 0) {
+        *f16p(a.pages, blk * L.stride + L.o_ks + 2 * (se + e)) = s16;
+        *f16p(a.pages, blk * L.stride + L.o_km + 2 * (se + e)) = m16;
+      }
+    }
+    long cb[4];  // chunk j of the block (its own page's data for j = 0; -1: out of range)
+    cb[0] = blk * L.stride + L.o_data;
+#pragma unroll
+    for (int j = 1; j < 4; ++j) {
+      const int id = hd.id(j - 1);
+      const uint32_t page = (uint32_t)id / (uint32_t)L.KC, slot = (uint32_t)id % (uint32_t)L.KC;
+      cb[j] = (id < 0 || (long)page >= L.nb) ? -1L : (long)page * L.stride + L.o_data + (long)slot * L.cb;
+    }
+    const int tpc = 2 * L.BS / bits;  // tokens per chunk
+    const long rowb = 2L * L.H * L.D * bits / 8;
+    const long within = (long)h * (L.D * bits / 8) + c * (bits / 2);
+#pragma unroll
+    for (int u = 0; u < TPT; ++u) {
+      const int pos = grp * KG + r * TPT + u;
+      const int j = pos / tpc;
+      const long base = j == 0 ? cb[0] : (j == 1 ? cb[1] : (j == 2 ? cb[2] : cb[3]));
+      if (base >= 0) {
+        uint32_t q[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = quant_code(x[u][e], mi[e], sc[e], bits);
+        store_codes4(a.pages + base + (pos % tpc) * rowb + within, pack4(q, bits), bits);
+      }
+    }
+  }
+  // Residual K of the deferred rows whose position this thread holds.
+  if (act) {
+    for (int d = 0; d < def.n; ++d) {
+      if (def.row[d] / TPT != r) continue;
+      float k[4];
+      ld_n<4>(a.key, a.kv_dtype, def.t[d] * a.k_s0 + h * a.k_s1 + 4 * c, k);
+      st_n<4>(a.res.ptr, a.res.dtype, rs_raw * a.res.s0 + (long)def.row[d] * a.res.s1 + h * a.res.s2 + 4 * c, k);
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void fin_split_t(const StepArgs& s, const FinHead& fh, int part, const Deferred& def,
+                                            const int64_t* grow) {
+  switch (s.w.L.KG) {
+    case 8: fin_split<DT, 2>(s, fh, part, def, grow); break;
+    case 16: fin_split<DT, 4>(s, fh, part, def, grow); break;
+    case 32: fin_split<DT, 8>(s, fh, part, def, grow); break;
+    default: fin_split<DT, 16>(s, fh, part, def, grow); break;  // 64 (the host picks this path for 8 to 64)
+  }
+}
+
 // Token row t of a fused step: round trip 1 takes the row's plan and values, the
 // device count and the fin rows' residual slots; the residual vote runs with the
 // row's second round trip (page header, sealed stats) in flight.
@@ -528,7 +665,18 @@ __global__ __launch_bounds__(kThreads) void write_step_kernel(StepArgs s) {
   extern __shared__ uint4 step_lds[];  // fin_staged's group values (dynamic: k_group * kThreads * 8 or 16 bytes)
   __shared__ Deferred def;
   __shared__ int64_t grow[kMaxDeferred];  // the fin row's token row per position
-  if ((long)blockIdx.x < s.fin_grid) {
+  const long fin_wgs = s.fin_parts > 0 ? s.fin_grid * s.fin_parts : s.fin_grid;
+  if ((long)blockIdx.x < fin_wgs) {
+    if (s.fin_parts > 0) {  // split fin rows: staged dtype, k_group 8 to 64
+      const long f = blockIdx.x / s.fin_parts;
+      const int part = (int)(blockIdx.x % s.fin_parts);
+      FinHead fh;
+      if (!fin_prologue(s, f, def, grow, &fh)) return;
+      if (s.staged == ECHOKV_F16) fin_split_t<ECHOKV_F16>(s, fh, part, def, grow);
+      else if (s.staged == ECHOKV_BF16) fin_split_t<ECHOKV_BF16>(s, fh, part, def, grow);
+      else fin_split_t<ECHOKV_F32>(s, fh, part, def, grow);
+      return;
+    }
     const long f = blockIdx.x;
     const bool staged = s.staged >= 0;
     if (!fin_prologue(s, f, def, staged ? grow : nullptr)) return;
@@ -545,7 +693,7 @@ __global__ __launch_bounds__(kThreads) void write_step_kernel(StepArgs s) {
     }
     return;
   }
-  step_token_row(s, (long)blockIdx.x - s.fin_grid);
+  step_token_row(s, (long)blockIdx.x - fin_wgs);
 }
 
 // ---------------------------------------------------------------------------
@@ -819,8 +967,9 @@ hipError_t launch_finalize_k(const FinArgs& a, long rows, hipStream_t s) {
   return hipGetLastError();
 }
 hipError_t launch_write_step(const StepArgs& a, hipStream_t s) {
-  const size_t lds = a.staged < 0 ? 0 : step_staged_lds(a.w.L.KG, a.staged);
-  hipLaunchKernelGGL(write_step_kernel, dim3((unsigned)(a.fin_grid + a.n_rows)), dim3(kThreads), lds, s, a);
+  const size_t lds = a.staged < 0 || a.fin_parts > 0 ? 0 : step_staged_lds(a.w.L.KG, a.staged);
+  const long fin_wgs = a.fin_parts > 0 ? a.fin_grid * a.fin_parts : a.fin_grid;
+  hipLaunchKernelGGL(write_step_kernel, dim3((unsigned)(fin_wgs + a.n_rows)), dim3(kThreads), lds, s, a);
   return hipGetLastError();
 }
 // Page headers of a step's freshly opened blocks in every layer, one launch: layer

@@ -17,7 +17,11 @@ import torch
 from echokv_amd import _lib
 
 
-def _kv(t: torch.Tensor) -> torch.Tensor:
+def _kv(t: torch.Tensor, n_rows: int) -> torch.Tensor:
+    """``t`` with contiguous channels; every one of the step's ``n_rows`` rows is
+    read (a row's words are requested before its slot is known)."""
+    if t.shape[0] < n_rows:
+        raise ValueError(f"key / value hold {t.shape[0]} rows, the step has {n_rows} token rows")
     if t.stride(-1) != 1:
         t = t.contiguous()
     return t
@@ -28,7 +32,7 @@ def write_tokens(store, key: torch.Tensor, value: torch.Tensor, meta, kref: torc
     if meta.n_rows == 0:
         return
     _lib.require_device(key, value, store.pages)
-    key, value = _kv(key), _kv(value)
+    key, value = _kv(key, meta.n_rows), _kv(value, meta.n_rows)
     if value.dtype != key.dtype:
         value = value.to(key.dtype)
     tok = meta.tok
@@ -81,7 +85,7 @@ def write_step(store, key: torch.Tensor, value: torch.Tensor, meta, kref: torch.
         raise ValueError(f"the fused step takes k_group <= {FUSED_MAX_K_GROUP}, got {store.layout.k_group}")
     fin = _fin_rows(store, meta)  # rows at or past the device count are never read
     _lib.require_device(key, value, store.pages)
-    key, value = _kv(key), _kv(value)
+    key, value = _kv(key, meta.n_rows), _kv(value, meta.n_rows)
     if value.dtype != key.dtype:
         value = value.to(key.dtype)
     tok = meta.tok
@@ -107,7 +111,7 @@ def finalize_k(store, key: torch.Tensor, meta, full_grid: bool = False) -> None:
         return
     fin = _fin_rows(store, meta)
     _lib.require_device(key, store.pages)
-    key = _kv(key)
+    key = _kv(key, 0)  # fin rows read only the key rows they name
     # A full grid only reads rows below the device count (<= fin's rows).
     res = _lib.residual(store.res_k)
     _lib.call(

@@ -62,7 +62,8 @@ const char* echokv_error_string(int code);
 
 /* Quantize-on-write of one step's token rows: V per token (groups of v_group),
  * K to the residual / under sealed stats / to the K_ref ring.
- * tok: [4, tok_s0] int64 = (slot, residual slot, sealed, kref row) per row.
+ * tok: [4, tok_s0] int64 = (slot, residual slot, sealed, kref row) per row; key and
+ * value hold n_rows rows, each read whatever its slot (-1 rows included).
  * Replaces echokv_vllm/kernels/write.py:29-36 (write_tokens) and its kernel
  * write.py:172-229 (_write_tokens_kernel). kref may be NULL. */
 int echokv_write_tokens(const echokv_layout* L, uint8_t* pages,
