@@ -6,6 +6,7 @@ captured HIP graph, with the canary firing. Every layer's attention output is
 checked against the float64 oracle over that layer's own page bytes, and the
 canary's δ̂ against the oracle canary on the rows it stashed."""
 
+import sys
 from types import SimpleNamespace
 
 import numpy as np
@@ -163,7 +164,8 @@ def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
     starts = np.concatenate([[0], np.cumsum(PROMPTS)])
     slots = slots_for(table_np, [0] * nreq, PROMPTS)
     md = builder.build(0, Batch(device, table, starts, PROMPTS, slots, int(starts[-1])))
-    assert md.prefill is not None and md.prefill.dense is not None and md.decode is None
+    assert md.prefill is not None and md.decode is None
+    assert (md.prefill.dense is not None) == (D != 256)  # head size 256: the fused kernel at every length
     q, k, v = rand(int(starts[-1]), HQ), rand(int(starts[-1]), H), rand(int(starts[-1]), H)
     outs = run_layers(layers, md, q, k, v)
     torch.cuda.synchronize()
@@ -287,3 +289,17 @@ def test_a_request_decodes_the_same_alone_and_in_a_batch(device, monkeypatch):
         assert torch.equal(outs["batch"][li][1], outs["alone"][li][0]), f"layer {li}"
     print("[backend] request 1 decodes bit-identically alone and in a batch of 4", flush=True)
     _vllm.set_forward_metadata(None)
+
+
+def test_serving_sequence_at_head_size_256(device, monkeypatch):
+    """The same serving sequence at head size 256: decode on the MFMA kernels as
+    half-heads (tier passes under graph replay included), prefill on the fused MFMA
+    kernel at every chunk length, the canary at 256 channels; against the oracle."""
+    for k, v in {"ECHOKV_K_GROUP": "16", "ECHOKV_MEM_BITS": "8", "ECHOKV_CANARY_INTERVAL": "2",
+                 "ECHOKV_KREF_WINDOW": "32", "ECHOKV_RESIDUAL_SLOTS": "24", "ECHOKV_OWN_GROUP_EXACT": "0"}.items():
+        monkeypatch.setenv(k, v)
+    monkeypatch.setattr(sys.modules[__name__], "D", 256)
+    try:
+        test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, False)
+    finally:
+        _vllm.set_forward_metadata(None)
