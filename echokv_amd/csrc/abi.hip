@@ -192,6 +192,14 @@ void decode_view(const echokv_layout* L, ek::DecodeArgs& a) {
   }
 }
 
+// Whether the MFMA decode folds the V scale into the P operand (DecodeArgs::ps): the
+// first pass's query heads times the kernel head's V groups fill at most the 16
+// MFMA columns (every later pass has as many query heads or fewer).
+int decode_ps(const ek::DecodeArgs& a, int gqa) {
+  const int G = a.L.D / a.L.VG, gs = gqa < 16 ? gqa : 16;
+  return G >= 1 && G <= 4 && gs * G <= 16 ? 1 : 0;
+}
+
 // echokv_decode and echokv_decode_static: the checks, then decode + merge with
 // the given workspaces, or (static_scratch) with the library's static scratch.
 int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* block_res, const int64_t* res_group,
@@ -263,6 +271,7 @@ int decode_run(const echokv_layout* L, const uint8_t* pages, const int64_t* bloc
   a.o_s1 = o_s1;
   a.out_dtype = out_dtype;
   a.ranges = 0;
+  a.ps = mfma ? decode_ps(a, gqa) : 0;
   if (mfma && !(flags & ECHOKV_DECODE_BATCH_INVARIANT) && ek::decode_ranges(a, a.ranges) != hipSuccess)
     return ECHOKV_ELAUNCH;
   // A wave's MFMA columns hold 16 query heads: a larger GQA runs in passes of 16
@@ -341,6 +350,7 @@ int64_t echokv_decode_workspace_rows(const echokv_layout* L, int32_t num_q_heads
   a.q_dtype = q_dtype;
   a.num_seqs = num_seqs;
   a.num_splits = num_splits;
+  a.ps = decode_ps(a, num_q_heads / L->num_kv_heads);
   int64_t rows = 0;
   for (int tier : {2, 4, 8}) {
     a.tier = tier;

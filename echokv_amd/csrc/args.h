@@ -167,6 +167,9 @@ struct DecodeArgs {
   long q_s0, q_s1;
   int q_dtype, hq, gqa;
   int g0, gs;  // this pass's query heads of each KV head: [g0, g0 + gs), gs <= 16
+  // 1: the V scale rides on the P operand (gs * (D / VG) <= 16, D / VG <= 4): the
+  // MFMA columns are (query head, V group) pairs; 0: V is dequantized per element.
+  int ps;
   const int64_t* q_rows;
   const int32_t* bt;
   long bt_s0;

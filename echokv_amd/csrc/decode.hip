@@ -295,6 +295,7 @@ struct Wave {
   uint32_t ql[QLO ? CPL / 2 : 1];     // fp16 query pairs (lo = q - hi)
   f4_t acc[CPM];                      // O^T fragments: sum_t p * codes * V scale
   f4_t acc_m;                         // sum_t p * V min of the lane's V group (every channel of it)
+  float acc_ml;                       // PS: this lane's tokens' share of sum_t w * V min of its column's group
   float m_run, l_lane;                // running max (scaled log2 units), this lane's sum
   float scale;                        // |softmax scale| * log2(e), > 0 (a negative scale negates the query)
 };
@@ -479,6 +480,92 @@ __device__ __forceinline__ void softmax_pv(Wave<D, QLO>& w, const float* x, cons
 }
 
 // ---------------------------------------------------------------------------
+// V scale on the P side (PS). When a pass's query heads times the head's V groups
+// fit the 16 MFMA columns (gs * G <= 16, G <= 4), column n stands for query head
+// n % gs and V group n / gs: the S^T product computes every query's scores once
+// per group it will meet (the columns were padding), and the PV operand of column
+// n is w * s[t, group(n)] -- the token's V scale folded into its weight -- so the
+// V operand is the codes alone, exact and unscaled:
+//   O^T[d, n] += codes[t, d]^T . (w * s)[t, n]          (16x16x16, hi then lo part)
+//   M[n]      += sum_t w[t] * m[t, group(n)]            (fp32 FMAs, per lane)
+// Of the output, row d of column n is real where group(d) == group(n): lane (c, n)
+// holds rows 4c .. 4c + 3, all in group c * G / 4, so the lanes with n / gs ==
+// c * G / 4 write their column's query, those rows' channels, plus M.
+// w = 2^k * exp2(x * scale - m_run) with the tier's shift k (INT8 6, INT4 2, INT2
+// 0): a weight near the row max times a typical V scale then sits in fp16's
+// normal range with room below for its lo part (lo = w * s - hi, normal down to
+// w * s = 2^-3), and w * s < 2^15 while s < 2^(7 - k) (w <= 2^(8 + k) under the
+// lazy rescale). A tile with a larger scale rescales exactly (w <= 2^k), which
+// keeps w * s finite for every finite fp16 V. The stored running max is m_run - k,
+// so partial rows of any tier combine as plain log-sum-exp partials.
+// ---------------------------------------------------------------------------
+template <int BITS>
+constexpr int ps_shift() { return BITS == 8 ? 6 : (BITS == 4 ? 2 : 0); }
+__device__ __forceinline__ int ps_shift_of(int bits) { return bits == 8 ? 6 : (bits == 4 ? 2 : 0); }
+// PS: column n's V group is n / gs (the padding columns past gs * G read group 0).
+__device__ __forceinline__ int ps_group(const DecodeArgs& a, int G, int n) {
+  const int g = n / a.gs;
+  return g < G ? g : 0;
+}
+
+
+// Online-softmax update and PV for PS. kk: the kernel's shift (the weights' unit);
+// kb: the shift of the tile's tier (its codes and scales); the generic path's
+// tiles of another tier scale the codes by 2^(kk - kb) and the P operand by
+// 2^(kb - kk), so the product stays in the kernel's unit.
+template <int D, bool QLO, int BITS, int VW>
+__device__ __forceinline__ void softmax_pv_ps(Wave<D, QLO>& w, const float* x, const VTile<VW>& vt, int kk, int kb) {
+  const VStats& vs = vt.st;
+  const float mt = rows_max(vmax(vmax3(x[0], x[1], x[2]), x[3])) * w.scale;
+  const float m_new = vmax(w.m_run, mt);
+  // The largest V scale of the lane's tokens, as fp16 bits (positive: ordered like
+  // the values; a negative or NaN pattern reads as large, which only rescales).
+  const uint32_t s2 = __builtin_elementwise_max(h2u(vs.s01) & 0xFFFFu, h2u(vs.s23) & 0xFFFFu);
+  const uint32_t s3 = __builtin_elementwise_max(h2u(vs.s01) >> 16, h2u(vs.s23) >> 16);
+  const bool big = __builtin_elementwise_max(s2, s3) >= ((uint32_t)(15 + 7 - kb) << 10);
+  if (__builtin_amdgcn_ballot_w64(m_new > w.m_run + (big ? 0.f : kLazyRescale))) {
+    const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);  // m_run = -inf at the start: 0
+    w.l_lane *= alpha;
+#pragma unroll
+    for (int j = 0; j < Wave<D, QLO>::CPM; ++j) w.acc[j] *= alpha;
+    w.acc_ml *= alpha;
+    w.m_run = m_new;
+  }
+  const float off = (float)kk - w.m_run;
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], w.scale, off));
+  w.l_lane += (p[0] + p[1]) + (p[2] + p[3]);
+  const _Float16 sv[4] = {vs.s01[0], vs.s01[1], vs.s23[0], vs.s23[1]};
+  const _Float16 mv[4] = {vs.m01[0], vs.m01[1], vs.m23[0], vs.m23[1]};
+  const float sc = kb == kk ? 1.f : __builtin_amdgcn_exp2f((float)(kb - kk));  // exact power of two
+  float b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w.acc_ml = __builtin_fmaf(p[i], (float)mv[i], w.acc_ml);
+    b[i] = __builtin_fmaf((float)sv[i], kb == kk ? p[i] : p[i] * sc, 0.f);
+  }
+  // b = hi + lo in fp16: hi rounded once, lo the exact remainder rounded once.
+  const h4_t bh = {(_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
+  h4_t bl;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) bl[i] = (_Float16)__builtin_fmaf((float)bh[i], -1.f, b[i]);
+  h4_t va[Wave<D, QLO>::CPM];
+  v_codes<BITS, Wave<D, QLO>::CPM, VW>(vt.w, va);
+  if (kb != kk) {  // generic-path tile of another tier: codes * 2^(kk - kb), exact
+    const _Float16 f = (_Float16)__builtin_amdgcn_exp2f((float)(kk - kb));
+    const h4_t f4 = {f, f, f, f};
+#pragma unroll
+    for (int j = 0; j < Wave<D, QLO>::CPM; ++j) va[j] *= f4;
+  }
+#pragma unroll
+  for (int j = 0; j < Wave<D, QLO>::CPM; ++j) {
+    w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j], bh, w.acc[j], 0, 0, 0);
+    w.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va[j], bl, w.acc[j], 0, 0, 0);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic register path: a tile of a block stored at another tier than the
 // kernel's (or whose chunk table names a chunk out of range), including its
 // open K group. Rare: only blocks demoted or downgraded under pool pressure.
@@ -528,7 +615,7 @@ __device__ __forceinline__ void load_as_bytes(const uint8_t* p, int bits, uint32
 // head h's channels from element rh of a row).
 // The block header is read once and each part's loads issue together: the tile
 // is a few memory round trips, not one per row.
-template <int D, bool QLO>
+template <int D, bool QLO, bool PS>
 __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs& a, long blk, int t0, int n_valid,
                                          long rslot, bool in_res, int h, long rh, int lane, int bits, float* x,
                                          VTile<D / 64>& vt) {
@@ -574,7 +661,7 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
   constexpr int VW = CPM / 4;  // words per token of the lane's V slice, one byte per code
   uint32_t (&vw)[4][VW] = vt.w;
   const int G = D / L.VG;
-  const int g = (n * CPM) / L.VG;
+  const int g = PS ? ps_group(a, G, n) : (n * CPM) / L.VG;
   _Float16 sv[4], mv[4];
   // The four rows at a compile-time width (one branch on the tier, not one per
   // row), so their loads issue together.
@@ -768,7 +855,7 @@ struct LaneConst {
   uint32_t vs_rd;                    // V scale of token 4c (32-byte rows: token 4c + i at + 32 i, V min at + 512)
 };
 
-template <int D, int BITS>
+template <int D, int BITS, bool PS>
 __device__ __forceinline__ LaneConst<D, BITS> lane_const(const DecodeArgs& a, int wv, int lane) {
   using R = Ring<D, BITS>;
   constexpr int CPL = D / 4, CPM = D / 16, VB = CPM * BITS / 8;
@@ -782,7 +869,7 @@ __device__ __forceinline__ LaneConst<D, BITS> lane_const(const DecodeArgs& a, in
   for (int i = 0; i < 4; ++i) k.v_rd[i] = R::OFF_V + unit_pos<D, BITS>(4 * c + i, vbyte / 16) + (vbyte % 16);
   k.s_rd = (uint32_t)(R::OFF_KS + wv * D * 2 + 2 * c * CPL);
   const int G = D >> a.vg_shift;
-  const int g = (n * CPM) >> a.vg_shift;
+  const int g = PS ? ps_group(a, G, n) : (n * CPM) >> a.vg_shift;
   k.vs_rd = (uint32_t)(R::OFF_VS + 4 * c * 32 + (wv * G + g) * 2);  // 32 bytes per token
   return k;
 }
@@ -1089,7 +1176,7 @@ __device__ __forceinline__ void range_priority(int left, int total) {
 
 // Blocks [b_start, b_end) of sequence `seq` for the KV heads of head group hg
 // (one wave per head).
-template <int D, int BITS, bool QLO, bool PASSES, bool PAIR>
+template <int D, int BITS, bool QLO, bool PASSES, bool PAIR, bool PS>
 __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b_start, int b_end, int hg, int wv,
                                             int lane, uint8_t* ring, uint32_t ring0, SpanSink sink,
                                             SpanPass pass = SpanPass{false, true, 0, false}) {
@@ -1114,6 +1201,13 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   const long rh = pair ? (long)(ha >> 1) * a.res.s2 + (ha & 1) * D : (long)ha * a.res.s2;
   uint8_t* const xch = ring + R::WG_BYTES;  // the score exchange (pair only)
   int xi = 0;
+  // Columns: query head qcol of the pass (PS: one per V group, cols = gs * G of them);
+  // `mine`: the lane's output rows are real (PS: its rows' V group is its column's).
+  const int G = D >> a.vg_shift;
+  const int cols = PS ? a.gs * G : a.gs;
+  const int qcol = PS ? n % a.gs : n;
+  const bool mine = live && n < cols && (!PS || n / a.gs == (c * G) >> 2);
+  constexpr int kk = PS ? ps_shift<BITS>() : 0;  // the weights' unit (PS): 2^kk
 
   W w;
   // The first chunk's block table row is requested with the query, so their
@@ -1121,8 +1215,8 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   const int nb_first = b_end - b_start < 64 ? b_end - b_start : 64;
   BlockLane bl;
   {
-    const bool qv = live && n < a.gs;
-    const long qb = q_row * a.q_s0 + (long)(kh * a.gqa + a.g0 + (qv ? n : 0)) * a.q_s1 + half * D + c * W::CPL;
+    const bool qv = live && n < cols;
+    const long qb = q_row * a.q_s0 + (long)(kh * a.gqa + a.g0 + (qv ? qcol : 0)) * a.q_s1 + half * D + c * W::CPL;
     float xq[W::CPL];
     // Scores are scaled inside the exponent (exp2(s * x - m)); the max is taken
     // on unscaled scores, which needs the scale positive: a negative one flips
@@ -1151,6 +1245,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
 #pragma unroll
   for (int j = 0; j < W::CPM; ++j) w.acc[j] = f4_t{0.f, 0.f, 0.f, 0.f};
   w.acc_m = f4_t{0.f, 0.f, 0.f, 0.f};
+  w.acc_ml = 0.f;
   w.m_run = -__builtin_inff();
   w.l_lane = 0.f;
   // A later tier pass continues the partial result the passes before it left in
@@ -1159,21 +1254,23 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   // with none leaves its row as it is.
   bool carried = !pass.carry;
   auto load_carry = [&]() {
-    if (live && n < a.gs) {
-      const long row = sink.part_row0 + ((long)kh * a.gqa + a.g0 + n) * sink.part_stride;
+    if (live && n < cols) {
+      const long row = sink.part_row0 + ((long)kh * a.gqa + a.g0 + qcol) * sink.part_stride;
       const float* src = a.acc + row * RD + half * D;
+      if (mine) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int j = 0; j < W::CPM; ++j) w.acc[j][i] = src[(4 * c + i) * W::CPM + j];
+          for (int j = 0; j < W::CPM; ++j) w.acc[j][i] = src[(4 * c + i) * W::CPM + j];
+        }
       }
-      w.m_run = a.ml[row * 2];
+      w.m_run = a.ml[row * 2] + (float)kk;  // stored: m_run - kk
       w.l_lane = c == 0 ? a.ml[row * 2 + 1] : 0.f;
     }
     carried = true;
   };
 
-  const LaneConst<D, BITS> kc = lane_const<D, BITS>(a, wv, lane);
+  const LaneConst<D, BITS> kc = lane_const<D, BITS, PS>(a, wv, lane);
   const JobLane<D, BITS> jl = job_lane<D, BITS>(a, wv, hg, lane);
   const int tpb_shift = a.bs_shift - 4;  // tiles per block = BS / 16
   const bool stats_ok = (D >> a.vg_shift) == 2 || (D >> a.vg_shift) == 4;
@@ -1274,7 +1371,8 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
       VTile<VW> vt;
       compute_tile<D, QLO, BITS>(w, a, kc, ring + (tt % R::NBUF) * R::SLOT, n_valid - t0, lane, x, vt);
       if (pair) pair_scores(xch, xi, wv, lane, x);
-      softmax_pv<D, QLO, BITS, VW>(w, x, vt, vscale_mask<BITS>());
+      if constexpr (PS) softmax_pv_ps<D, QLO, BITS, VW>(w, x, vt, kk, kk);
+      else softmax_pv<D, QLO, BITS, VW>(w, x, vt, vscale_mask<BITS>());
     }
     wait_vmcnt<0>();  // nothing of this chunk may still be landing in the ring
     wg_barrier();     // every wave is done reading the ring before the next chunk refills it
@@ -1292,20 +1390,29 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
         const int n_valid = seq_len - ((c0 + orig(b)) << a.bs_shift);
         float x[4];
         VTile<D / 64> vt;  // codes widened to bytes
-        tile_any<D, QLO>(w, a, blk, t0, n_valid, rslot, in_res, ha, rh, lane, tier, x, vt);
+        tile_any<D, QLO, PS>(w, a, blk, t0, n_valid, rslot, in_res, ha, rh, lane, tier, x, vt);
         if (pair) pair_scores(xch, xi, wv, lane, x);
-        softmax_pv<D, QLO, 8, D / 64>(w, x, vt,
-                                      tier == 8 ? vscale_mask<8>() : (tier == 4 ? vscale_mask<4>() : vscale_mask<2>()));
+        if constexpr (PS)
+          softmax_pv_ps<D, QLO, 8, D / 64>(w, x, vt, kk, ps_shift_of(tier));
+        else
+          softmax_pv<D, QLO, 8, D / 64>(w, x, vt,
+                                        tier == 8 ? vscale_mask<8>() : (tier == 4 ? vscale_mask<4>() : vscale_mask<2>()));
       }
     }
   }
 
   if (!carried) return;  // no block of this pass's tier: the row keeps the earlier passes' result
   const float l = rows_sum(w.l_lane);
+  if constexpr (PS) {
+    const float mterm = rows_sum(w.acc_ml);  // the column's V min term, every row of its group
 #pragma unroll
-  for (int j = 0; j < W::CPM; ++j) w.acc[j] += w.acc_m;  // the V min term, the same for the lane's channels
-  if (live && n < a.gs) {
-    const long qh = (long)kh * a.gqa + a.g0 + n;
+    for (int j = 0; j < W::CPM; ++j) w.acc[j] += mterm;
+  } else {
+#pragma unroll
+    for (int j = 0; j < W::CPM; ++j) w.acc[j] += w.acc_m;  // the V min term, the same for the lane's channels
+  }
+  if (mine) {
+    const long qh = (long)kh * a.gqa + a.g0 + qcol;
     if (sink.direct) {  // lane (c, n): channels (4c + i) * CPM + j of query head qh (of its half)
       const float inv = 1.0f / l;
       const long o = q_row * a.o_s0 + qh * a.o_s1 + half * D;
@@ -1325,8 +1432,8 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
 #pragma unroll
       for (int j = 0; j < W::CPM; ++j) dst[(4 * c + i) * W::CPM + j] = w.acc[j][i];
     }
-    if (c == 0 && half == 0) {  // the two halves hold the same (max, sum)
-      a.ml[row * 2] = w.m_run;
+    if (c == 0 && half == 0) {  // the two halves hold the same (max, sum); PS: the group-0 column
+      a.ml[row * 2] = w.m_run - (float)kk;
       a.ml[row * 2 + 1] = l;
     }
   }
@@ -1340,7 +1447,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
 // Three waves per SIMD (<= 168 VGPRs) where the ring leaves LDS for three
 // workgroups per CU; INT8's larger ring and the float32-query variant get two.
 // PAIR: head size 256 as half-heads (DecodeArgs::pair), D = 128.
-template <int D, int BITS, bool QLO, bool PAIR>
+template <int D, int BITS, bool QLO, bool PAIR, bool PS>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
   SpanPass pass{false, true, 0, false};
@@ -1372,7 +1479,7 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   const int bps = split_blocks(a, n_blocks);
   const int b_start = split * bps;
   const int b_end = b_start + bps < n_blocks ? b_start + bps : n_blocks;
-  decode_span<D, BITS, QLO, true, PAIR>(a, seq, b_start, b_end, (int)(item % n_hg), wv, lane, ring_lds, ring0,
+  decode_span<D, BITS, QLO, true, PAIR, PS>(a, seq, b_start, b_end, (int)(item % n_hg), wv, lane, ring_lds, ring0,
                                   SpanSink{seq * a.hq * a.num_splits + split, a.num_splits, false, 0, 0}, pass);
 }
 
@@ -1435,7 +1542,7 @@ __device__ __forceinline__ void seq_of_block(const DecodeArgs& a, long x, int la
   first = base;
 }
 
-template <int D, int BITS, bool QLO, bool PAIR>
+template <int D, int BITS, bool QLO, bool PAIR, bool PS>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_balanced_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
   const int lane = threadIdx.x & 63;
@@ -1462,7 +1569,7 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
     if (nb > 0) {
       const bool whole = pos == first && end == first + nb;
       const long slot = 2 * r + (pos == lo ? 0 : 1);
-      decode_span<D, BITS, QLO, false, PAIR>(a, seq, (int)(pos - first), (int)(end - first), hg, wv, lane, ring_lds,
+      decode_span<D, BITS, QLO, false, PAIR, PS>(a, seq, (int)(pos - first), (int)(end - first), hg, wv, lane, ring_lds,
                                        ring0, SpanSink{slot * a.hq, 1, whole, (int)(hi - end), (int)(hi - lo)});
     }
     pos = end;
@@ -1699,7 +1806,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
 template <int D, int BITS, bool PAIR>
 constexpr int decode_lds() { return Ring<D, BITS>::WG_BYTES + (PAIR ? kPairLds : 0); }
 
-template <int D, int BITS, bool QLO, bool PAIR>
+template <int D, int BITS, bool QLO, bool PAIR, bool PS>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
   const dim3 block(64 * kHeadsPerGroup);
   constexpr int lds = decode_lds<D, BITS, PAIR>();
@@ -1707,22 +1814,22 @@ hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
   const long span = 8 * n_hg;  // the kernels permute workgroups within runs of `span`
   if (a.ranges > 0) {
     static std::atomic<uint64_t> attr_done{0};  // devices whose limit is raised, one bit each
-    if (ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO, PAIR>, lds, &attr_done) != hipSuccess)
+    if (ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO, PAIR, PS>, lds, &attr_done) != hipSuccess)
       return hipErrorInvalidValue;
     const long wgs = (a.ranges * n_hg + span - 1) / span * span;
-    hipLaunchKernelGGL((decode_balanced_kernel<D, BITS, QLO, PAIR>), dim3((unsigned)wgs), block, lds, s, a);
+    hipLaunchKernelGGL((decode_balanced_kernel<D, BITS, QLO, PAIR, PS>), dim3((unsigned)wgs), block, lds, s, a);
     return hipGetLastError();
   }
   static std::atomic<uint64_t> attr_done{0};
-  if (ensure_lds_limit((const void*)decode_kernel<D, BITS, QLO, PAIR>, lds, &attr_done) != hipSuccess)
+  if (ensure_lds_limit((const void*)decode_kernel<D, BITS, QLO, PAIR, PS>, lds, &attr_done) != hipSuccess)
     return hipErrorInvalidValue;
   const long items = (a.num_seqs * a.num_splits * n_hg + span - 1) / span * span;
-  hipLaunchKernelGGL((decode_kernel<D, BITS, QLO, PAIR>), dim3((unsigned)items), block, lds, s, a);
+  hipLaunchKernelGGL((decode_kernel<D, BITS, QLO, PAIR, PS>), dim3((unsigned)items), block, lds, s, a);
   return hipGetLastError();
 }
 
 // Workgroups of the balanced kernel the current device holds at once (cached per device).
-template <int D, int BITS, bool QLO, bool PAIR>
+template <int D, int BITS, bool QLO, bool PAIR, bool PS>
 hipError_t balanced_slots(long& slots) {
   constexpr int kMaxDevices = 64;
   static std::atomic<long> per_device[kMaxDevices];
@@ -1735,12 +1842,12 @@ hipError_t balanced_slots(long& slots) {
     int cus = 0, per_cu = 0;
     const size_t lds = (size_t)decode_lds<D, BITS, PAIR>();
     static std::atomic<uint64_t> attr_done{0};
-    if ((e = ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO, PAIR>, (int)lds, &attr_done)) !=
+    if ((e = ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO, PAIR, PS>, (int)lds, &attr_done)) !=
         hipSuccess)
       return e;
     if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
     if ((e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-             &per_cu, (const void*)decode_balanced_kernel<D, BITS, QLO, PAIR>, 64 * kHeadsPerGroup, lds)) != hipSuccess)
+             &per_cu, (const void*)decode_balanced_kernel<D, BITS, QLO, PAIR, PS>, 64 * kHeadsPerGroup, lds)) != hipSuccess)
       return e;
     v = (long)(cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
     per_device[dev].store(v, std::memory_order_release);
@@ -1749,11 +1856,15 @@ hipError_t balanced_slots(long& slots) {
   return hipSuccess;
 }
 
-template <int D, bool QLO, bool PAIR>
+template <int D, bool QLO, bool PAIR, bool PS>
 hipError_t decode_slots_d(const DecodeArgs& a, long& slots) {
-  if (a.tier == 8) return balanced_slots<D, 8, QLO, PAIR>(slots);
-  if (a.tier == 2) return balanced_slots<D, 2, QLO, PAIR>(slots);
-  return balanced_slots<D, 4, QLO, PAIR>(slots);
+  if (a.tier == 8) return balanced_slots<D, 8, QLO, PAIR, PS>(slots);
+  if (a.tier == 2) return balanced_slots<D, 2, QLO, PAIR, PS>(slots);
+  return balanced_slots<D, 4, QLO, PAIR, PS>(slots);
+}
+template <int D, bool QLO, bool PAIR>
+hipError_t decode_slots_p(const DecodeArgs& a, long& slots) {
+  return a.ps ? decode_slots_d<D, QLO, PAIR, true>(a, slots) : decode_slots_d<D, QLO, PAIR, false>(a, slots);
 }
 
 hipError_t decode_ranges(const DecodeArgs& a, long& ranges) {
@@ -1761,11 +1872,11 @@ hipError_t decode_ranges(const DecodeArgs& a, long& ranges) {
   long slots = 0;
   hipError_t e;
   if (a.L.D == 128 && a.pair)
-    e = qlo ? decode_slots_d<128, true, true>(a, slots) : decode_slots_d<128, false, true>(a, slots);
+    e = qlo ? decode_slots_p<128, true, true>(a, slots) : decode_slots_p<128, false, true>(a, slots);
   else if (a.L.D == 128)
-    e = qlo ? decode_slots_d<128, true, false>(a, slots) : decode_slots_d<128, false, false>(a, slots);
+    e = qlo ? decode_slots_p<128, true, false>(a, slots) : decode_slots_p<128, false, false>(a, slots);
   else if (a.L.D == 64 && !a.pair)
-    e = qlo ? decode_slots_d<64, true, false>(a, slots) : decode_slots_d<64, false, false>(a, slots);
+    e = qlo ? decode_slots_p<64, true, false>(a, slots) : decode_slots_p<64, false, false>(a, slots);
   else return hipErrorInvalidValue;
   if (e != hipSuccess) return e;
   const long n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
@@ -1776,11 +1887,15 @@ hipError_t decode_ranges(const DecodeArgs& a, long& ranges) {
   return hipSuccess;
 }
 
+template <int D, bool QLO, bool PAIR, bool PS>
+hipError_t launch_decode_t4(const DecodeArgs& a, hipStream_t s) {
+  if (a.tier == 8) return launch_decode_t<D, 8, QLO, PAIR, PS>(a, s);
+  if (a.tier == 2) return launch_decode_t<D, 2, QLO, PAIR, PS>(a, s);
+  return launch_decode_t<D, 4, QLO, PAIR, PS>(a, s);
+}
 template <int D, bool QLO, bool PAIR>
 hipError_t launch_decode_d(const DecodeArgs& a, hipStream_t s) {
-  if (a.tier == 8) return launch_decode_t<D, 8, QLO, PAIR>(a, s);
-  if (a.tier == 2) return launch_decode_t<D, 2, QLO, PAIR>(a, s);
-  return launch_decode_t<D, 4, QLO, PAIR>(a, s);
+  return a.ps ? launch_decode_t4<D, QLO, PAIR, true>(a, s) : launch_decode_t4<D, QLO, PAIR, false>(a, s);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
