@@ -195,8 +195,11 @@ void decode_view(const echokv_layout* L, ek::DecodeArgs& a) {
 // Whether the MFMA decode folds the V scale into the P operand (DecodeArgs::ps): the
 // first pass's query heads times the kernel head's V groups fill at most the 16
 // MFMA columns (every later pass has as many query heads or fewer).
+// 2: two tiles per step (the INT8 kernel), for 4 query heads x 4 V groups at head
+// size 128.
 int decode_ps(const ek::DecodeArgs& a, int gqa) {
   const int G = a.L.D / a.L.VG, gs = gqa < 16 ? gqa : 16;
+  if (G == 4 && gs == 4 && a.L.D == 128 && !a.pair) return 2;
   return G >= 1 && G <= 4 && gs * G <= 16 ? 1 : 0;
 }
 

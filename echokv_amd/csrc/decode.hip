@@ -431,6 +431,16 @@ __device__ __forceinline__ void v_codes(const uint32_t (*vw)[VW], h4_t* va) {
   }
 }
 
+// The lane's V codes of channels j in [P * CPM / 2, (P + 1) * CPM / 2) (half of its
+// channels), as v_codes: va[j - P * CPM / 2].
+template <int BITS, int CPM, int VW, int P>
+__device__ __forceinline__ void v_codes_half(const uint32_t (*vw)[VW], h4_t* va) {
+  h4_t all[CPM];
+  v_codes<BITS, CPM, VW>(vw, all);  // the other half's conversions are dead code
+#pragma unroll
+  for (int j = 0; j < CPM / 2; ++j) va[j] = all[P * CPM / 2 + j];
+}
+
 // Online-softmax update with the tile's unscaled scores x (masked: -inf), then
 // O^T += V^T P^T with V = codes * (s hi + s lo) + min and P = p hi + p lo, and
 // the min term in acc_m (the lane's rows share one V group, so its rows of acc_m
@@ -699,7 +709,7 @@ __device__ __forceinline__ void tile_any(const Wave<D, QLO>& w, const DecodeArgs
 
 // ---------------------------------------------------------------------------
 // Tier-specialised pipelined path. The 4 waves of a workgroup (the 4 KV heads of
-// a head group) stream the split's tiles through one NBUF-slot ring in LDS,
+// a head group) stream the split's tiles through one ring of LDS slots,
 // filled by direct global->LDS DMA (global_load_lds_dword{,x4}: lane L's bytes
 // land at M0 + size * L). A token row holds [K codes of all heads | V codes of
 // all heads], so the group's 4 heads are one contiguous 4 * D * b/8-byte
@@ -776,10 +786,13 @@ struct Ring {
   static constexpr int SLOT = OFF_DUMMY + 16;
   static constexpr int J = 2 * NK + 3;           // DMA jobs per tile
   static constexpr int M = (J + 3) / 4;          // DMA instructions per wave per tile
-  static constexpr int NBUF = BITS == 8 ? 3 : 4;
-  static constexpr int WG_BYTES = NBUF * SLOT;
   static_assert(U >= 4 && U <= 64, "segment units");
 };
+
+// Ring slots of a workgroup: two-tile steps (PSV 2) take a pair of slots per step,
+// with one step in flight while a step computes.
+template <int BITS, int PSV>
+constexpr int ring_slots() { return PSV == 2 ? 4 : (BITS == 8 ? 3 : 4); }
 
 // LDS byte offset (within a slot's side) of 16-byte unit u of token n.
 template <int D, int BITS>
@@ -1049,6 +1062,208 @@ __device__ __forceinline__ void compute_tile(const Wave<D, QLO>& w, const Decode
   vt.st = VStats{s01, s23, m01, m23};
 }
 
+// ---------------------------------------------------------------------------
+// Two tiles per step (PS with 4 query heads x 4 V groups, D 128; the INT8 kernel:
+// at INT2 / INT4 the step's operands need about 200 registers, so those tiers keep
+// one tile per step at three waves per SIMD, which measured faster). Tiles u = 0, 1
+// of a step share its fixed costs (one barrier, one softmax reduction, one
+// exponent per score), and both contractions use all 16 MFMA columns:
+//  S^T: column n = q + 4 (u + 2x) is query q's scores of tile u (x: a copy), so a
+//       lane builds the (q * k_scale) hi / lo operand of one tile's K group only;
+//       each tile's MFMAs fill every column, and a lane keeps its own tile's.
+//  PV:  column n = q + 4g (query q, V group g), as with one tile; K = 32 runs over
+//       the lane's 4 tokens of tile 0, then of tile 1, so one 16x16x32 product per
+//       16 channels and weight part takes both tiles. The other tile's weights come
+//       from the neighbouring group of 4 lanes in the row of 16 (DPP row_ror:4, bank
+//       masked): that group is the same query at the other tile.
+// ---------------------------------------------------------------------------
+constexpr int kRowRor4 = 0x124;  // DPP row_ror:4
+template <int BANKS>
+__device__ __forceinline__ float dpp_ror4(float old, float src) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src), kRowRor4, 0xF, BANKS,
+                                                    false));
+}
+
+// S^T of block j for both tiles: `ks` this lane's own tile's k_scale words (its
+// columns' tile), km0 / km1 each tile's k_min words, kf0 / kf1 each tile's codes.
+template <int D, bool QLO, int BITS>
+__device__ __forceinline__ void s_pair_block(const Wave<D, QLO>& w, const uint32_t* ks, const uint32_t* km0,
+                                             const uint32_t* km1, const h8_t& kf0, const h8_t& kf1, int j, f4_t& s0,
+                                             f4_t& s1) {
+  uint32_t hi[4], lo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const h2_t q = u2h(w.qn[4 * j + i]), sc = u2h(ks[i]);
+    const h2_t ph = q * sc;
+    h2_t pl = __builtin_elementwise_fma(q, sc, -ph);
+    if constexpr (QLO) pl = __builtin_elementwise_fma(u2h(w.ql[4 * j + i]), sc, pl);
+    hi[i] = h2u(ph);
+    lo[i] = h2u(pl);
+  }
+  const h8_t h8 = w2h8(hi[0], hi[1], hi[2], hi[3]), l8 = w2h8(lo[0], lo[1], lo[2], lo[3]);
+  const h8_t qh = w2h8(w.qn[4 * j], w.qn[4 * j + 1], w.qn[4 * j + 2], w.qn[4 * j + 3]);
+  const h8_t m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f,
+                      (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f, (_Float16)-1024.0f};
+  s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf0, h8, s0, 0, 0, 0);
+  s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf1, h8, s1, 0, 0, 0);
+  s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf0, l8, s0, 0, 0, 0);
+  s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf1, l8, s1, 0, 0, 0);
+  if constexpr (BITS == 8) {
+    s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, h8, s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, h8, s1, 0, 0, 0);
+    s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, l8, s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(m1024, l8, s1, 0, 0, 0);
+  } else {
+    (void)m1024;
+  }
+  s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(w2h8(km0[0], km0[1], km0[2], km0[3]), qh, s0, 0, 0, 0);
+  s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(w2h8(km1[0], km1[1], km1[2], km1[3]), qh, s1, 0, 0, 0);
+  if constexpr (QLO) {
+    const h8_t ql = w2h8(w.ql[4 * j], w.ql[4 * j + 1], w.ql[4 * j + 2], w.ql[4 * j + 3]);
+    s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(w2h8(km0[0], km0[1], km0[2], km0[3]), ql, s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(w2h8(km1[0], km1[1], km1[2], km1[3]), ql, s1, 0, 0, 0);
+  }
+}
+
+// One two-tile step from LDS slots sp0 / sp1 (tier BITS, both tiles taken by the
+// pipelined path): n_rel0 / n_rel1 valid tokens in each (16 or fewer). The online
+// softmax state is the one-tile PS state (columns q + 4g), so single tiles and
+// generic-path tiles mix freely with steps. Phases are kept apart (sched
+// barriers) so that each phase's operands alone are live: the K words and S
+// accumulators, then the weights, then the V codes half a head at a time.
+template <int D, bool QLO, int BITS>
+__device__ __forceinline__ void pair_step(Wave<D, QLO>& w, const LaneConst<D, BITS>& k, const uint8_t* sp0,
+                                          const uint8_t* sp1, int n_rel0, int n_rel1, int lane) {
+  using W = Wave<D, QLO>;
+  constexpr int CPL = W::CPL, NQK = W::NQK, CPM = W::CPM;
+  constexpr int kk = ps_shift<BITS>();
+  static_assert(D == 128, "two-tile steps: 4 query heads x 4 V groups of 32 channels");
+  const int c = lane >> 4, n = lane & 15;
+  const bool t1 = (n >> 2) & 1;         // the lane's S^T column belongs to tile 1
+  const uint8_t* spo = t1 ? sp1 : sp0;  // its own tile's slot (per lane)
+
+  // ---- S^T of both tiles ----
+  constexpr int KW = CPL * BITS / 32 > 0 ? CPL * BITS / 32 : 1;
+  uint32_t kw0[KW], kw1[KW];
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int e = 0; e < k_units<D, BITS>(); ++e) {
+      load_bytes<16>(sp0 + k.k_rd[e], kw0 + 4 * e);
+      load_bytes<16>(sp1 + k.k_rd[e], kw1 + 4 * e);
+    }
+  } else {
+    load_bytes<CPL * BITS / 8>(sp0 + k.k_rd[0], kw0);
+    load_bytes<CPL * BITS / 8>(sp1 + k.k_rd[0], kw1);
+  }
+  f4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  const CodeK ck = code_consts<BITS>();
+#pragma unroll
+  for (int j = 0; j < NQK; ++j) {
+    uint32_t ks[4], km0[4], km1[4];
+    load_bytes<16>(spo + k.s_rd + 16 * j, ks);
+    load_bytes<16>(sp0 + k.s_rd + 4 * D * 2 + 16 * j, km0);
+    load_bytes<16>(sp1 + k.s_rd + 4 * D * 2 + 16 * j, km1);
+    s_pair_block<D, QLO, BITS>(w, ks, km0, km1, kfrag_j<BITS>(kw0, j, ck), kfrag_j<BITS>(kw1, j, ck), j, s0, s1);
+  }
+  // The lane's own tile's scores, masked past its valid tokens; selected in
+  // straight-line code right after the MFMAs (their first reader must be one the
+  // compiler sees, so it places the wait states the MFMA results need).
+  const int t = 4 * c;
+  const int nr = t1 ? n_rel1 : n_rel0;
+  float x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[i] = t + i < nr ? (t1 ? s1[i] : s0[i]) : -__builtin_inff();
+    asm volatile("" : "+v"(x[i]));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- weights: online softmax over both tiles' scores of each query ----
+  // V scale / min of the lane's 4 tokens of each tile, its column's V group
+  // (32-byte rows per token; tokens past the sequence: 0, their weights are 0).
+  const _Float16* vs0 = (const _Float16*)(sp0 + k.vs_rd);
+  const _Float16* vs1 = (const _Float16*)(sp1 + k.vs_rd);
+  h2_t sa = {vs0[0], vs0[16]}, sb = {vs0[32], vs0[48]}, sc = {vs1[0], vs1[16]}, sd = {vs1[32], vs1[48]};
+  h2_t ma = {vs0[256], vs0[272]}, mb = {vs0[288], vs0[304]}, mc = {vs1[256], vs1[272]}, md = {vs1[288], vs1[304]};
+  if (n_rel0 < 16 || n_rel1 < 16) {
+    auto keep = [&](int nrel, uint32_t& k01, uint32_t& k23) {
+      k01 = t + 1 < nrel ? ~0u : (t < nrel ? 0xFFFFu : 0u);
+      k23 = t + 3 < nrel ? ~0u : (t + 2 < nrel ? 0xFFFFu : 0u);
+    };
+    uint32_t a01, a23, b01, b23;
+    keep(n_rel0, a01, a23);
+    keep(n_rel1, b01, b23);
+    sa = u2h(h2u(sa) & a01), ma = u2h(h2u(ma) & a01), sb = u2h(h2u(sb) & a23), mb = u2h(h2u(mb) & a23);
+    sc = u2h(h2u(sc) & b01), mc = u2h(h2u(mc) & b01), sd = u2h(h2u(sd) & b23), md = u2h(h2u(md) & b23);
+  }
+  float mt = rows_max(vmax(vmax3(x[0], x[1], x[2]), x[3]));
+  mt = vmax(mt, dpp_ror4<0xF>(mt, mt));
+  mt *= w.scale;
+  const float m_new = vmax(w.m_run, mt);
+  // The largest V scale (fp16 bits; a negative or NaN pattern reads as large).
+  const uint32_t sm0 = __builtin_elementwise_max(h2u(sa) & 0xFFFFu, h2u(sb) & 0xFFFFu);
+  const uint32_t sm1 = __builtin_elementwise_max(h2u(sa) >> 16, h2u(sb) >> 16);
+  const uint32_t sm2 = __builtin_elementwise_max(h2u(sc) & 0xFFFFu, h2u(sd) & 0xFFFFu);
+  const uint32_t sm3 = __builtin_elementwise_max(h2u(sc) >> 16, h2u(sd) >> 16);
+  const uint32_t smax = __builtin_elementwise_max(__builtin_elementwise_max(sm0, sm1), __builtin_elementwise_max(sm2, sm3));
+  const bool big = smax >= ((uint32_t)(15 + 7 - kk) << 10);
+  if (__builtin_amdgcn_ballot_w64(m_new > w.m_run + (big ? 0.f : kLazyRescale))) {
+    const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
+    w.l_lane *= alpha;
+#pragma unroll
+    for (int j = 0; j < CPM; ++j) w.acc[j] *= alpha;
+    w.acc_ml *= alpha;
+    w.m_run = m_new;
+  }
+  const float off = (float)kk - w.m_run;
+  float p[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float own = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], w.scale, off));
+    p[i] = dpp_ror4<0xA>(own, own);      // tile 0: odd groups of 4 lanes take the neighbour's
+    p[4 + i] = dpp_ror4<0x5>(own, own);  // tile 1: even groups take the neighbour's
+  }
+  w.l_lane += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+  const _Float16 sv[8] = {sa[0], sa[1], sb[0], sb[1], sc[0], sc[1], sd[0], sd[1]};
+  const _Float16 mv[8] = {ma[0], ma[1], mb[0], mb[1], mc[0], mc[1], md[0], md[1]};
+  float b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    w.acc_ml = __builtin_fmaf(p[i], (float)mv[i], w.acc_ml);
+    b[i] = __builtin_fmaf((float)sv[i], p[i], 0.f);
+  }
+  h8_t bh, bl;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) bh[i] = (_Float16)b[i];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) bl[i] = (_Float16)__builtin_fmaf((float)bh[i], -1.f, b[i]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- O^T += V^T P^T over both tiles, half a head's channels at a time ----
+  constexpr int VB = CPM * BITS / 8;
+  constexpr int VW = VB >= 4 ? VB / 4 : 1;
+  uint32_t vw0[4][VW], vw1[4][VW];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    load_bytes<VB>(sp0 + k.v_rd[i], vw0[i]);
+    load_bytes<VB>(sp1 + k.v_rd[i], vw1[i]);
+  }
+  auto pv_half = [&](auto part) {
+    constexpr int P = decltype(part)::value;
+    h4_t va0[CPM / 2], va1[CPM / 2];
+    v_codes_half<BITS, CPM, VW, P>(vw0, va0);
+    v_codes_half<BITS, CPM, VW, P>(vw1, va1);
+#pragma unroll
+    for (int j = 0; j < CPM / 2; ++j) {
+      const h8_t av = __builtin_shufflevector(va0[j], va1[j], 0, 1, 2, 3, 4, 5, 6, 7);
+      w.acc[P * CPM / 2 + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bh, w.acc[P * CPM / 2 + j], 0, 0, 0);
+      w.acc[P * CPM / 2 + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bl, w.acc[P * CPM / 2 + j], 0, 0, 0);
+    }
+  };
+  pv_half(std::integral_constant<int, 0>{});
+  pv_half(std::integral_constant<int, 1>{});
+}
+
 // Wait for this wave's part of the tile about to be read: `ahead` tiles were
 // issued after it (wave-uniform, NB - 2 at most), M DMA instructions each, so at
 // most ahead * M of this wave's loads may stay in flight.
@@ -1176,12 +1391,14 @@ __device__ __forceinline__ void range_priority(int left, int total) {
 
 // Blocks [b_start, b_end) of sequence `seq` for the KV heads of head group hg
 // (one wave per head).
-template <int D, int BITS, bool QLO, bool PASSES, bool PAIR, bool PS>
+template <int D, int BITS, bool QLO, bool PASSES, bool PAIR, int PS>
 __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b_start, int b_end, int hg, int wv,
                                             int lane, uint8_t* ring, uint32_t ring0, SpanSink sink,
                                             SpanPass pass = SpanPass{false, true, 0, false}) {
   using W = Wave<D, QLO>;
   using R = Ring<D, BITS>;
+  constexpr int NB = ring_slots<BITS, PS>();
+  static_assert(PS != 2 || (D == 128 && !PAIR), "two-tile steps: D 128, whole heads");
   const Lay& L = a.L;
   const int seq_len = (int)a.lens[seq];
   const long q_row = a.q_rows ? a.q_rows[seq] : seq;
@@ -1199,7 +1416,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
   const int RD = pair ? 2 * D : D;
   const int ha = live ? h : L.H - 1;
   const long rh = pair ? (long)(ha >> 1) * a.res.s2 + (ha & 1) * D : (long)ha * a.res.s2;
-  uint8_t* const xch = ring + R::WG_BYTES;  // the score exchange (pair only)
+  uint8_t* const xch = ring + NB * R::SLOT;  // the score exchange (pair only)
   int xi = 0;
   // Columns: query head qcol of the pass (PS: one per V group, cols = gs * G of them);
   // `mine`: the lane's output rows are real (PS: its rows' V group is its column's).
@@ -1270,7 +1487,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
     carried = true;
   };
 
-  const LaneConst<D, BITS> kc = lane_const<D, BITS, PS>(a, wv, lane);
+  const LaneConst<D, BITS> kc = lane_const<D, BITS, PS != 0>(a, wv, lane);
   const JobLane<D, BITS> jl = job_lane<D, BITS>(a, wv, hg, lane);
   const int tpb_shift = a.bs_shift - 4;  // tiles per block = BS / 16
   const bool stats_ok = (D >> a.vg_shift) == 2 || (D >> a.vg_shift) == 4;
@@ -1339,40 +1556,89 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
       const uint64_t cb1 = BITS >= 4 ? rl64(bl.cb1, b) : 0u;
       const uint64_t cb2 = BITS == 8 ? rl64(bl.cb2, b) : 0u;
       const uint64_t cb3 = BITS == 8 ? rl64(bl.cb3, b) : 0u;
-      const uint32_t slot = ring0 + (uint32_t)((tt % R::NBUF) * R::SLOT);
+      const uint32_t slot = ring0 + (uint32_t)((tt % NB) * R::SLOT);
       issue_tile<D, BITS>(a, jl, slot, piped(tt), t0, lane, wv, pg, cb1, cb2, cb3);
     };
 
-    // Tile tt: wait for this wave's part of it, meet the others (every part has
-    // landed; every wave is done with tile tt - 1), refill tt - 1's slot with
-    // tile tt + NBUF - 1, compute tile tt.
     bool rare = false;
-#pragma unroll 1
-    for (int tt = 0; tt < R::NBUF - 1 && tt < n_tiles; ++tt) issue(tt);
-#pragma unroll 1
-    for (int tt = 0; tt < n_tiles; ++tt) {
-      const int ahead = (n_tiles - 1 - tt) < (R::NBUF - 2) ? (n_tiles - 1 - tt) : (R::NBUF - 2);
-      wait_tile<D, BITS, R::NBUF>(ahead);
-      wg_barrier();
-      if (tt + R::NBUF - 1 < n_tiles) issue(tt + R::NBUF - 1);
+    constexpr int VW = W::CPM * BITS / 8 >= 4 ? W::CPM * BITS / 8 / 4 : 1;
+    // One pipelined tile on its own (the one-tile loop; a step whose other tile
+    // is not taken).
+    auto single = [&](int tt) {
       const int b = tt >> tpb_shift;
-      const int bo = orig(b);
-      if (sink.total > 0 && (tt & 3) == 0) range_priority(b_end - c0 - bo + sink.rem_after, sink.total);
-      if (!((m_blk >> b) & 1)) continue;
-      if (!piped(tt)) {
-        rare = true;
-        continue;
-      }
-      if (!live && !pair) continue;
       const int t0 = (tt & ((1 << tpb_shift) - 1)) << 4;
-      const int n_valid = seq_len - ((c0 + bo) << a.bs_shift);
-      constexpr int VW = W::CPM * BITS / 8 >= 4 ? W::CPM * BITS / 8 / 4 : 1;
+      const int n_valid = seq_len - ((c0 + orig(b)) << a.bs_shift);
       float x[4];
       VTile<VW> vt;
-      compute_tile<D, QLO, BITS>(w, a, kc, ring + (tt % R::NBUF) * R::SLOT, n_valid - t0, lane, x, vt);
+      compute_tile<D, QLO, BITS>(w, a, kc, ring + (tt % NB) * R::SLOT, n_valid - t0, lane, x, vt);
       if (pair) pair_scores(xch, xi, wv, lane, x);
       if constexpr (PS) softmax_pv_ps<D, QLO, BITS, VW>(w, x, vt, kk, kk);
       else softmax_pv<D, QLO, BITS, VW>(w, x, vt, vscale_mask<BITS>());
+    };
+    if constexpr (PS == 2) {
+      // Two tiles per step: step pp is tiles 2pp, 2pp + 1 in slots of the ring's
+      // NB / 2 pairs. Wait for this wave's part of step pp, meet the others (every
+      // part has landed; every wave is done with step pp - 1), refill step pp - 1's
+      // pair with step pp + NB/2 - 1, compute step pp. A tile past the last of the
+      // chunk issues dummies, so every step issues the same number of DMAs.
+      constexpr int NB2 = NB / 2;
+      const int n_pairs = (n_tiles + 1) >> 1;
+      auto issue2 = [&](int pp) {
+        issue(2 * pp);
+        if (2 * pp + 1 < n_tiles) {
+          issue(2 * pp + 1);
+        } else {
+          const uint32_t slot = ring0 + (uint32_t)(((2 * pp + 1) % NB) * R::SLOT);
+          issue_tile<D, BITS>(a, jl, slot, false, 0, lane, wv, rl64(bl.pg, 0), 0u, 0u, 0u);
+        }
+      };
+#pragma unroll 1
+      for (int pp = 0; pp < NB2 - 1 && pp < n_pairs; ++pp) issue2(pp);
+#pragma unroll 1
+      for (int pp = 0; pp < n_pairs; ++pp) {
+        const int ahead = (n_pairs - 1 - pp) < (NB2 - 2) ? (n_pairs - 1 - pp) : (NB2 - 2);
+        wait_ahead<2 * R::M, NB2 - 2>(ahead);
+        wg_barrier();
+        if (pp + NB2 - 1 < n_pairs) issue2(pp + NB2 - 1);
+        const int tt0 = 2 * pp, tt1 = tt0 + 1;
+        const int b0 = tt0 >> tpb_shift, b1 = tt1 >> tpb_shift;
+        if (sink.total > 0 && (pp & 1) == 0) range_priority(b_end - c0 - orig(b0) + sink.rem_after, sink.total);
+        const bool ok0 = (m_blk >> b0) & 1, ok1 = tt1 < n_tiles && ((m_blk >> b1) & 1);
+        const bool p0 = ok0 && piped(tt0), p1 = ok1 && piped(tt1);
+        if ((ok0 && !p0) || (ok1 && !p1)) rare = true;
+        if (!live) continue;
+        if (p0 && p1) {
+          const int nv0 = seq_len - ((c0 + orig(b0)) << a.bs_shift) - ((tt0 & ((1 << tpb_shift) - 1)) << 4);
+          const int nv1 = seq_len - ((c0 + orig(b1)) << a.bs_shift) - ((tt1 & ((1 << tpb_shift) - 1)) << 4);
+          pair_step<D, QLO, BITS>(w, kc, ring + (tt0 % NB) * R::SLOT, ring + (tt1 % NB) * R::SLOT, nv0, nv1, lane);
+        } else {
+          if (p0) single(tt0);
+          if (p1) single(tt1);
+        }
+      }
+    } else {
+      // Tile tt: wait for this wave's part of it, meet the others (every part has
+      // landed; every wave is done with tile tt - 1), refill tt - 1's slot with
+      // tile tt + NB - 1, compute tile tt.
+#pragma unroll 1
+      for (int tt = 0; tt < NB - 1 && tt < n_tiles; ++tt) issue(tt);
+#pragma unroll 1
+      for (int tt = 0; tt < n_tiles; ++tt) {
+        const int ahead = (n_tiles - 1 - tt) < (NB - 2) ? (n_tiles - 1 - tt) : (NB - 2);
+        wait_tile<D, BITS, NB>(ahead);
+        wg_barrier();
+        if (tt + NB - 1 < n_tiles) issue(tt + NB - 1);
+        const int b = tt >> tpb_shift;
+        const int bo = orig(b);
+        if (sink.total > 0 && (tt & 3) == 0) range_priority(b_end - c0 - bo + sink.rem_after, sink.total);
+        if (!((m_blk >> b) & 1)) continue;
+        if (!piped(tt)) {
+          rare = true;
+          continue;
+        }
+        if (!live && !pair) continue;
+        single(tt);
+      }
     }
     wait_vmcnt<0>();  // nothing of this chunk may still be landing in the ring
     wg_barrier();     // every wave is done reading the ring before the next chunk refills it
@@ -1390,7 +1656,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
         const int n_valid = seq_len - ((c0 + orig(b)) << a.bs_shift);
         float x[4];
         VTile<D / 64> vt;  // codes widened to bytes
-        tile_any<D, QLO, PS>(w, a, blk, t0, n_valid, rslot, in_res, ha, rh, lane, tier, x, vt);
+        tile_any<D, QLO, PS != 0>(w, a, blk, t0, n_valid, rslot, in_res, ha, rh, lane, tier, x, vt);
         if (pair) pair_scores(xch, xi, wv, lane, x);
         if constexpr (PS)
           softmax_pv_ps<D, QLO, 8, D / 64>(w, x, vt, kk, ps_shift_of(tier));
@@ -1447,7 +1713,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
 // Three waves per SIMD (<= 168 VGPRs) where the ring leaves LDS for three
 // workgroups per CU; INT8's larger ring and the float32-query variant get two.
 // PAIR: head size 256 as half-heads (DecodeArgs::pair), D = 128.
-template <int D, int BITS, bool QLO, bool PAIR, bool PS>
+template <int D, int BITS, bool QLO, bool PAIR, int PS>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
   SpanPass pass{false, true, 0, false};
@@ -1542,7 +1808,7 @@ __device__ __forceinline__ void seq_of_block(const DecodeArgs& a, long x, int la
   first = base;
 }
 
-template <int D, int BITS, bool QLO, bool PAIR, bool PS>
+template <int D, int BITS, bool QLO, bool PAIR, int PS>
 __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) void decode_balanced_kernel(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t ring_lds[];
   const int lane = threadIdx.x & 63;
@@ -1803,13 +2069,13 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
 
 // Dynamic LDS of a decode workgroup: the ring, and with PAIR the score exchange
 // (every tier's ring leaves room for it at the workgroups per CU the launch bounds give).
-template <int D, int BITS, bool PAIR>
-constexpr int decode_lds() { return Ring<D, BITS>::WG_BYTES + (PAIR ? kPairLds : 0); }
+template <int D, int BITS, bool PAIR, int PS>
+constexpr int decode_lds() { return ring_slots<BITS, PS>() * Ring<D, BITS>::SLOT + (PAIR ? kPairLds : 0); }
 
-template <int D, int BITS, bool QLO, bool PAIR, bool PS>
+template <int D, int BITS, bool QLO, bool PAIR, int PS>
 hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
   const dim3 block(64 * kHeadsPerGroup);
-  constexpr int lds = decode_lds<D, BITS, PAIR>();
+  constexpr int lds = decode_lds<D, BITS, PAIR, PS>();
   const long n_hg = (a.L.H + kHeadsPerGroup - 1) / kHeadsPerGroup;
   const long span = 8 * n_hg;  // the kernels permute workgroups within runs of `span`
   if (a.ranges > 0) {
@@ -1829,7 +2095,7 @@ hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t s) {
 }
 
 // Workgroups of the balanced kernel the current device holds at once (cached per device).
-template <int D, int BITS, bool QLO, bool PAIR, bool PS>
+template <int D, int BITS, bool QLO, bool PAIR, int PS>
 hipError_t balanced_slots(long& slots) {
   constexpr int kMaxDevices = 64;
   static std::atomic<long> per_device[kMaxDevices];
@@ -1840,7 +2106,7 @@ hipError_t balanced_slots(long& slots) {
   long v = per_device[dev].load(std::memory_order_acquire);
   if (v <= 0) {
     int cus = 0, per_cu = 0;
-    const size_t lds = (size_t)decode_lds<D, BITS, PAIR>();
+    const size_t lds = (size_t)decode_lds<D, BITS, PAIR, PS>();
     static std::atomic<uint64_t> attr_done{0};
     if ((e = ensure_lds_limit((const void*)decode_balanced_kernel<D, BITS, QLO, PAIR, PS>, (int)lds, &attr_done)) !=
         hipSuccess)
@@ -1856,15 +2122,18 @@ hipError_t balanced_slots(long& slots) {
   return hipSuccess;
 }
 
-template <int D, bool QLO, bool PAIR, bool PS>
+template <int D, bool QLO, bool PAIR, int PS>
 hipError_t decode_slots_d(const DecodeArgs& a, long& slots) {
   if (a.tier == 8) return balanced_slots<D, 8, QLO, PAIR, PS>(slots);
-  if (a.tier == 2) return balanced_slots<D, 2, QLO, PAIR, PS>(slots);
-  return balanced_slots<D, 4, QLO, PAIR, PS>(slots);
+  constexpr int PS1 = PS == 2 ? 1 : PS;  // as launch_decode_t4
+  if (a.tier == 2) return balanced_slots<D, 2, QLO, PAIR, PS1>(slots);
+  return balanced_slots<D, 4, QLO, PAIR, PS1>(slots);
 }
 template <int D, bool QLO, bool PAIR>
 hipError_t decode_slots_p(const DecodeArgs& a, long& slots) {
-  return a.ps ? decode_slots_d<D, QLO, PAIR, true>(a, slots) : decode_slots_d<D, QLO, PAIR, false>(a, slots);
+  if constexpr (D == 128 && !PAIR)
+    if (a.ps == 2) return decode_slots_d<D, QLO, PAIR, 2>(a, slots);
+  return a.ps ? decode_slots_d<D, QLO, PAIR, 1>(a, slots) : decode_slots_d<D, QLO, PAIR, 0>(a, slots);
 }
 
 hipError_t decode_ranges(const DecodeArgs& a, long& ranges) {
@@ -1887,15 +2156,21 @@ hipError_t decode_ranges(const DecodeArgs& a, long& ranges) {
   return hipSuccess;
 }
 
-template <int D, bool QLO, bool PAIR, bool PS>
+// Two-tile steps (PS 2) run the INT8 kernel only: at INT2 / INT4 the step's
+// operands do not fit the 168 registers that three waves per SIMD leave, and with
+// two waves per SIMD those tiers decode slower than one tile at a time with three.
+template <int D, bool QLO, bool PAIR, int PS>
 hipError_t launch_decode_t4(const DecodeArgs& a, hipStream_t s) {
   if (a.tier == 8) return launch_decode_t<D, 8, QLO, PAIR, PS>(a, s);
-  if (a.tier == 2) return launch_decode_t<D, 2, QLO, PAIR, PS>(a, s);
-  return launch_decode_t<D, 4, QLO, PAIR, PS>(a, s);
+  constexpr int PS1 = PS == 2 ? 1 : PS;
+  if (a.tier == 2) return launch_decode_t<D, 2, QLO, PAIR, PS1>(a, s);
+  return launch_decode_t<D, 4, QLO, PAIR, PS1>(a, s);
 }
 template <int D, bool QLO, bool PAIR>
 hipError_t launch_decode_d(const DecodeArgs& a, hipStream_t s) {
-  return a.ps ? launch_decode_t4<D, QLO, PAIR, true>(a, s) : launch_decode_t4<D, QLO, PAIR, false>(a, s);
+  if constexpr (D == 128 && !PAIR)
+    if (a.ps == 2) return launch_decode_t4<D, QLO, PAIR, 2>(a, s);
+  return a.ps ? launch_decode_t4<D, QLO, PAIR, 1>(a, s) : launch_decode_t4<D, QLO, PAIR, 0>(a, s);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, long num_seqs, hipStream_t s) {
