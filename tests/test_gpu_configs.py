@@ -70,11 +70,11 @@ def slots_of(table, lens, pos_fn, bs):
 
 
 def build_layer(device, lens, bits, *, h=8, d=128, bs=16, kg=16, vg=32, mem_bits=8, dtype=torch.float16, seed=1,
-                outliers=0.01, v_outliers=0.0, pages=None, table=None):
+                outliers=0.01, v_outliers=0.0, pages=None, table=None, v_mult=1.0):
     """A layer store written through the product path: each sequence's first
     len - 1 tokens in one step, then its last token in a second (decode) step.
     ``outliers`` / ``v_outliers``: the share of (head, channel) pairs of K / V
-    scaled x10."""
+    scaled x10; ``v_mult``: every V value's factor."""
     rng = np.random.default_rng(seed)
     lens = np.asarray(lens, np.int64)
     if table is None:
@@ -92,7 +92,7 @@ def build_layer(device, lens, bits, *, h=8, d=128, bs=16, kg=16, vg=32, mem_bits
     def kv(n):
         k = torch.randn(n, h, d, generator=gen, device=device)
         k.view(n, h * d)[:, out_ch] *= 10
-        v = torch.randn(n, h, d, generator=gen, device=device)
+        v = torch.randn(n, h, d, generator=gen, device=device) * v_mult
         v.view(n, h * d)[:, v_ch] *= 10
         return k.to(dtype), v.to(dtype)
 
@@ -167,6 +167,32 @@ def test_cfg2_with_k_and_v_outliers(device, bits, span):
     dec.decode_attention(store, q, table_d, lens_d, 128 ** -0.5, tier=bits, out=out16)
     raw = float(np.abs(out16.float().cpu().numpy() - ref).max())
     check(f"cfg2 v-outliers {span} int{bits} fp16 out (raw max-abs {raw:.3e})", out16, ref)
+
+
+@pytest.mark.parametrize("bits", [8, 4, 2])
+@pytest.mark.parametrize("gqa", [4, 7])
+def test_large_v_values_stay_finite_and_accurate(device, bits, gqa):
+    """V values in the thousands (V scales far above typical): where the kernel
+    folds the V scale into the P operand (GQA 4 here), a tile with such scales
+    rescales its weights exactly, so the operand w * s stays inside fp16; GQA 7
+    takes the per-element V path. Every case is within the north-star bar scaled
+    by the values' factor (the same relative accuracy as unit-scale data)."""
+    rng = np.random.default_rng(31)
+    lens = np.concatenate([rng.integers(1, 40, 12), rng.integers(500, 3000, 4)])
+    mult = 3000.0
+    store, table = build_layer(device, lens, bits, h=4, seed=31, v_mult=mult)
+    ps = oracle_view(store)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    lens_d = torch.from_numpy(lens).to(device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(32)
+    q = (torch.randn(len(lens), 4 * gqa, 128, device=device, generator=gen) * 2).half()
+    ref = OA.decode_attention(ps, q.float().cpu().numpy(), table, lens, 128 ** -0.5, vectorized=True)
+    print(f"[large V int{bits} gqa{gqa}] max |out| {np.abs(ref).max():.1f}", flush=True)
+    for inv in (False, True):
+        got = dec.decode_attention(store, q, table_d, lens_d, 128 ** -0.5, tier=bits, batch_invariant=inv)
+        assert torch.isfinite(got).all(), "non-finite output"
+        check(f"large V int{bits} gqa{gqa}" + (" split schedule" if inv else ""), got, ref, tol=TOL * mult)
 
 
 @pytest.mark.parametrize("bits", [8, 2])
