@@ -842,6 +842,9 @@ def main():
     ap.add_argument("--prefill-only", action="store_true", help="only the config-3 prefill measurement")
     ap.add_argument("--config4", action="store_true",
                     help="only config 4 (70B shape, 80 layers, about 102 GB of pages): decode per tier and the canary")
+    ap.add_argument("--config5", action="store_true",
+                    help="only config 5's stand-in (bench_e2e.py with its defaults): a random-init Llama-3.1-8B-shaped "
+                         "model served through the backend at ECHOKV_MEM_BITS=4 against a dense 16-bit KV loop")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 1 GiB device-to-device 5 times (the reference kernel for FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
@@ -856,6 +859,11 @@ def main():
         return
     if args.config4:
         print(json.dumps({"cfg4": run_cfg4()}), flush=True)
+        return
+    if args.config5:
+        import bench_e2e
+
+        print(json.dumps({"cfg5": bench_e2e.run_cfg5(bench_e2e.parser().parse_args([]))}), flush=True)
         return
     print(json.dumps(run(args)), flush=True)
 

@@ -488,7 +488,7 @@ def run_system(which: str, args) -> dict:
     return res
 
 
-def main():
+def parser() -> argparse.ArgumentParser:
     ap = argparse.ArgumentParser()
     ap.add_argument("--system", choices=("both", "echokv", "dense"), default="both")
     ap.add_argument("--prompts", type=int, default=256)
@@ -502,7 +502,12 @@ def main():
     ap.add_argument("--no-layer-times", dest="layer_times", action="store_false")
     ap.add_argument("--graphs", action="store_true",
                     help="replay decode steps from HIP graphs (not run on the GPU yet: see the module docstring)")
-    args = ap.parse_args()
+    return ap
+
+
+def run_cfg5(args) -> dict:
+    """Both systems (or the one ``args.system`` names) on the cfg5 workload; the
+    result dict that ``main`` prints (``bench.py --config5`` runs it with the defaults)."""
     os.environ.setdefault("ECHOKV_MEM_BITS", "4")
     out = {"workload": f"cfg5 stand-in: {args.prompts} x ({args.input_len} in, {args.output_len} out), greedy, "
                        f"{args.kv_gib:g} GiB KV, block {args.block_size}, random-init bf16 Llama-3.1-8B shape, "
@@ -513,7 +518,11 @@ def main():
     if "echokv" in out and "dense" in out:
         out["speedup_output_tok_s"] = round(out["echokv"]["output_tok_s"] / out["dense"]["output_tok_s"], 3)
         out["capacity_ratio"] = round(out["echokv"]["kv_capacity_tokens"] / out["dense"]["kv_capacity_tokens"], 3)
-    print(json.dumps(out), flush=True)
+    return out
+
+
+def main():
+    print(json.dumps(run_cfg5(parser().parse_args())), flush=True)
 
 
 if __name__ == "__main__":
