@@ -1538,7 +1538,7 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
     // A tile takes the pipelined path when its block is stored at the kernel's
     // tier with every chunk in range and it is not the block's open K group;
     // the others (rare: demoted / downgraded blocks, each sequence's open
-    // group) are computed after the chunk's pipelined tiles, from global memory.
+    // group) are computed on the generic path from global memory (generic_tiles).
     // Per-block bit masks (one bit per lane = block) keep the per-tile test scalar.
     const uint64_t m_fast = stats_ok ? __builtin_amdgcn_ballot_w64(lane < n_take && bl.fast_rg != kNotFast) : 0ull;
     const uint64_t m_open = __builtin_amdgcn_ballot_w64(bl.fast_rg >= 0);
@@ -1560,7 +1560,6 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
       issue_tile<D, BITS>(a, jl, slot, piped(tt), t0, lane, wv, pg, cb1, cb2, cb3);
     };
 
-    bool rare = false;
     constexpr int VW = W::CPM * BITS / 8 >= 4 ? W::CPM * BITS / 8 / 4 : 1;
     // One pipelined tile on its own (the one-tile loop; a step whose other tile
     // is not taken).
@@ -1575,74 +1574,15 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
       if constexpr (PS) softmax_pv_ps<D, QLO, BITS, VW>(w, x, vt, kk, kk);
       else softmax_pv<D, QLO, BITS, VW>(w, x, vt, vscale_mask<BITS>());
     };
-    if constexpr (PS == 2) {
-      // Two tiles per step: step pp is tiles 2pp, 2pp + 1 in slots of the ring's
-      // NB / 2 pairs. Wait for this wave's part of step pp, meet the others (every
-      // part has landed; every wave is done with step pp - 1), refill step pp - 1's
-      // pair with step pp + NB/2 - 1, compute step pp. A tile past the last of the
-      // chunk issues dummies, so every step issues the same number of DMAs.
-      constexpr int NB2 = NB / 2;
-      const int n_pairs = (n_tiles + 1) >> 1;
-      auto issue2 = [&](int pp) {
-        issue(2 * pp);
-        if (2 * pp + 1 < n_tiles) {
-          issue(2 * pp + 1);
-        } else {
-          const uint32_t slot = ring0 + (uint32_t)(((2 * pp + 1) % NB) * R::SLOT);
-          issue_tile<D, BITS>(a, jl, slot, false, 0, lane, wv, rl64(bl.pg, 0), 0u, 0u, 0u);
-        }
-      };
-#pragma unroll 1
-      for (int pp = 0; pp < NB2 - 1 && pp < n_pairs; ++pp) issue2(pp);
-#pragma unroll 1
-      for (int pp = 0; pp < n_pairs; ++pp) {
-        const int ahead = (n_pairs - 1 - pp) < (NB2 - 2) ? (n_pairs - 1 - pp) : (NB2 - 2);
-        wait_ahead<2 * R::M, NB2 - 2>(ahead);
-        wg_barrier();
-        if (pp + NB2 - 1 < n_pairs) issue2(pp + NB2 - 1);
-        const int tt0 = 2 * pp, tt1 = tt0 + 1;
-        const int b0 = tt0 >> tpb_shift, b1 = tt1 >> tpb_shift;
-        if (sink.total > 0 && (pp & 1) == 0) range_priority(b_end - c0 - orig(b0) + sink.rem_after, sink.total);
-        const bool ok0 = (m_blk >> b0) & 1, ok1 = tt1 < n_tiles && ((m_blk >> b1) & 1);
-        const bool p0 = ok0 && piped(tt0), p1 = ok1 && piped(tt1);
-        if ((ok0 && !p0) || (ok1 && !p1)) rare = true;
-        if (!live) continue;
-        if (p0 && p1) {
-          const int nv0 = seq_len - ((c0 + orig(b0)) << a.bs_shift) - ((tt0 & ((1 << tpb_shift) - 1)) << 4);
-          const int nv1 = seq_len - ((c0 + orig(b1)) << a.bs_shift) - ((tt1 & ((1 << tpb_shift) - 1)) << 4);
-          pair_step<D, QLO, BITS>(w, kc, ring + (tt0 % NB) * R::SLOT, ring + (tt1 % NB) * R::SLOT, nv0, nv1, lane);
-        } else {
-          if (p0) single(tt0);
-          if (p1) single(tt1);
-        }
-      }
-    } else {
-      // Tile tt: wait for this wave's part of it, meet the others (every part has
-      // landed; every wave is done with tile tt - 1), refill tt - 1's slot with
-      // tile tt + NB - 1, compute tile tt.
-#pragma unroll 1
-      for (int tt = 0; tt < NB - 1 && tt < n_tiles; ++tt) issue(tt);
-#pragma unroll 1
-      for (int tt = 0; tt < n_tiles; ++tt) {
-        const int ahead = (n_tiles - 1 - tt) < (NB - 2) ? (n_tiles - 1 - tt) : (NB - 2);
-        wait_tile<D, BITS, NB>(ahead);
-        wg_barrier();
-        if (tt + NB - 1 < n_tiles) issue(tt + NB - 1);
-        const int b = tt >> tpb_shift;
-        const int bo = orig(b);
-        if (sink.total > 0 && (tt & 3) == 0) range_priority(b_end - c0 - bo + sink.rem_after, sink.total);
-        if (!((m_blk >> b) & 1)) continue;
-        if (!piped(tt)) {
-          rare = true;
-          continue;
-        }
-        if (!live && !pair) continue;
-        single(tt);
-      }
-    }
-    wait_vmcnt<0>();  // nothing of this chunk may still be landing in the ring
-    wg_barrier();     // every wave is done reading the ring before the next chunk refills it
-    if (rare && (live || pair)) {
+    // The chunk's tiles the pipeline does not take (each sequence's open K group,
+    // blocks at another tier), on the generic register path. They run right after
+    // the pipeline's first DMAs are issued: their loads retire behind those DMAs,
+    // so their memory latency overlaps the pipeline's fill instead of adding to the
+    // span's end (the workgroups holding an open group are the kernel's last).
+    const uint64_t m_valid = (!PASSES ? m_blk : (n_take >= 64 ? ~0ull : (1ull << n_take) - 1)) &
+                             (nb >= 64 ? ~0ull : (1ull << nb) - 1);
+    auto generic_tiles = [&]() {
+      if (!(live || pair) || ((m_valid & ~m_fast) == 0 && (m_valid & m_open) == 0)) return;
 #pragma unroll 1
       for (int tt = 0; tt < n_tiles; ++tt) {
         const int b = tt >> tpb_shift;
@@ -1664,7 +1604,72 @@ __device__ __forceinline__ void decode_span(const DecodeArgs& a, long seq, int b
           softmax_pv<D, QLO, 8, D / 64>(w, x, vt,
                                         tier == 8 ? vscale_mask<8>() : (tier == 4 ? vscale_mask<4>() : vscale_mask<2>()));
       }
+    };
+    if constexpr (PS == 2) {
+      // Two tiles per step: step pp is tiles 2pp, 2pp + 1 in slots of the ring's
+      // NB / 2 pairs. Wait for this wave's part of step pp, meet the others (every
+      // part has landed; every wave is done with step pp - 1), refill step pp - 1's
+      // pair with step pp + NB/2 - 1, compute step pp. A tile past the last of the
+      // chunk issues dummies, so every step issues the same number of DMAs.
+      constexpr int NB2 = NB / 2;
+      const int n_pairs = (n_tiles + 1) >> 1;
+      auto issue2 = [&](int pp) {
+        issue(2 * pp);
+        if (2 * pp + 1 < n_tiles) {
+          issue(2 * pp + 1);
+        } else {
+          const uint32_t slot = ring0 + (uint32_t)(((2 * pp + 1) % NB) * R::SLOT);
+          issue_tile<D, BITS>(a, jl, slot, false, 0, lane, wv, rl64(bl.pg, 0), 0u, 0u, 0u);
+        }
+      };
+#pragma unroll 1
+      for (int pp = 0; pp < NB2 - 1 && pp < n_pairs; ++pp) issue2(pp);
+      generic_tiles();
+#pragma unroll 1
+      for (int pp = 0; pp < n_pairs; ++pp) {
+        const int ahead = (n_pairs - 1 - pp) < (NB2 - 2) ? (n_pairs - 1 - pp) : (NB2 - 2);
+        wait_ahead<2 * R::M, NB2 - 2>(ahead);
+        wg_barrier();
+        if (pp + NB2 - 1 < n_pairs) issue2(pp + NB2 - 1);
+        const int tt0 = 2 * pp, tt1 = tt0 + 1;
+        const int b0 = tt0 >> tpb_shift, b1 = tt1 >> tpb_shift;
+        if (sink.total > 0 && (pp & 1) == 0) range_priority(b_end - c0 - orig(b0) + sink.rem_after, sink.total);
+        const bool ok0 = (m_blk >> b0) & 1, ok1 = tt1 < n_tiles && ((m_blk >> b1) & 1);
+        const bool p0 = ok0 && piped(tt0), p1 = ok1 && piped(tt1);
+        if (!live) continue;
+        if (p0 && p1) {
+          const int nv0 = seq_len - ((c0 + orig(b0)) << a.bs_shift) - ((tt0 & ((1 << tpb_shift) - 1)) << 4);
+          const int nv1 = seq_len - ((c0 + orig(b1)) << a.bs_shift) - ((tt1 & ((1 << tpb_shift) - 1)) << 4);
+          pair_step<D, QLO, BITS>(w, kc, ring + (tt0 % NB) * R::SLOT, ring + (tt1 % NB) * R::SLOT, nv0, nv1, lane);
+        } else {
+          if (p0) single(tt0);
+          if (p1) single(tt1);
+        }
+      }
+    } else {
+      // Tile tt: wait for this wave's part of it, meet the others (every part has
+      // landed; every wave is done with tile tt - 1), refill tt - 1's slot with
+      // tile tt + NB - 1, compute tile tt.
+#pragma unroll 1
+      for (int tt = 0; tt < NB - 1 && tt < n_tiles; ++tt) issue(tt);
+      generic_tiles();
+#pragma unroll 1
+      for (int tt = 0; tt < n_tiles; ++tt) {
+        const int ahead = (n_tiles - 1 - tt) < (NB - 2) ? (n_tiles - 1 - tt) : (NB - 2);
+        wait_tile<D, BITS, NB>(ahead);
+        wg_barrier();
+        if (tt + NB - 1 < n_tiles) issue(tt + NB - 1);
+        const int b = tt >> tpb_shift;
+        const int bo = orig(b);
+        if (sink.total > 0 && (tt & 3) == 0) range_priority(b_end - c0 - bo + sink.rem_after, sink.total);
+        if (!((m_blk >> b) & 1)) continue;
+        if (!piped(tt)) continue;  // computed by generic_tiles
+        if (!live && !pair) continue;
+        single(tt);
+      }
     }
+    wait_vmcnt<0>();  // nothing of this chunk may still be landing in the ring
+    wg_barrier();     // every wave is done reading the ring before the next chunk refills it
   }
 
   if (!carried) return;  // no block of this pass's tier: the row keeps the earlier passes' result
