@@ -23,7 +23,7 @@ raises are those of ``echokv_vllm/config.py:40-99``:
 
 This build's own: ECHOKV_OWN_GROUP_EXACT=1 (prefill sees each query's own K
 group at full precision) and ECHOKV_BATCH_INVARIANT=0 (the balanced decode
-schedule); ECHOKV_V_GROUP must be a power of 2 from 4 to 256.
+schedule); ECHOKV_V_GROUP is 1 to 256 channels.
 
 Read elsewhere: ECHOKV_CUDAGRAPH=0 keeps attention out of full graphs (the
 backend), ECHOKV_CHECK_HOST_SLOTS=1 checks the host slot mapping every step. The
@@ -80,9 +80,9 @@ def _is_pow2(x: int) -> bool:
 
 
 def v_group_supported(v_group: int, head_size: int | None = None) -> bool:
-    """V groups the kernels store and read: powers of two from 4 to 256 channels
-    (dividing the head size, when one is given)."""
-    return _is_pow2(v_group) and 4 <= v_group <= 256 and (head_size is None or head_size % v_group == 0)
+    """V groups the kernels store and read: 1 to 256 channels, dividing the head
+    size when one is given (the reference's rule, ``backend.py:100-102``)."""
+    return 1 <= v_group <= 256 and (head_size is None or head_size % v_group == 0)
 
 
 class Setting(NamedTuple):
@@ -108,11 +108,11 @@ SETTINGS: tuple[Setting, ...] = (
     Setting("ECHOKV_ALPHA", "alpha", float, lambda s: 0.1),
     Setting("ECHOKV_K_GROUP", "k_group", int, lambda s: 32,
             lambda v, s: None if v >= 16 and _is_pow2(v) else f"ECHOKV_K_GROUP must be a power of 2 and >= 16, got {v}"),
-    # The reference takes any V group dividing the head size; the kernels reduce a V
-    # group across lanes in power-of-two segments of 4-channel quads.
+    # Any V group that divides the head size, as the reference (checked against the
+    # head size in supports_head_size and TieredLayout).
     Setting("ECHOKV_V_GROUP", "v_group", int, lambda s: 32,
             lambda v, s: None if v_group_supported(v) else
-            f"ECHOKV_V_GROUP must be a power of 2 from 4 to 256 (this build's kernels), got {v}"),
+            f"ECHOKV_V_GROUP must be 1 to 256 channels, got {v}"),
     Setting("ECHOKV_RESIDUAL_SLOTS", "residual_slots", int, lambda s: None),
     Setting("ECHOKV_CANARY_INTERVAL", "canary_interval", int, lambda s: 64,
             lambda v, s: None if v >= 1 else "ECHOKV_CANARY_INTERVAL must be >= 1"),

@@ -8,8 +8,8 @@ namespace {
 bool lay_ok(const echokv_layout* L) {
   if (!L) return false;
   const int H = L->num_kv_heads, D = L->head_size, BS = L->block_size, KG = L->k_group, VG = L->v_group;
-  if (H <= 0 || D <= 0 || BS <= 0 || KG <= 0 || VG < 4 || L->chunks_per_page <= 0 || L->num_blocks <= 0) return false;
-  if (D % 4 || D % VG || BS % 16 || BS % KG || (VG & (VG - 1)) || VG > 256) return false;
+  if (H <= 0 || D <= 0 || BS <= 0 || KG <= 0 || VG <= 0 || L->chunks_per_page <= 0 || L->num_blocks <= 0) return false;
+  if (D % 4 || D % VG || BS % 16 || BS % KG || VG > 256) return false;
   if (L->page_stride % 16 || L->chunk_bytes != (int64_t)BS * H * D / 2) return false;
   return true;
 }

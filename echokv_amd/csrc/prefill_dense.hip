@@ -132,7 +132,7 @@ __device__ __forceinline__ void dequant_key(const PackArgs& a, long blk, int off
   vc.load(a.pages + rb + (long)L.H * D * BITS / 8 + hb);
   const int G = D / L.VG;
   const long pg = blk * L.stride;
-  if (L.VG >= CPT) {  // the thread's channels share one (scale, min)
+  if (L.VG % CPT == 0) {  // the thread's channels share one (scale, min)
     const long ve = ((long)off * L.H + h) * G + c0 / L.VG;
     const float vs = (float)*f16p(a.pages, pg + L.o_vs + 2 * ve);
     const float vm = (float)*f16p(a.pages, pg + L.o_vm + 2 * ve);

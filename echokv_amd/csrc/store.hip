@@ -2,13 +2,74 @@
 //
 // One workgroup of 256 threads per token row / K group / block; a thread owns
 // four consecutive channels of one KV head, so a V group of VG channels is a
-// segment of VG/4 lanes reduced with cross-lane shuffles, and every thread
-// stores its four packed codes (1, 2 or 4 bytes) next to its neighbours'
-// (coalesced). Numerics follow echokv_vllm/quant.py bit for bit: float32
-// extremes, fp16-rounded stats, IEEE division, round half to even.
+// segment of VG/4 lanes reduced with cross-lane shuffles (any other V group is
+// scanned per group, store_v4), and every thread stores its four packed codes
+// (1, 2 or 4 bytes) next to its neighbours' (coalesced). Numerics follow
+// echokv_vllm/quant.py bit for bit: float32 extremes, fp16-rounded stats, IEEE
+// division, round half to even.
 #include "args.h"
 
 namespace ek {
+
+// V groups of 4 * 2^j channels are lane segments (seg_minmax); any other divisor
+// of D (24, 12, 6, 3, 2, 1 channels at D 96, ...) is not. The same for every
+// thread of a launch.
+__device__ __forceinline__ bool v_segments(const Lay& L) {
+  const int w = L.VG / 4;
+  return L.VG % 4 == 0 && (w & (w - 1)) == 0;
+}
+
+// One token's V (head h, channels 4c..4c+3, values x) at `bits`: the group stats
+// (written by the thread holding a group's first channel) and the packed codes at
+// byte `vrow` (the token row's V side). With lane segments, (mn, mx) are the
+// thread's group extremes already (seg_minmax over the wave); otherwise each
+// channel's group is scanned from the source row, val(ch) = the row's channel ch,
+// so a thread's channels may sit in up to four groups.
+// quant.py:26-45 (quantize over groups of VG along the head dimension).
+template <typename Val>
+__device__ __forceinline__ void store_v4(const Lay& L, uint8_t* pages, long blk, long vrow, int off, int h, int c,
+                                         const float x[4], int bits, float mn, float mx, Val val) {
+  const int G = L.D / L.VG;
+  const long sb = blk * L.stride;
+  uint32_t q[4];
+  if (v_segments(L)) {
+    _Float16 s16, m16;
+    float s, m;
+    group_stats(mn, mx, bits, s16, m16, s, m);
+    if ((4 * c) % L.VG == 0) {
+      const long e = ((long)off * L.H + h) * G + (4 * c) / L.VG;
+      *f16p(pages, sb + L.o_vs + 2 * e) = s16;
+      *f16p(pages, sb + L.o_vm + 2 * e) = m16;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = quant_code(x[e], m, s, bits);
+  } else {
+    int gp = -1;
+    float s = 1.f, m = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ch = 4 * c + e, g = ch / L.VG;
+      if (g != gp) {  // a group starts here or at e == 0
+        float gmn = val(g * L.VG), gmx = gmn;
+        for (int j = g * L.VG + 1; j < (g + 1) * L.VG; ++j) {
+          const float y = val(j);
+          gmn = fminf(gmn, y);
+          gmx = fmaxf(gmx, y);
+        }
+        _Float16 s16, m16;
+        group_stats(gmn, gmx, bits, s16, m16, s, m);
+        if (ch % L.VG == 0) {
+          const long ve = ((long)off * L.H + h) * G + g;
+          *f16p(pages, sb + L.o_vs + 2 * ve) = s16;
+          *f16p(pages, sb + L.o_vm + 2 * ve) = m16;
+        }
+        gp = g;
+      }
+      q[e] = quant_code(x[e], m, s, bits);
+    }
+  }
+  store_codes4(pages + vrow + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
+}
 
 
 // ---------------------------------------------------------------------------
@@ -42,7 +103,6 @@ __device__ __forceinline__ void write_token_row(const WriteTokArgs& a, long t, R
   const int off = (int)(slot % L.BS);
   if (blk >= L.nb) return;
   const Hdr hd = load_hdr(a.pages, L, blk);
-  const int G = L.D / L.VG;
   bool rh = true;
   for (int base = 0; base < items; base += kThreads) {
     const int i = base + (int)threadIdx.x;
@@ -68,21 +128,12 @@ __device__ __forceinline__ void write_token_row(const WriteTokArgs& a, long t, R
     const int side = L.H * L.D * bits / 8;
     float mn = fminf(fminf(x[0], x[1]), fminf(x[2], x[3]));
     float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    seg_minmax(mn, mx, L.VG / 4);  // all lanes take part: segments never straddle `act`
+    // All lanes take part (uniform branch): segments never straddle `act`.
+    if (v_segments(L)) seg_minmax(mn, mx, L.VG / 4);
     if (!act || rb < 0) continue;
-    _Float16 s16, m16;
-    float s, m;
-    group_stats(mn, mx, bits, s16, m16, s, m);
-    const int g = (4 * c) / L.VG;
-    if ((4 * c) % L.VG == 0) {
-      const long e = ((long)off * L.H + h) * G + g;
-      *f16p(a.pages, blk * L.stride + L.o_vs + 2 * e) = s16;
-      *f16p(a.pages, blk * L.stride + L.o_vm + 2 * e) = m16;
-    }
-    uint32_t q[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) q[e] = quant_code(x[e], m, s, bits);
-    store_codes4(a.pages + rb + side + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
+    const long vsrc = t * a.v_s0 + h * a.v_s1;
+    store_v4(L, a.pages, blk, rb + side, off, h, c, x, bits, mn, mx,
+             [&](int ch) { return ld(a.value, a.kv_dtype, vsrc + ch); });
 
     // K: residual (open group), codes under the sealed stats, K_ref ring.
     if (rh && rslot >= 0 && rslot < a.res.rows)
@@ -747,7 +798,6 @@ __global__ __launch_bounds__(kThreads) void store_blocks_kernel(StoreBlkArgs a) 
       quantize_k_group(L, a.pages, blk, grp, grp * L.KG, L.KG, bits, h, c, fetch);
     }
   }
-  const int G = L.D / L.VG;
   const int side = L.H * L.D * bits / 8;
   const int items = L.H * quads;
   for (int off = 0; off < L.BS; ++off) {
@@ -764,20 +814,10 @@ __global__ __launch_bounds__(kThreads) void store_blocks_kernel(StoreBlkArgs a) 
       }
       float mn = fminf(fminf(x[0], x[1]), fminf(x[2], x[3]));
       float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-      seg_minmax(mn, mx, L.VG / 4);
+      if (v_segments(L)) seg_minmax(mn, mx, L.VG / 4);  // uniform branch
       if (!act || rb < 0) continue;
-      _Float16 s16, m16;
-      float s, m;
-      group_stats(mn, mx, bits, s16, m16, s, m);
-      if ((4 * c) % L.VG == 0) {
-        const long e = ((long)off * L.H + h) * G + (4 * c) / L.VG;
-        *f16p(a.pages, blk * L.stride + L.o_vs + 2 * e) = s16;
-        *f16p(a.pages, blk * L.stride + L.o_vm + 2 * e) = m16;
-      }
-      uint32_t q[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) q[e] = quant_code(x[e], m, s, bits);
-      store_codes4(a.pages + rb + side + (long)h * (L.D * bits / 8) + c * (bits / 2), pack4(q, bits), bits);
+      const float* vrow = vb + (long)off * rowsz + h * L.D;
+      store_v4(L, a.pages, blk, rb + side, off, h, c, x, bits, mn, mx, [&](int ch) { return vrow[ch]; });
     }
   }
 }
@@ -799,11 +839,14 @@ __device__ __forceinline__ void dequant_token4(const Lay& L, const uint8_t* page
   }
   const long hb = (long)h * (L.D * bits / 8) + c * (bits / 2);
   const uint32_t vc = load_codes4(pages + rb + L.H * L.D * bits / 8 + hb, bits);
-  const long ve = ((long)off * L.H + h) * G + (4 * c) / L.VG;
-  const float vs = (float)*f16p(pages, blk * L.stride + L.o_vs + 2 * ve);
-  const float vm = (float)*f16p(pages, blk * L.stride + L.o_vm + 2 * ve);
+  const long ve = ((long)off * L.H + h) * G;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = code_at(vc, e, bits) * vs + vm;
+  for (int e = 0; e < 4; ++e) {  // channel 4c + e's V group (one for every e unless VG is not a lane segment)
+    const long vg = ve + (v_segments(L) ? 4 * c : 4 * c + e) / L.VG;
+    const float vs = (float)*f16p(pages, blk * L.stride + L.o_vs + 2 * vg);
+    const float vm = (float)*f16p(pages, blk * L.stride + L.o_vm + 2 * vg);
+    v[e] = code_at(vc, e, bits) * vs + vm;
+  }
   const long rs = block_res[blk];
   const int grp = off / L.KG;
   if (rs >= 0 && rs < res.rows && res_group[rs] == grp) {

@@ -288,18 +288,20 @@ def test_reference_module_path_is_this_package():
 
 # ---- V groups ----------------------------------------------------------------------------
 
-def test_v_groups_the_kernels_do_not_store_are_refused_up_front(monkeypatch):
-    for vg in ("4", "16", "64", "128"):
+def test_any_v_group_dividing_the_head_size_is_taken(monkeypatch):
+    """The reference's rule (``backend.py:100-102``): the head size must divide by
+    the V group (and by 4); any such V group is stored, powers of two or not."""
+    for vg, ok96 in (("4", True), ("16", True), ("24", True), ("6", True), ("3", True), ("1", True),
+                     ("64", False), ("20", False)):
         monkeypatch.setenv("ECHOKV_V_GROUP", vg)
         assert load_config().v_group == int(vg)
-    monkeypatch.setenv("ECHOKV_V_GROUP", "32")
-    assert EchoKVAttentionBackend.supports_head_size(96)
-    for vg in ("24", "6", "2", "512"):
+        assert EchoKVAttentionBackend.supports_head_size(96) is ok96
+    monkeypatch.setenv("ECHOKV_V_GROUP", "20")
+    assert EchoKVAttentionBackend.supports_head_size(80)
+    for vg in ("0", "512"):
         monkeypatch.setenv("ECHOKV_V_GROUP", vg)
         with pytest.raises(ValueError, match="ECHOKV_V_GROUP"):
             load_config()
-        with pytest.raises(ValueError, match="ECHOKV_V_GROUP"):
-            EchoKVAttentionBackend.supports_head_size(96)
 
 
 def test_batch_invariant_is_the_default_and_can_be_turned_off(monkeypatch):

@@ -405,12 +405,14 @@ def test_v_group_and_head_size_variants(device, d, vg, bits, h):
 
 @pytest.mark.parametrize("d,bs,kg,vg,h,gqa", [(96, 16, 16, 32, 4, 4), (256, 16, 16, 32, 4, 4), (256, 32, 32, 256, 2, 4),
                                                (128, 16, 8, 32, 4, 4), (128, 48, 16, 32, 4, 4), (128, 16, 16, 4, 4, 4),
-                                               (80, 32, 32, 16, 4, 2), (96, 16, 16, 32, 2, 20)])
+                                               (80, 32, 32, 16, 4, 2), (96, 16, 16, 32, 2, 20), (96, 16, 16, 24, 4, 4),
+                                               (96, 32, 32, 3, 2, 7), (80, 16, 16, 20, 2, 4)])
 @pytest.mark.parametrize("bits", [8, 4, 2])
 def test_layouts_outside_the_mfma_kernels(device, d, bs, kg, vg, h, gqa, bits):
-    """Head sizes other than 64 / 128 / 256 (up to 256), head size 256 with one V
-    group per head, K groups under 16, block sizes that are not powers of two and V
-    groups under D/16 take the fp32 decode kernel (the reference's PyTorch path
+    """Head sizes other than 64 / 128 / 256 (up to 256) with V groups of any size
+    (24, 3, 20 channels), head size 256 with one V group per head, K groups under
+    16, block sizes that are not powers of two and V groups under D/16 take the fp32
+    decode kernel (the reference's PyTorch path
     serves them there), GQA 20 in two passes of query heads; prefill attends
     through decode rows (head size 256 included). Both equal the oracle."""
     lens = np.array([1, 17, 300, 64, 1000])

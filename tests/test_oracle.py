@@ -62,6 +62,28 @@ def test_quantize_invariants(bits):
     assert np.all(sc.astype(np.float32) >= 2.0 ** -14)
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_quantize_groups_of_any_size_are_consecutive_channel_runs(bits):
+    """V groups that are not powers of two (the reference takes any divisor of the
+    head size): group j of size g is channels [j*g, (j+1)*g), each quantized as a
+    row of its own -- a transposed grouping (channels j, j + D/g, ...) fails this.
+    Group 32 is pinned to the reference's bytes above."""
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal((8, 96), dtype=np.float32) * 2
+    x[:, 5] += 9.0  # an outlier channel that moves one group's stats only
+    for g in (96, 24, 12, 6, 3, 1):
+        c, sc, mn = OQ.quantize(x, bits, g)
+        assert sc.shape == (8, 96 // g)
+        for j in range(96 // g):
+            cj, scj, mnj = OQ.quantize(x[:, j * g : (j + 1) * g], bits, g)
+            assert np.array_equal(c[:, j * g : (j + 1) * g], cj)
+            assert np.array_equal(sc[:, j : j + 1].view(np.uint16), scj.view(np.uint16))
+            assert np.array_equal(mn[:, j : j + 1].view(np.uint16), mnj.view(np.uint16))
+        y = OQ.dequantize(c, sc, mn, g)
+        assert np.all(np.abs(y - x) <= 0.5 * np.repeat(sc.astype(np.float32), g, axis=-1)
+                      + np.repeat(np.abs(mn.astype(np.float32) - x.reshape(8, -1, g).min(-1)), g, axis=-1) + 1e-6)
+
+
 def test_fake_quant_channels_keeps_partial_tail_exact():
     rng = np.random.default_rng(12)
     k = rng.standard_normal((40, 2, 16), dtype=np.float32)
