@@ -24,7 +24,7 @@ from oracle import store as OS
 
 pytestmark = pytest.mark.gpu
 
-H, HQ, D, BS, KG, LAYERS = 8, 32, 128, 16, 16, 3
+H, HQ, D, BS, KG, VG, LAYERS = 8, 32, 128, 16, 16, 32, 3
 PROMPTS = [40, 150, 17, 300]
 TOL = 2e-3
 
@@ -48,7 +48,7 @@ def env(monkeypatch, request):
 
 
 def make_engine(device, tiers):
-    per_token = TieredLayout.per_token_bytes(H, D, 8, KG, 32)
+    per_token = TieredLayout.per_token_bytes(H, D, 8, KG, VG)
     num_blocks = 128
     pool = torch.zeros(num_blocks, LAYERS, BS, per_token, dtype=torch.uint8, device=device)
     layers = []
@@ -165,7 +165,8 @@ def test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, env):
     slots = slots_for(table_np, [0] * nreq, PROMPTS)
     md = builder.build(0, Batch(device, table, starts, PROMPTS, slots, int(starts[-1])))
     assert md.prefill is not None and md.decode is None
-    assert (md.prefill.dense is not None) == (D != 256)  # head size 256: the fused kernel at every length
+    # head size 256: the fused MFMA kernel at every length; 96: the fp32 kernel
+    assert (md.prefill.dense is not None) == (D in (64, 128))
     q, k, v = rand(int(starts[-1]), HQ), rand(int(starts[-1]), H), rand(int(starts[-1]), H)
     outs = run_layers(layers, md, q, k, v)
     torch.cuda.synchronize()
@@ -299,6 +300,27 @@ def test_serving_sequence_at_head_size_256(device, monkeypatch):
                  "ECHOKV_KREF_WINDOW": "32", "ECHOKV_RESIDUAL_SLOTS": "24", "ECHOKV_OWN_GROUP_EXACT": "0"}.items():
         monkeypatch.setenv(k, v)
     monkeypatch.setattr(sys.modules[__name__], "D", 256)
+    try:
+        test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, False)
+    finally:
+        _vllm.set_forward_metadata(None)
+
+
+def test_serving_sequence_at_head_size_96_v_group_24(device, monkeypatch):
+    """The same serving sequence at head size 96 with ECHOKV_V_GROUP=24 (a V group
+    that is not a power of two, which the reference takes: it divides the head
+    size): the backend selects it, the store writes it, and decode (eager and graph
+    replayed, tier passes), prefill and the canary run on the fp32 kernels; against
+    the oracle."""
+    from echokv_amd.backend import EchoKVAttentionBackend
+
+    for k, v in {"ECHOKV_K_GROUP": "16", "ECHOKV_MEM_BITS": "8", "ECHOKV_CANARY_INTERVAL": "2",
+                 "ECHOKV_KREF_WINDOW": "32", "ECHOKV_RESIDUAL_SLOTS": "24", "ECHOKV_OWN_GROUP_EXACT": "0",
+                 "ECHOKV_V_GROUP": "24"}.items():
+        monkeypatch.setenv(k, v)
+    assert EchoKVAttentionBackend.supports_head_size(96)
+    monkeypatch.setattr(sys.modules[__name__], "D", 96)
+    monkeypatch.setattr(sys.modules[__name__], "VG", 24)
     try:
         test_prefill_decode_and_graph_replayed_steps_match_the_oracle(device, False)
     finally:
