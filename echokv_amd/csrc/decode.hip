@@ -1784,10 +1784,18 @@ __device__ __forceinline__ long wave_total(long x) {
   return x;
 }
 
-// Total blocks of the batch (every lane gets it).
-__device__ __forceinline__ long batch_blocks(const DecodeArgs& a, int lane) {
+// The balanced partition weighs each live sequence as its blocks plus kSeqCost:
+// a range that starts a sequence pays a span start-up (block facts, the ring's
+// fill, the open K group's tile), about kSeqCost tiles of streaming, so ranges
+// holding sequence boundaries get fewer blocks and end with the others. (cfg2
+// INT4 layer-step: 6 -> 97.2 us, 0 -> 100.5 us; 4, 8, 10 and 12 measured no better.)
+constexpr int kSeqCost = 6;
+__device__ __forceinline__ int seq_cost(int nb) { return nb > 0 ? nb + kSeqCost : 0; }
+
+// Total cost of the batch (every lane gets it).
+__device__ __forceinline__ long batch_cost(const DecodeArgs& a, int lane) {
   long t = 0;
-  for (long s0 = 0; s0 < a.num_seqs; s0 += 64) t += wave_total(seq_blocks(a, s0 + lane));
+  for (long s0 = 0; s0 < a.num_seqs; s0 += 64) t += wave_total(seq_cost(seq_blocks(a, s0 + lane)));
   return t;
 }
 
@@ -1806,23 +1814,48 @@ __device__ __forceinline__ long div_floor(long n, long d) {
 // First block of range r (of `ranges` over T blocks).
 __device__ __forceinline__ long range_begin(long r, long ranges, long T) { return div_floor(r * T, ranges); }
 
-// The sequence holding global block x, and that sequence's first global block.
-__device__ __forceinline__ void seq_of_block(const DecodeArgs& a, long x, int lane, long& seq, long& first) {
-  long base = 0;
+// Range r's blocks [lo, hi) under the cost partition, and the sequence holding
+// block lo with its first block: one walk over the lengths (64 sequences per step)
+// places both ends.
+__device__ __forceinline__ void range_blocks(const DecodeArgs& a, long r, int lane, long& seq, long& first, long& lo,
+                                             long& hi) {
+  const long CT = uni(batch_cost(a, lane));
+  const long c0 = range_begin(r, a.ranges, CT), c1 = range_begin(r + 1, a.ranges, CT);
+  long base_c = 0, base_b = 0;
+  bool found = false;
+  seq = a.num_seqs;
   for (long s0 = 0; s0 < a.num_seqs; s0 += 64) {
     const int nb = seq_blocks(a, s0 + lane);
-    const int incl = wave_incl_scan(nb, lane);
-    const int tot = __builtin_amdgcn_readlane(incl, 63);
-    if (x < base + tot) {
-      const int k = __builtin_popcountll(__builtin_amdgcn_ballot_w64(base + incl <= x));  // lanes ending at or before x
-      seq = s0 + k;
-      first = base + __builtin_amdgcn_readlane(incl, k) - __builtin_amdgcn_readlane(nb, k);
+    const int cost = seq_cost(nb);
+    const int incl_c = wave_incl_scan(cost, lane), incl_b = wave_incl_scan(nb, lane);
+    const int tot_c = __builtin_amdgcn_readlane(incl_c, 63);
+    // The block at cost c in this step's sequences: lanes whose costs end at or
+    // before c come before it.
+    auto at = [&](long c, long& sq, long& f) -> long {
+      const int k = __builtin_popcountll(__builtin_amdgcn_ballot_w64(base_c + incl_c <= c));
+      sq = s0 + k;
+      const long cum = base_c + __builtin_amdgcn_readlane(incl_c, k) - __builtin_amdgcn_readlane(cost, k);
+      f = base_b + __builtin_amdgcn_readlane(incl_b, k) - __builtin_amdgcn_readlane(nb, k);
+      const long off = c - cum - kSeqCost;
+      return f + (off > 0 ? off : 0);
+    };
+    if (!found && c0 < base_c + tot_c) {
+      lo = at(c0, seq, first);
+      found = true;
+    }
+    if (c1 < base_c + tot_c) {
+      long s2, f2;
+      hi = at(c1, s2, f2);
       return;
     }
-    base += tot;
+    base_c += tot_c;
+    base_b += __builtin_amdgcn_readlane(incl_b, 63);
   }
-  seq = a.num_seqs;
-  first = base;
+  if (!found) {
+    lo = base_b;
+    first = base_b;
+  }
+  hi = base_b;
 }
 
 template <int D, int BITS, bool QLO, bool PAIR, int PS>
@@ -1839,11 +1872,11 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
   const long r = item / n_hg;
   const int hg = (int)(item % n_hg);
   if (r >= a.ranges) return;
-  const long T = uni(batch_blocks(a, lane));
-  const long lo = range_begin(r, a.ranges, T), hi = range_begin(r + 1, a.ranges, T);
+  long seq, first, lo, hi;
+  range_blocks(a, r, lane, seq, first, lo, hi);
+  lo = uni(lo);
+  hi = uni(hi);
   if (lo >= hi) return;
-  long seq, first;
-  seq_of_block(a, lo, lane, seq, first);
   seq = uni(seq);
   first = uni(first);
   for (long pos = lo; pos < hi && seq < a.num_seqs;) {
@@ -1879,19 +1912,32 @@ __global__ __launch_bounds__(256) void merge_balanced_kernel(DecodeArgs a) {
   if (head % a.gqa < a.g0 || head % a.gqa >= a.g0 + a.gs) return;  // another pass's query heads
   const int nb = seq_blocks(a, seq);
   if (nb == 0) return;
-  long first = 0;
-  for (long s0 = 0; s0 < seq; s0 += 64) first += wave_total(s0 + lane < seq ? seq_blocks(a, s0 + lane) : 0);
-  first = uni(first);
-  const long T = uni(batch_blocks(a, lane));
+  long cum = 0, CT;  // the sequence's first cost coordinate (its blocks start kSeqCost later); the batch's
+  if (a.num_seqs <= 64) {  // one load of the lengths for both
+    const int cl = seq_cost(seq_blocks(a, lane));
+    cum = wave_total(lane < seq ? cl : 0);
+    CT = wave_total(cl);
+  } else {
+    for (long s0 = 0; s0 < seq; s0 += 64) cum += wave_total(s0 + lane < seq ? seq_cost(seq_blocks(a, s0 + lane)) : 0);
+    CT = batch_cost(a, lane);
+  }
+  cum = uni(cum);
+  CT = uni(CT);
   const long R = a.ranges;
-  auto range_of = [&](long x) {  // the range holding block x: floor(x R / T), then past empty ends
-    long q = div_floor(x * R, T);
-    while (range_begin(q + 1, R, T) <= x) ++q;
+  // The range holding the block at cost c: range q covers costs [range_begin(q),
+  // range_begin(q + 1)), and each block has a cost of its own. floor(c R / CT) is
+  // that range or the one before it (range_begin rounds down: range q + 1 may start
+  // at c itself), and empty ranges past it start at c too.
+  auto range_of = [&](long c) {
+    long q = div_floor(c * R, CT);
+    while (range_begin(q + 1, R, CT) <= c) ++q;
     return q;
   };
-  const long rf = range_of(first), rl = range_of(first + nb - 1);
+  const long rf = range_of(cum + kSeqCost), rl = range_of(cum + kSeqCost + nb - 1);
   if (rf == rl) return;  // written directly by the decode kernel
-  const bool rf_second = first > range_begin(rf, R, T);
+  // The sequence is range rf's second span when the range starts at an earlier
+  // sequence's cost (which maps to that sequence's blocks).
+  const bool rf_second = range_begin(rf, R, CT) < cum;
   auto slot_of = [&](long q) { return 2 * q + (q == rf && rf_second ? 1 : 0); };
   const long n = rl - rf + 1;
   if (n <= 16) {
@@ -1900,7 +1946,7 @@ __global__ __launch_bounds__(256) void merge_balanced_kernel(DecodeArgs a) {
     // weights are applied once the pairs are in.
     const int pi = lane & 15;
     const long qi = rf + pi;
-    const bool mine = lane < 16 && pi < n && range_begin(qi, R, T) < range_begin(qi + 1, R, T);
+    const bool mine = lane < 16 && pi < n && range_begin(qi, R, CT) < range_begin(qi + 1, R, CT);
     float mq = -__builtin_inff(), lq = 0.f;
     if (mine) {
       const long pr = slot_of(qi) * a.hq + head;
@@ -1943,7 +1989,7 @@ __global__ __launch_bounds__(256) void merge_balanced_kernel(DecodeArgs a) {
   float m = -__builtin_inff();
   for (long g = 0; g < n; g += 64) {
     const long q = rf + g + lane;
-    if (q <= rl && range_begin(q, R, T) < range_begin(q + 1, R, T)) m = fmaxf(m, a.ml[(slot_of(q) * a.hq + head) * 2]);
+    if (q <= rl && range_begin(q, R, CT) < range_begin(q + 1, R, CT)) m = fmaxf(m, a.ml[(slot_of(q) * a.hq + head) * 2]);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
@@ -1952,7 +1998,7 @@ __global__ __launch_bounds__(256) void merge_balanced_kernel(DecodeArgs a) {
   for (long g = 0; g < n; g += 64) {
     const long q = rf + g + lane;
     float w = 0.f;
-    if (q <= rl && range_begin(q, R, T) < range_begin(q + 1, R, T)) {
+    if (q <= rl && range_begin(q, R, CT) < range_begin(q + 1, R, CT)) {
       const long pr = slot_of(q) * a.hq + head;
       w = __builtin_amdgcn_exp2f(a.ml[pr * 2] - m);
       den += a.ml[pr * 2 + 1] * w;
