@@ -1756,10 +1756,11 @@ __global__ __launch_bounds__(64 * kHeadsPerGroup, (BITS == 8 || QLO) ? 2 : 3) vo
 
 // ---------------------------------------------------------------------------
 // Balanced schedule. The batch's blocks, sequence after sequence, are cut into
-// `ranges` contiguous ranges of equal block count, range r = [r T / R, (r+1) T / R)
-// (T blocks in all): one persistent workgroup per range and head group, as many
-// as the chip holds at once, so every workgroup streams the same number of
-// bytes and none waits for a late one. A sequence that lies inside one range
+// `ranges` contiguous ranges of equal cost (a live sequence costs its blocks plus
+// kSeqCost for its span start-up; range r covers costs [r C / R, (r+1) C / R) of
+// C in all): one persistent workgroup per range and head group, as many as the
+// chip holds at once, so every workgroup streams about the same work and none
+// waits for a late one. A sequence that lies inside one range
 // is written straight to its output row; the pieces of a longer one (each
 // range's first and last span) go to partial slots 2r and 2r + 1 and a merge
 // kernel combines them. Ranges depend on the whole batch, so results are not
