@@ -138,23 +138,29 @@ class DecodeWork:
     host_tier_masks: np.ndarray | None = None  # [layers] the same, on the host
 
     def run(self, impl, query: torch.Tensor, block_table: torch.Tensor, out: torch.Tensor) -> None:
-        # On the split schedule each tier the layer holds runs on its own fast path:
-        # under graph capture through the device mask (read when the kernels run, so
-        # a replayed graph follows the layer's tiers); eagerly, a layer holding one
-        # tier runs that tier's kernel alone.
-        tier, mask = impl.decode_tier(), None
-        if self.batch_invariant and self.tier_masks is not None:
+        # Each tier the layer holds runs on its own fast path (tier passes, on the
+        # split schedule): under graph capture through the device mask (read when the
+        # kernels run, so a replayed graph follows the layer's tiers); eagerly, a layer
+        # holding one tier runs that tier's kernel alone, and one holding several
+        # takes the tier passes on either schedule (the balanced kernel has none: its
+        # other tiers' blocks would take the generic path, about 2.6x slower a block).
+        tier, mask, inv, ws = impl.decode_tier(), None, self.batch_invariant, self.workspace
+        if self.tier_masks is not None:
             if _capturing(query):
-                mask = self.tier_masks[impl.group_index, :1]
+                if inv:
+                    mask = self.tier_masks[impl.group_index, :1]
             else:
                 held = int(self.host_tier_masks[impl.group_index])
                 if held & (held - 1):
                     mask = self.tier_masks[impl.group_index, :1]
+                    if not inv:
+                        inv = True
+                        ws = impl.split_workspace(ws, self.lens.shape[0], self.num_splits)
                 elif held:
                     tier = held
         dec.decode_attention(impl.store, query, block_table, self.lens, impl.scale, q_rows=self.rows,
-                             bt_rows=self.reqs, out=out, num_splits=self.num_splits, workspace=self.workspace,
-                             tier=tier, batch_invariant=self.batch_invariant, tier_mask=mask)
+                             bt_rows=self.reqs, out=out, num_splits=self.num_splits, workspace=ws,
+                             tier=tier, batch_invariant=inv, tier_mask=mask)
 
 
 @dataclass
@@ -478,6 +484,12 @@ class EchoKVAttentionImpl(AttentionImpl):
         full = dec.workspace_rows(store, self.num_heads, self.stash.dtype, max(cap, n_dec), num_splits, flags)
         acc, ml = self._workspace(full, store.device)  # sized for the graph capacity on first use
         return (acc, ml) if acc.shape[0] >= rows else None
+
+    def split_workspace(self, ws: tuple | None, n_dec: int, num_splits: int) -> tuple | None:
+        """``ws`` if it holds the rows a split-schedule decode of ``n_dec`` entries needs,
+        else None (the call allocates its own: eager steps only)."""
+        rows = dec.workspace_rows(self.store, self.num_heads, self.stash.dtype, n_dec, num_splits, 1)
+        return ws if ws is not None and ws[0].shape[0] >= rows else None
 
     def decode_tier(self) -> int:
         """The tier whose specialised decode kernel runs: the layer's current tier."""

@@ -292,6 +292,66 @@ def test_a_request_decodes_the_same_alone_and_in_a_batch(device, monkeypatch):
     _vllm.set_forward_metadata(None)
 
 
+def test_balanced_schedule_takes_tier_passes_for_mixed_layers_in_eager_steps(device, monkeypatch):
+    """ECHOKV_BATCH_INVARIANT=0 (the balanced schedule): once a layer holds blocks of
+    two tiers (its controller moved, and a request opened a block at the new tier), an
+    eager step decodes that layer with the split schedule's tier passes, each tier on
+    its own kernel, and a layer holding one tier on that tier's balanced kernel;
+    against the oracle."""
+    from echokv_amd.kernels import decode as dec_mod
+
+    for k, v in {"ECHOKV_K_GROUP": "16", "ECHOKV_MEM_BITS": "8", "ECHOKV_RESIDUAL_SLOTS": "24",
+                 "ECHOKV_CANARY_INTERVAL": "1000", "ECHOKV_BATCH_INVARIANT": "0"}.items():
+        monkeypatch.setenv(k, v)
+    calls = []
+    real = dec_mod.decode_attention
+
+    def spy(*args, **kw):
+        calls.append((kw.get("batch_invariant"), kw.get("tier_mask") is not None, kw.get("tier")))
+        return real(*args, **kw)
+
+    monkeypatch.setattr(dec_mod, "decode_attention", spy)
+    rng = np.random.default_rng(21)
+    builder, layers, _ = make_engine(device, tiers=[4, 8, 2])
+    nreq = len(PROMPTS)
+    table_np = rng.permutation(128)[: nreq * 32].reshape(nreq, 32).astype(np.int64)
+    table = torch.from_numpy(table_np).to(device, torch.int32)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(22)
+
+    def rand(n, heads):
+        return [torch.randn(n, heads, D, device=device, generator=gen).half() for _ in range(LAYERS)]
+
+    starts = np.concatenate([[0], np.cumsum(PROMPTS)])
+    md = builder.build(0, Batch(device, table, starts, PROMPTS, slots_for(table_np, [0] * nreq, PROMPTS),
+                                int(starts[-1])))
+    run_layers(layers, md, rand(int(starts[-1]), HQ), rand(int(starts[-1]), H), rand(int(starts[-1]), H))
+    for layer, bits in zip(layers, (8, 2, 4)):  # blocks opened from now on take the new tier
+        layer.impl.controller.bits = bits
+    lens = list(PROMPTS)
+    mixed_seen = False
+    for step in range(6):  # request 3 (300 tokens) opens block 19 at its 5th step
+        slots = slots_for(table_np, lens, [1] * nreq)
+        lens = [x + 1 for x in lens]
+        md = builder.build(0, Batch(device, table, np.arange(nreq + 1), lens, slots, nreq))
+        assert md.decode is not None and not md.decode.batch_invariant
+        calls.clear()
+        q = rand(nreq, HQ)
+        outs = run_layers(layers, md, q, rand(nreq, H), rand(nreq, H))
+        torch.cuda.synchronize()
+        held = [int(md.decode.host_tier_masks[l.impl.group_index]) for l in layers]
+        assert len(calls) == LAYERS
+        for (inv, has_mask, tier), h in zip(calls, held):
+            if h & (h - 1):
+                assert inv and has_mask, f"step {step}: a layer holding tiers {h} took {calls}"
+                mixed_seen = True
+            else:
+                assert not inv and not has_mask and tier == h, f"step {step}: held {h}, call {(inv, has_mask, tier)}"
+        check_decode(layers, table_np, lens, q, outs, f"balanced eager decode {step}, held {held}")
+    assert mixed_seen, "a layer came to hold two tiers during the eager steps"
+    _vllm.set_forward_metadata(None)
+
+
 def test_serving_sequence_at_head_size_256(device, monkeypatch):
     """The same serving sequence at head size 256: decode on the MFMA kernels as
     half-heads (tier passes under graph replay included), prefill on the fused MFMA
