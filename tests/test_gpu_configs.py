@@ -305,6 +305,37 @@ def test_cfg4_gqa8_long_context_split_paths(device):
     assert -(-nblk // 4) > 64 and -(-nblk // -(-nblk // 200)) > 64
 
 
+@pytest.mark.parametrize("bits", [8, 4, 2])
+def test_balanced_cost_ranges_at_every_boundary_position(device, bits):
+    """The balanced schedule's ranges of equal cost (a live sequence costs its blocks
+    plus its start-up) against the merge, which finds each piece's range from the
+    same cost coordinate: lengths of 1 to 300 tokens around block boundaries, padding
+    rows of length 0 among them, and range counts from a few (each range holding many
+    sequences) to more than the batch's cost (most ranges empty). Every live row
+    against the oracle; padding rows are left as they were."""
+    lens_live = np.array([1, 15, 16, 17, 31, 32, 33, 47, 64, 65, 100, 129, 200, 255, 256, 257, 300, 2, 3, 48])
+    store, table = build_layer(device, lens_live, bits, seed=41, v_outliers=0.01)
+    ps = oracle_view(store)
+    lens = lens_live.copy()
+    lens[[3, 9, 15]] = 0  # padding rows
+    live = lens > 0
+    gen = torch.Generator(device=device)
+    gen.manual_seed(42)
+    q = torch.randn(len(lens), 32, 128, device=device, generator=gen).half()
+    scale = 128 ** -0.5
+    ref = OA.decode_attention(ps, q[torch.from_numpy(live).to(device)].float().cpu().numpy(), table[live],
+                              lens[live], scale, vectorized=True)
+    table_d = torch.from_numpy(table).to(device, torch.int32)
+    lens_d = torch.from_numpy(lens).to(device)
+    for ns in (1, 2, 8, 64):  # ranges are capped at S * splits / 2
+        out = torch.full((len(lens), 32, 128), 7.0, device=device)
+        dec.decode_attention(store, q, table_d, lens_d, scale, tier=bits, batch_invariant=False, num_splits=ns,
+                             out=out)
+        torch.cuda.synchronize()
+        check(f"balanced int{bits}, splits {ns}", out[torch.from_numpy(live).to(device)], ref)
+        assert bool((out[torch.from_numpy(~live).to(device)] == 7.0).all()), "padding rows were written"
+
+
 def test_cfg4_batch_at_int4_balanced(device):
     """cfg4's decode batch at one tier: 16 sequences of 32,768 tokens, GQA 8, INT4,
     the balanced schedule (the benchmark's) and the split one, against the
